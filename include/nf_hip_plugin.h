@@ -1,0 +1,132 @@
+/*
+ * nf_hip_plugin.h — exported C entry points of libnf_plugin_hip.so, the
+ * MI355X (gfx950) execution provider for NeuralOS's quantized linear path.
+ *
+ * The provider is a drop-in for the reference's plugins/metal (and the
+ * plugins/cuda slot): an engine that links or dlopen()s this library and
+ * calls nf_plugin_register / nf_plugin_register_mem gets the same op names,
+ * argument conventions and error codes.  Everything else in the library has
+ * hidden visibility.
+ *
+ * Ops served by dispatch() (op name -> inputs -> outputs):
+ *   dequant_q4_0 / dequant_q8_0             W(quant) -> f32[count]
+ *   dequant_q4_0_f16 / dequant_q8_0_f16     W(quant) -> f16[count]
+ *       count = output size_bytes / element size (metal_provider.mm:2654-2684)
+ *   dequant_q4_0_linear / dequant_q4_0_linear_f16
+ *   dequant_q8_0_linear / dequant_q8_0_linear_f16   (Q8_0: new, additive)
+ *       A[M,K], W[N,K] quant -> C[M,N]; path chosen by the OUTPUT dtype:
+ *       F16 output => f16 activations, weights rounded to f16, fp32 accumulate,
+ *       f16 result; otherwise f32 in/out with exact f32 weights
+ *       (metal_provider.mm:1396-1468, 2990-3031).
+ *   linear / linear_tiled                   A[M,K], B[N,K] dense -> C[M,N]
+ *       (metal_provider.mm:2544-2613; f16 A with f32 C is computed correctly)
+ * M, N, K come from the push constants of the enclosing nf_task_desc
+ * (bytes 20, 24, 28), recovered through the offsetof bridge
+ * (metal_provider.mm:2301-2307).
+ */
+#ifndef NF_HIP_PLUGIN_H
+#define NF_HIP_PLUGIN_H
+
+#include <stdbool.h>
+#include "nf_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* 48-byte push-constant block carried in nf_task_desc.push_constants.
+ * Layout of metal_provider.mm:70-83 / llama_dag_builder.hpp:105-111. */
+typedef struct nf_push_constants {
+    uint32_t seq_len;
+    uint32_t n_heads;
+    uint32_t head_dim;
+    float epsilon;
+    float theta;
+    uint32_t M; /* byte 20 */
+    uint32_t N; /* byte 24 */
+    uint32_t K; /* byte 28 */
+    uint32_t step_idx;
+    uint32_t max_seq_len;
+    uint32_t window_size;
+    uint32_t _pad1;
+} nf_push_constants;
+
+/* ---- plugin entry points -------------------------------------------- */
+
+/* Fill the provider vtable and return the provider handle (a process-wide
+ * singleton).  Replaces metal_provider.mm:3266-3281 (and the plugins/cuda
+ * slot, cuda_provider.cpp:188-202); contract neuro_fabric_abi.h:233-254. */
+NF_API nf_status nf_plugin_register(nf_provider_vtable *vt, nf_provider *out);
+
+/* Fill the memory vtable (alloc / import_buffer / can_import).  One-argument
+ * form of metal_provider.mm:3283-3289; contract neuro_buffer_abi.h:262-271.
+ * Callers that declare it with a second argument (nf_generate.cpp:62) are
+ * harmless under the SysV calling convention. */
+NF_API nf_status nf_plugin_register_mem(nf_provider_mem_vtable *mem_vt);
+
+/* Optional async DDI (dispatch_async / wait / poll / query_caps).
+ * Contract neuro_ddi.h:51-84; the Metal plugin does not export it. */
+NF_API nf_status nf_plugin_register_ddi(nf_ddi_vtable *ddi_vt);
+
+/* ---- per-dispatch GPU timing ring ------------------------------------ */
+/* Same signatures and ring semantics (1024 entries, oldest overwritten) as
+ * metal_provider.mm:2149-2189, measured with HIP events on the provider's
+ * stream.  Enabling clears the ring. */
+NF_API void nf_hip_enable_timing(bool enable);
+NF_API uint32_t nf_hip_get_timing_count(void);
+NF_API void nf_hip_get_timings(char (*op_names)[64], double *gpu_ms, uint32_t max_count);
+NF_API void nf_hip_get_timings_ext(char (*op_names)[64], double *gpu_ms, uint8_t *dtypes,
+                                   uint32_t *elem_counts, uint32_t max_count);
+
+/* ---- MI355X extensions (no counterpart in the reference) -------------- */
+
+/* Which kernel a dispatch would run and the work it represents.  Pure host
+ * logic: validates exactly like dispatch() and needs no GPU, so callers
+ * (and tests) can inspect kernel selection and size checks. */
+typedef struct nf_hip_plan {
+    char kernel[64];       /* kernel family, e.g. "gemv_q4_0_f32" */
+    uint32_t M, N, K;
+    uint64_t count;        /* dequant ops: elements written */
+    uint64_t weight_bytes; /* algorithmic bytes, each operand counted once */
+    uint64_t act_bytes;
+    uint64_t out_bytes;
+    uint64_t flops;        /* 2*M*N*K for matmul ops, 0 otherwise */
+} nf_hip_plan;
+
+NF_API nf_status nf_hip_plan_dispatch(const char *op_name,
+                                      const nf_tensor_desc *in_descs, uint32_t n_in,
+                                      const nf_tensor_desc *out_descs, uint32_t n_out,
+                                      const void *push_constants, uint32_t push_constants_size,
+                                      nf_hip_plan *plan);
+
+/* Batch-size switch points between the skinny (GEMV) kernels and the MFMA
+ * GEMM kernels: dispatch uses the GEMV family while M <= max_m.  Defaults
+ * come from measurement; environment overrides NF_HIP_GEMV_MAX_M_F32 and
+ * NF_HIP_GEMV_MAX_M_F16 are read at nf_plugin_register. */
+NF_API void nf_hip_set_gemv_max_m(uint32_t f32_path, uint32_t f16_path);
+NF_API void nf_hip_get_gemv_max_m(uint32_t *f32_path, uint32_t *f16_path);
+
+/* Dispatch `n_tasks` prepared task descriptors in order, `repeat` times —
+ * a compiled step submitted with one call, the way Session::step walks its
+ * plan (PipelineEngine.hpp:518-561) but without a thread hop per node.  Each
+ * element goes through the same path as vtable.dispatch (same validation,
+ * same stream); returns the first non-NF_OK status. */
+NF_API nf_status nf_hip_run_tasks(nf_provider self, const nf_task_desc *tasks, uint32_t n_tasks,
+                                  uint32_t repeat);
+
+/* The in-order hipStream_t (as void*) every dispatch is launched on, so a
+ * caller can time or capture (hipStreamBeginCapture) a run of dispatches.
+ * NF_ERROR_INVALID_ARG before init. */
+NF_API nf_status nf_hip_get_stream(nf_provider self, void **stream);
+
+/* Device pointer behind one of this provider's buffers (for zero-copy
+ * hand-off to other HIP code in the same process). */
+NF_API nf_status nf_hip_buffer_device_ptr(nf_buffer buf, void **dev_ptr);
+
+/* Last error text recorded by the provider (thread-local, never NULL). */
+NF_API const char *nf_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NF_HIP_PLUGIN_H */

@@ -1,0 +1,94 @@
+// common.hpp — device helpers shared by the gfx950 kernels.
+//
+// Block formats (ggml/GGUF, 32 elements per block along K):
+//   Q4_0 (18 B): u16 fp16 scale d, then qs[16]; element i < 16 is the low
+//                nibble of qs[i], element i >= 16 the high nibble of
+//                qs[i-16]; value = d * (nibble - 8).
+//   Q8_0 (34 B): u16 fp16 scale d, then 32 int8 codes; value = d * q.
+// (metal_provider.mm:500-530, dequant_test.cpp:61-128.)
+//
+// Numerics: the f32 value d*q is exact in fp32 (an 11-bit significand times
+// an integer of at most 8 bits), so the f32 path is exact.  The f16 path
+// rounds that exact product to nearest-even fp16 (metal_provider.mm:749,758),
+// which is what a single IEEE fp16 conversion or an fp16 multiply of the two
+// exactly-representable factors yields.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nfk {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Q4_0 {
+  static constexpr int kBytes = 18;
+};
+struct Q8_0 {
+  static constexpr int kBytes = 34;
+};
+
+__device__ __forceinline__ float h2f_bits(uint16_t h) {
+  return (float)__builtin_bit_cast(half_t, h);
+}
+
+// Value of element `i` (0..31) of a block starting at `blk` (2-byte aligned).
+template <class QF>
+__device__ __forceinline__ int code_of(const uint8_t* blk, int i);
+
+template <>
+__device__ __forceinline__ int code_of<Q4_0>(const uint8_t* blk, int i) {
+  const uint8_t b = blk[2 + (i & 15)];
+  return (i < 16 ? (b & 0xF) : (b >> 4)) - 8;
+}
+
+template <>
+__device__ __forceinline__ int code_of<Q8_0>(const uint8_t* blk, int i) {
+  return (int)(int8_t)blk[2 + i];
+}
+
+// Eight consecutive elements [8*quarter, 8*quarter+8) of one block, as exact
+// f32 products d*q.  `blk` is 2-byte aligned; loads are 16-bit.
+template <class QF>
+__device__ __forceinline__ void quarter_f32(const uint8_t* blk, int quarter, float v[8]);
+
+template <>
+__device__ __forceinline__ void quarter_f32<Q4_0>(const uint8_t* blk, int quarter, float v[8]) {
+  const uint16_t* p = reinterpret_cast<const uint16_t*>(blk);
+  const float d = h2f_bits(p[0]);
+  // Quarters 0/2 read qs[0..7], quarters 1/3 read qs[8..15]; quarters 2/3
+  // take the high nibbles.
+  const uint16_t* q = p + 1 + (quarter & 1) * 4;
+  const int shift = (quarter >> 1) * 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t s = q[j];
+    v[2 * j + 0] = d * (float)((int)((s >> shift) & 0xF) - 8);
+    v[2 * j + 1] = d * (float)((int)((s >> (8 + shift)) & 0xF) - 8);
+  }
+}
+
+template <>
+__device__ __forceinline__ void quarter_f32<Q8_0>(const uint8_t* blk, int quarter, float v[8]) {
+  const uint16_t* p = reinterpret_cast<const uint16_t*>(blk);
+  const float d = h2f_bits(p[0]);
+  const uint16_t* q = p + 1 + quarter * 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t s = q[j];
+    v[2 * j + 0] = d * (float)(int)(int8_t)(s & 0xFF);
+    v[2 * j + 1] = d * (float)(int)(int8_t)(s >> 8);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace nfk

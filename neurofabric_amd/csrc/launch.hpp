@@ -1,0 +1,29 @@
+// launch.hpp — host entry points of the kernel translation units.
+//
+// Each function validates nothing (plan.cpp already did) and enqueues on
+// `s`.  Shapes: A[M,K] row-major, W[N,K] as 32-element blocks along K,
+// C[M,N] row-major.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "plan.hpp"
+
+namespace nfhip {
+
+hipError_t launch_dequant(QFmt q, EType out_t, const void* w, void* out, uint64_t count,
+                          hipStream_t s);
+
+hipError_t launch_gemv(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
+                       uint32_t N, uint32_t K, hipStream_t s);
+
+hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
+                            uint32_t N, uint32_t K, hipStream_t s);
+
+hipError_t launch_generic(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
+                          uint32_t N, uint32_t K, hipStream_t s);
+
+hipError_t launch_dense(EType a, EType b, EType c, const void* A, const void* B, void* C,
+                        uint32_t M, uint32_t N, uint32_t K, hipStream_t s);
+
+}  // namespace nfhip

@@ -1,0 +1,170 @@
+// plan.cpp — validation and kernel selection for every op the provider serves.
+//
+// Semantics follow the reference's Metal host code:
+//   * dequant ops write count = out.size_bytes / element-size elements
+//     (metal_provider.mm:2654-2684);
+//   * the fused dequant+linear op picks its f16 path from the OUTPUT dtype
+//     (metal_provider.mm:2997) and reads M, N, K from push-constant bytes
+//     20/24/28 (metal_provider.mm:2301-2307, 3006-3007);
+//   * dense linear picks its path from A's and C's dtypes
+//     (metal_provider.mm:2551-2552).
+// Where the reference would read out of bounds or reinterpret a buffer with
+// the wrong element type, this provider returns NF_ERROR_INVALID_ARG instead.
+#include "plan.hpp"
+
+#include <cstring>
+#include <unordered_map>
+
+namespace nfhip {
+namespace {
+
+struct OpInfo {
+  OpKind kind;
+  QFmt q;
+  bool f16_out;  // dequant only: op name carries the _f16 suffix
+};
+
+const std::unordered_map<std::string, OpInfo>& op_table() {
+  static const std::unordered_map<std::string, OpInfo> t = {
+      {"dequant_q4_0", {OpKind::Dequant, QFmt::Q4_0, false}},
+      {"dequant_q4_0_f16", {OpKind::Dequant, QFmt::Q4_0, true}},
+      {"dequant_q8_0", {OpKind::Dequant, QFmt::Q8_0, false}},
+      {"dequant_q8_0_f16", {OpKind::Dequant, QFmt::Q8_0, true}},
+      {"dequant_q4_0_linear", {OpKind::FusedLinear, QFmt::Q4_0, false}},
+      {"dequant_q4_0_linear_f16", {OpKind::FusedLinear, QFmt::Q4_0, false}},
+      {"dequant_q8_0_linear", {OpKind::FusedLinear, QFmt::Q8_0, false}},
+      {"dequant_q8_0_linear_f16", {OpKind::FusedLinear, QFmt::Q8_0, false}},
+      {"linear", {OpKind::DenseLinear, QFmt::None, false}},
+      {"linear_tiled", {OpKind::DenseLinear, QFmt::None, false}},
+  };
+  return t;
+}
+
+const char* qname(QFmt q) { return q == QFmt::Q4_0 ? "q4_0" : "q8_0"; }
+const char* ename(EType e) { return e == EType::F16 ? "f16" : "f32"; }
+
+nf_status fail(std::string* why, const std::string& msg) {
+  if (why) *why = msg;
+  return NF_ERROR_INVALID_ARG;
+}
+
+// Reads M, N, K from the push-constant block (bytes 20, 24, 28).
+nf_status read_mnk(const uint8_t* pc, uint32_t pc_size, uint32_t* M, uint32_t* N, uint32_t* K,
+                   std::string* why) {
+  if (!pc || pc_size < 32 || pc_size > 64)
+    return fail(why, "matmul ops need push constants carrying M, N, K (bytes 20..31)");
+  std::memcpy(M, pc + 20, 4);
+  std::memcpy(N, pc + 24, 4);
+  std::memcpy(K, pc + 28, 4);
+  if (*M == 0 || *N == 0 || *K == 0) return fail(why, "M, N and K must be non-zero");
+  if (*M > (1u << 30) || *N > (1u << 30) || *K > (1u << 30))
+    return fail(why, "M, N, K beyond 2^30 are not supported");
+  return NF_OK;
+}
+
+}  // namespace
+
+bool op_known(const char* op_name) {
+  return op_name && op_table().count(op_name) != 0;
+}
+
+nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint32_t n_in,
+                    const nf_tensor_desc* const* outs, uint32_t n_out, const uint8_t* pc,
+                    uint32_t pc_size, const Tuning& tuning, Plan* plan, std::string* why) {
+  if (!op_name) return fail(why, "null op name");
+  auto it = op_table().find(op_name);
+  if (it == op_table().end()) {
+    if (why) *why = std::string("unsupported op '") + op_name + "'";
+    return NF_ERROR_UNSUPPORTED_OP;
+  }
+  const OpInfo& info = it->second;
+  Plan p;
+  p.op = info.kind;
+  p.q = info.q;
+
+  if (info.kind == OpKind::Dequant) {
+    if (n_in < 1 || n_out < 1 || !ins || !outs || !ins[0] || !outs[0])
+      return fail(why, "dequant ops take 1 input and 1 output");
+    p.c = info.f16_out ? EType::F16 : EType::F32;
+    p.path = Path::Dequant;
+    p.count = outs[0]->size_bytes / elt_bytes(p.c);
+    const uint64_t blocks = (p.count + 31) / 32;
+    p.weight_bytes = blocks * block_bytes(p.q);
+    p.out_bytes = p.count * elt_bytes(p.c);
+    if (ins[0]->size_bytes < p.weight_bytes)
+      return fail(why, "quantized input holds fewer blocks than the output needs");
+    p.kernel = std::string("dequant_") + qname(p.q) + "_" + ename(p.c);
+    *plan = p;
+    return NF_OK;
+  }
+
+  if (n_in < 2 || n_out < 1 || !ins || !outs || !ins[0] || !ins[1] || !outs[0])
+    return fail(why, "linear ops take 2 inputs (A, W) and 1 output");
+  nf_status st = read_mnk(pc, pc_size, &p.M, &p.N, &p.K, why);
+  if (st != NF_OK) return st;
+  const uint64_t M = p.M, N = p.N, K = p.K;
+  p.flops = 2ull * M * N * K;
+
+  if (info.kind == OpKind::FusedLinear) {
+    // Path from the output dtype (metal_provider.mm:2997).
+    if (outs[0]->dtype == NF_DTYPE_F16) {
+      p.a = p.b = p.c = EType::F16;
+      if (ins[0]->dtype != NF_DTYPE_F16)
+        return fail(why, "f16 output requires f16 activations (A dtype must be F16)");
+    } else {
+      if (outs[0]->dtype != NF_DTYPE_F32)
+        return fail(why, "fused linear output must be F32 or F16");
+      if (ins[0]->dtype != NF_DTYPE_F32)
+        return fail(why, "f32 output requires f32 activations (A dtype must be F32)");
+      p.a = p.b = p.c = EType::F32;
+    }
+    const uint64_t blocks = (K % 32 == 0) ? N * (K / 32) : (N * K + 31) / 32;
+    p.weight_bytes = blocks * block_bytes(p.q);
+    p.act_bytes = M * K * elt_bytes(p.a);
+    p.out_bytes = M * N * elt_bytes(p.c);
+    if (ins[0]->size_bytes < p.act_bytes) return fail(why, "A is smaller than M*K elements");
+    if (ins[1]->size_bytes < p.weight_bytes)
+      return fail(why, "W holds fewer quantized blocks than N*K/32");
+    if (outs[0]->size_bytes < p.out_bytes) return fail(why, "C is smaller than M*N elements");
+    const std::string tag = std::string(qname(p.q)) + "_" + ename(p.c);
+    if (K % 32 != 0) {
+      p.path = Path::Generic;
+      p.kernel = "generic_" + tag;
+    } else {
+      const uint32_t max_m = (p.c == EType::F16) ? tuning.gemv_max_m_f16 : tuning.gemv_max_m_f32;
+      if (p.M <= max_m) {
+        p.path = Path::Gemv;
+        p.kernel = "gemv_" + tag;
+      } else {
+        p.path = Path::GemmMfma;
+        p.kernel = "gemm_mfma_" + tag;
+      }
+    }
+    *plan = p;
+    return NF_OK;
+  }
+
+  // Dense linear: dtype-driven (metal_provider.mm:2551-2552).
+  auto etype_of = [](nf_dtype d, bool* ok) {
+    *ok = (d == NF_DTYPE_F16 || d == NF_DTYPE_F32);
+    return d == NF_DTYPE_F16 ? EType::F16 : EType::F32;
+  };
+  bool ok_a = false, ok_b = false, ok_c = false;
+  p.a = etype_of(ins[0]->dtype, &ok_a);
+  p.b = etype_of(ins[1]->dtype, &ok_b);
+  p.c = etype_of(outs[0]->dtype, &ok_c);
+  if (!ok_a || !ok_c) return fail(why, "linear needs F32 or F16 activations and output");
+  if (!ok_b) p.b = p.a;  // untyped weight buffer: same element type as A
+  p.weight_bytes = N * K * elt_bytes(p.b);
+  p.act_bytes = M * K * elt_bytes(p.a);
+  p.out_bytes = M * N * elt_bytes(p.c);
+  if (ins[0]->size_bytes < p.act_bytes) return fail(why, "A is smaller than M*K elements");
+  if (ins[1]->size_bytes < p.weight_bytes) return fail(why, "B is smaller than N*K elements");
+  if (outs[0]->size_bytes < p.out_bytes) return fail(why, "C is smaller than M*N elements");
+  p.path = Path::Dense;
+  p.kernel = std::string("linear_") + ename(p.a) + ename(p.b) + "_" + ename(p.c);
+  *plan = p;
+  return NF_OK;
+}
+
+}  // namespace nfhip

@@ -1,0 +1,62 @@
+// plan.hpp — host-side op planning for the HIP provider.
+//
+// Turns (op name, operand descriptors, push constants) into a validated
+// execution plan: which kernel family runs, with which M/N/K and how much
+// algorithmic work it represents.  No HIP types appear here, so the same
+// logic backs dispatch() and the GPU-free nf_hip_plan_dispatch() query.
+#pragma once
+
+#include <cstdint>
+#include <string>
+
+#include "nf_abi.h"
+
+namespace nfhip {
+
+enum class OpKind { Dequant, FusedLinear, DenseLinear };
+enum class QFmt { None, Q4_0, Q8_0 };
+enum class EType { F32, F16 };
+enum class Path {
+  Dequant,   // standalone dequantization
+  Gemv,      // skinny kernel (decode), M <= crossover
+  GemmMfma,  // LDS-tiled MFMA kernel (prefill), M > crossover
+  Generic,   // flat-index fallback for K % 32 != 0
+  Dense      // dense linear (weights already dequantized)
+};
+
+// Default switch points (M <= max_m runs the skinny kernels).  The f32 path
+// has no MFMA kernel yet, so every M stays on the skinny kernels.
+struct Tuning {
+  uint32_t gemv_max_m_f32 = 0xFFFFFFFFu;
+  uint32_t gemv_max_m_f16 = 16;
+};
+
+struct Plan {
+  OpKind op = OpKind::Dequant;
+  QFmt q = QFmt::None;
+  EType a = EType::F32, b = EType::F32, c = EType::F32;
+  Path path = Path::Dequant;
+  uint32_t M = 0, N = 0, K = 0;
+  uint64_t count = 0;  // dequant: output elements
+  uint64_t weight_bytes = 0, act_bytes = 0, out_bytes = 0, flops = 0;
+  std::string kernel;
+};
+
+// Bytes of one 32-element block: Q4_0 = 2 (fp16 scale) + 16, Q8_0 = 2 + 32
+// (gguf_loader.hpp:64,68).
+inline uint32_t block_bytes(QFmt q) { return q == QFmt::Q4_0 ? 18u : (q == QFmt::Q8_0 ? 34u : 0u); }
+inline uint32_t elt_bytes(EType t) { return t == EType::F16 ? 2u : 4u; }
+
+// Validates and plans one dispatch.  `ins`/`outs` are descriptor pointers
+// (may be null when n == 0).  `pc` points at the task's push-constant bytes
+// or is null.  Returns NF_OK, NF_ERROR_UNSUPPORTED_OP (unknown name) or
+// NF_ERROR_INVALID_ARG (arity, dtype or size mismatch); `why` receives a
+// human-readable reason on error.
+nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint32_t n_in,
+                    const nf_tensor_desc* const* outs, uint32_t n_out, const uint8_t* pc,
+                    uint32_t pc_size, const Tuning& tuning, Plan* plan, std::string* why);
+
+// True when `op_name` is served by this provider.
+bool op_known(const char* op_name);
+
+}  // namespace nfhip

@@ -1,0 +1,741 @@
+// provider.hip — the "amd_hip" execution provider behind the NeuralOS C ABI.
+//
+// Drop-in for plugins/metal (metal_provider.mm:1999-2120, 2199-2313,
+// 3154-3289) on a discrete MI355X:
+//   * buffers are hipMalloc'd device memory, zero-filled at allocation, with
+//     a pinned host staging copy for map/unmap (map = device->host copy
+//     after all enqueued work, unmap = host->device copy on the same stream);
+//   * every dispatch is validated on the host (plan.cpp) and then enqueued
+//     on ONE in-order HIP stream under a mutex, so dependent ops dispatched
+//     from different engine threads execute in submission order — the
+//     engine treats "dispatch returned" as done (PipelineEngine.hpp:639-650);
+//   * cache_sync(INVALIDATE) blocks until the last dispatch that wrote the
+//     buffer has finished (the Metal fence contract, metal_provider.mm:2044-2062);
+//   * unknown ops return NF_ERROR_UNSUPPORTED_OP, bad arity or sizes
+//     NF_ERROR_INVALID_ARG, HIP failures NF_ERROR_DEVICE_LOST / _INTERNAL /
+//     _OUT_OF_MEMORY.  Nothing falls back to the CPU.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <chrono>
+#include <cstddef>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+
+#include "launch.hpp"
+#include "nf_abi.h"
+#include "nf_hip_plugin.h"
+#include "plan.hpp"
+
+namespace nfhip {
+namespace {
+
+thread_local std::string t_last_error;
+
+nf_status set_error(nf_status st, const std::string& msg) {
+  t_last_error = msg;
+  return st;
+}
+
+nf_status map_hip(hipError_t e, const char* where) {
+  if (e == hipSuccess) return NF_OK;
+  std::string msg = std::string(where) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+  switch (e) {
+    case hipErrorOutOfMemory:
+      return set_error(NF_ERROR_OUT_OF_MEMORY, msg);
+    case hipErrorInvalidValue:
+    case hipErrorInvalidConfiguration:
+    case hipErrorInvalidDeviceFunction:
+    case hipErrorNoBinaryForGpu:
+      return set_error(NF_ERROR_INTERNAL, msg);
+    default:
+      return set_error(NF_ERROR_DEVICE_LOST, msg);
+  }
+}
+
+// Buffers at or above this size drop their host staging after unmap, so
+// uploading model weights does not keep a second pinned copy alive.
+constexpr uint64_t kKeepStagingBelow = 64ull << 20;
+
+struct Provider;
+
+struct Buffer {
+  std::atomic<uint32_t> refs{1};
+  Provider* prov = nullptr;
+  nf_tensor_desc desc{};
+  void* dev = nullptr;
+  uint64_t bytes = 0;  // desc.size_bytes
+  uint64_t alloc_bytes = 0;
+  bool owns_dev = true;
+  std::mutex mu;  // guards the fields below
+  void* host = nullptr;     // pinned staging
+  bool host_valid = false;  // staging mirrors device contents
+  bool mapped = false;
+  uint64_t map_seq = 0;     // last_write_seq when the mapping was (re)filled
+  std::atomic<uint64_t> last_write_seq{0};
+};
+
+struct TimingRec {
+  char op[64];
+  hipEvent_t start = nullptr, stop = nullptr;
+  uint8_t dtype = 0;
+  uint32_t elems = 0;
+};
+
+constexpr uint32_t kTimingRing = 1024;
+
+struct Provider {
+  std::mutex mu;  // init/shutdown and every launch
+  bool initialized = false;
+  int device = -1;
+  hipStream_t stream = nullptr;
+  hipDeviceProp_t props{};
+  uint64_t issued_seq = 0;            // guarded by mu
+  std::atomic<uint64_t> done_seq{0};  // all dispatches <= done_seq finished
+  Tuning tuning;
+  // timing ring
+  std::atomic<bool> timing{false};
+  std::atomic<uint32_t> timing_head{0};
+  bool ring_ready = false;
+  TimingRec ring[kTimingRing];
+};
+
+Provider g_prov;
+
+Provider* as_prov(nf_provider p) { return reinterpret_cast<Provider*>(p); }
+Buffer* as_buf(nf_buffer b) { return reinterpret_cast<Buffer*>(b); }
+
+// Drain the provider stream; everything issued so far is then complete.
+nf_status drain(Provider* p) {
+  uint64_t target;
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (!p->initialized) return NF_OK;
+    target = p->issued_seq;
+  }
+  hipError_t e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) return map_hip(e, "hipStreamSynchronize");
+  uint64_t cur = p->done_seq.load();
+  while (cur < target && !p->done_seq.compare_exchange_weak(cur, target)) {
+  }
+  return NF_OK;
+}
+
+nf_status wait_for_writes(Buffer* b) {
+  Provider* p = b->prov;
+  if (b->last_write_seq.load() <= p->done_seq.load()) return NF_OK;
+  return drain(p);
+}
+
+nf_status ensure_staging(Buffer* b) {
+  if (b->host) return NF_OK;
+  void* h = nullptr;
+  hipError_t e = hipHostMalloc(&h, b->alloc_bytes, hipHostMallocDefault);
+  if (e != hipSuccess) return map_hip(e, "hipHostMalloc(staging)");
+  b->host = h;
+  b->host_valid = false;
+  return NF_OK;
+}
+
+// Copy between staging and device on the provider stream, then wait.
+nf_status copy_sync(Buffer* b, bool to_host) {
+  Provider* p = b->prov;
+  if (b->bytes == 0) return NF_OK;
+  hipError_t e;
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (!p->initialized) return set_error(NF_ERROR_INVALID_ARG, "provider not initialised");
+    e = to_host ? hipMemcpyAsync(b->host, b->dev, b->bytes, hipMemcpyDeviceToHost, p->stream)
+                : hipMemcpyAsync(b->dev, b->host, b->bytes, hipMemcpyHostToDevice, p->stream);
+  }
+  if (e != hipSuccess) return map_hip(e, to_host ? "hipMemcpyAsync(D2H)" : "hipMemcpyAsync(H2D)");
+  return drain(p);
+}
+
+void free_buffer(Buffer* b) {
+  Provider* p = b->prov;
+  if (p && p->initialized) (void)hipStreamSynchronize(p->stream);
+  if (b->owns_dev && b->dev) (void)hipFree(b->dev);
+  if (b->host) (void)hipHostFree(b->host);
+  delete b;
+}
+
+/* ---- nf_buffer_ops ------------------------------------------------- */
+
+uint32_t buf_retain(nf_buffer self) {
+  return as_buf(self)->refs.fetch_add(1, std::memory_order_relaxed) + 1;
+}
+
+uint32_t buf_release(nf_buffer self) {
+  Buffer* b = as_buf(self);
+  const uint32_t prev = b->refs.fetch_sub(1, std::memory_order_acq_rel);
+  if (prev == 1) free_buffer(b);
+  return prev - 1;
+}
+
+nf_status buf_map(nf_buffer self, void** out_ptr) {
+  if (!self || !out_ptr) return set_error(NF_ERROR_INVALID_ARG, "map: null argument");
+  Buffer* b = as_buf(self);
+  std::lock_guard<std::mutex> lk(b->mu);
+  if (b->mapped) return set_error(NF_ERROR_INVALID_ARG, "map: buffer already mapped");
+  nf_status st = ensure_staging(b);
+  if (st != NF_OK) return st;
+  if (!b->host_valid) {
+    st = copy_sync(b, /*to_host=*/true);  // ordered after every enqueued write
+    if (st != NF_OK) return st;
+    b->host_valid = true;
+  }
+  b->map_seq = b->last_write_seq.load();
+  b->mapped = true;
+  *out_ptr = b->host;
+  return NF_OK;
+}
+
+nf_status buf_unmap(nf_buffer self) {
+  if (!self) return set_error(NF_ERROR_INVALID_ARG, "unmap: null buffer");
+  Buffer* b = as_buf(self);
+  std::lock_guard<std::mutex> lk(b->mu);
+  if (!b->mapped) return NF_OK;  // unmapping an unmapped buffer is a no-op, as in Metal
+  b->mapped = false;
+  // Upload the host view unless a dispatch wrote the buffer while it was
+  // mapped (the device contents are then newer than the staging copy).
+  if (b->last_write_seq.load() == b->map_seq) {
+    nf_status st = copy_sync(b, /*to_host=*/false);
+    if (st != NF_OK) return st;
+    b->host_valid = true;
+  }
+  if (b->bytes >= kKeepStagingBelow) {
+    (void)hipHostFree(b->host);
+    b->host = nullptr;
+    b->host_valid = false;
+  }
+  return NF_OK;
+}
+
+nf_status buf_cache_sync(nf_buffer self, nf_cache_op op, uint64_t, uint64_t) {
+  if (!self) return set_error(NF_ERROR_INVALID_ARG, "cache_sync: null buffer");
+  Buffer* b = as_buf(self);
+  std::lock_guard<std::mutex> lk(b->mu);
+  if ((op & NF_CACHE_FLUSH) && b->mapped) {
+    // Host writes made through a live mapping become visible to the device.
+    nf_status st = copy_sync(b, false);
+    if (st != NF_OK) return st;
+  }
+  if (op & NF_CACHE_INVALIDATE) {
+    nf_status st = wait_for_writes(b);
+    if (st != NF_OK) return st;
+    if (b->mapped) {
+      // A live mapping sees the device's latest contents.
+      st = copy_sync(b, true);
+      if (st != NF_OK) return st;
+      b->host_valid = true;
+      b->map_seq = b->last_write_seq.load();
+    }
+  }
+  return NF_OK;
+}
+
+nf_status buf_get_info(nf_buffer self, nf_buffer_info* info) {
+  if (!self || !info) return set_error(NF_ERROR_INVALID_ARG, "get_info: null argument");
+  Buffer* b = as_buf(self);
+  std::memset(info, 0, sizeof(*info));
+  info->desc = b->desc;
+  info->domain = NF_MEM_DOMAIN_DEVICE;
+  info->offset_bytes = 0;
+  info->share_token = reinterpret_cast<uint64_t>(b->dev);
+  info->refcount = b->refs.load(std::memory_order_relaxed);
+  return NF_OK;
+}
+
+nf_status buf_export(nf_buffer self, uint64_t* token, nf_mem_domain* domain) {
+  if (!self || !token || !domain) return set_error(NF_ERROR_INVALID_ARG, "export: null argument");
+  *token = reinterpret_cast<uint64_t>(as_buf(self)->dev);
+  *domain = NF_MEM_DOMAIN_DEVICE;
+  return NF_OK;
+}
+
+nf_status wrap_device_ptr(Provider* p, uint64_t token, const nf_tensor_desc* desc, nf_buffer* out);
+
+nf_status buf_import(nf_provider provider, uint64_t token, nf_mem_domain domain,
+                     const nf_tensor_desc* desc, nf_buffer* out) {
+  if (domain != NF_MEM_DOMAIN_DEVICE)
+    return set_error(NF_ERROR_UNSUPPORTED_OP, "import: only NF_MEM_DOMAIN_DEVICE tokens are accepted");
+  return wrap_device_ptr(as_prov(provider), token, desc, out);
+}
+
+nf_buffer_ops make_ops() {
+  nf_buffer_ops ops{};
+  ops.retain = buf_retain;
+  ops.release = buf_release;
+  ops.map = buf_map;
+  ops.unmap = buf_unmap;
+  ops.cache_sync = buf_cache_sync;
+  ops.get_info = buf_get_info;
+  ops.export_handle = buf_export;
+  ops.import_handle = buf_import;
+  return ops;
+}
+
+/* ---- provider vtable ----------------------------------------------- */
+
+const char* hip_get_name(nf_provider) { return "amd_hip"; }
+uint32_t hip_get_abi_version(nf_provider) { return NF_ABI_VERSION; }
+
+nf_status hip_init(nf_provider self) {
+  Provider* p = as_prov(self);
+  if (!p) return set_error(NF_ERROR_INVALID_ARG, "init: null provider");
+  std::lock_guard<std::mutex> lk(p->mu);
+  if (p->initialized) return NF_OK;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0)
+    return set_error(NF_ERROR_DEVICE_LOST, "init: no HIP device visible");
+  e = hipGetDevice(&p->device);
+  if (e != hipSuccess) return map_hip(e, "hipGetDevice");
+  e = hipGetDeviceProperties(&p->props, p->device);
+  if (e != hipSuccess) return map_hip(e, "hipGetDeviceProperties");
+  if (std::strncmp(p->props.gcnArchName, "gfx950", 6) != 0)
+    return set_error(NF_ERROR_DEVICE_LOST, std::string("init: kernels are built for gfx950, device is ") +
+                                               p->props.gcnArchName);
+  e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) return map_hip(e, "hipStreamCreateWithFlags");
+  p->initialized = true;
+  return NF_OK;
+}
+
+void hip_shutdown(nf_provider self) {
+  Provider* p = as_prov(self);
+  if (!p) return;
+  std::lock_guard<std::mutex> lk(p->mu);
+  if (!p->initialized) return;
+  (void)hipStreamSynchronize(p->stream);
+  p->done_seq.store(p->issued_seq);
+  if (p->ring_ready) {
+    for (auto& r : p->ring) {
+      (void)hipEventDestroy(r.start);
+      (void)hipEventDestroy(r.stop);
+      r.start = r.stop = nullptr;
+    }
+    p->ring_ready = false;
+  }
+  (void)hipStreamDestroy(p->stream);
+  p->stream = nullptr;
+  p->initialized = false;
+}
+
+nf_status alloc_buffer(Provider* p, const nf_tensor_desc* desc, nf_buffer* out) {
+  if (!p || !desc || !out) return set_error(NF_ERROR_INVALID_ARG, "alloc: null argument");
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (!p->initialized) return set_error(NF_ERROR_INVALID_ARG, "alloc: provider not initialised");
+  }
+  Buffer* b = new Buffer;
+  b->prov = p;
+  b->desc = *desc;
+  b->bytes = desc->size_bytes;
+  b->alloc_bytes = (desc->size_bytes + 255) & ~255ull;
+  if (b->alloc_bytes == 0) b->alloc_bytes = 256;
+  hipError_t e = hipMalloc(&b->dev, b->alloc_bytes);
+  if (e != hipSuccess) {
+    delete b;
+    return map_hip(e, "hipMalloc");
+  }
+  // Zero-fill, as the reference does (metal_provider.mm:2277-2278).
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    e = hipMemsetAsync(b->dev, 0, b->alloc_bytes, p->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(b->dev);
+    delete b;
+    return map_hip(e, "zero-fill");
+  }
+  *out = reinterpret_cast<nf_buffer>(b);
+  return NF_OK;
+}
+
+nf_status wrap_device_ptr(Provider* p, uint64_t token, const nf_tensor_desc* desc, nf_buffer* out) {
+  if (!p || !desc || !out || token == 0) return set_error(NF_ERROR_INVALID_ARG, "import: bad argument");
+  Buffer* b = new Buffer;
+  b->prov = p;
+  b->desc = *desc;
+  b->bytes = desc->size_bytes;
+  b->alloc_bytes = desc->size_bytes ? desc->size_bytes : 1;
+  b->dev = reinterpret_cast<void*>(token);
+  b->owns_dev = false;
+  *out = reinterpret_cast<nf_buffer>(b);
+  return NF_OK;
+}
+
+nf_status hip_buffer_alloc(nf_provider self, const nf_tensor_desc* desc, nf_buffer* out) {
+  return alloc_buffer(as_prov(self), desc, out);
+}
+
+void hip_buffer_free(nf_provider, nf_buffer buf) {
+  if (buf) buf_release(buf);
+}
+
+nf_status hip_buffer_map(nf_provider, nf_buffer buf, void** out) { return buf_map(buf, out); }
+nf_status hip_buffer_unmap(nf_provider, nf_buffer buf) { return buf_unmap(buf); }
+
+bool reads_push_constants(const char* op) {
+  return std::strstr(op, "linear") != nullptr;
+}
+
+// The engine passes &task_desc.inputs[0]; step back to the descriptor to
+// read its push constants (metal_provider.mm:2301-2307).
+const nf_task_desc* enclosing_task(const nf_buffer* inputs) {
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(inputs) - offsetof(nf_task_desc, inputs);
+  return reinterpret_cast<const nf_task_desc*>(base);
+}
+
+hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, hipStream_t s) {
+  switch (pl.path) {
+    case Path::Dequant:
+      return launch_dequant(pl.q, pl.c, in[0]->dev, out[0]->dev, pl.count, s);
+    case Path::Gemv:
+      return launch_gemv(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
+    case Path::GemmMfma:
+      return launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
+    case Path::Generic:
+      return launch_generic(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
+    case Path::Dense:
+      return launch_dense(pl.a, pl.b, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+void ensure_ring(Provider* p) {
+  if (p->ring_ready) return;
+  for (auto& r : p->ring) {
+    (void)hipEventCreate(&r.start);
+    (void)hipEventCreate(&r.stop);
+  }
+  p->ring_ready = true;
+}
+
+nf_status hip_dispatch(nf_provider self, const char* op_name, const nf_buffer* inputs,
+                       uint32_t n_in, nf_buffer* outputs, uint32_t n_out) {
+  Provider* p = as_prov(self);
+  if (!p || !op_name) return set_error(NF_ERROR_INVALID_ARG, "dispatch: null provider or op name");
+  if (!op_known(op_name))
+    return set_error(NF_ERROR_UNSUPPORTED_OP, std::string("dispatch: unsupported op '") + op_name + "'");
+  if (n_in > NF_MAX_TASK_INPUTS || n_out > NF_MAX_TASK_OUTPUTS || (n_in && !inputs) || (n_out && !outputs))
+    return set_error(NF_ERROR_INVALID_ARG, "dispatch: bad input/output arrays");
+  Buffer* in[NF_MAX_TASK_INPUTS] = {};
+  Buffer* out[NF_MAX_TASK_OUTPUTS] = {};
+  const nf_tensor_desc* in_d[NF_MAX_TASK_INPUTS] = {};
+  const nf_tensor_desc* out_d[NF_MAX_TASK_OUTPUTS] = {};
+  for (uint32_t i = 0; i < n_in; ++i) {
+    in[i] = as_buf(inputs[i]);
+    if (!in[i]) return set_error(NF_ERROR_INVALID_ARG, "dispatch: null input buffer");
+    in_d[i] = &in[i]->desc;
+  }
+  for (uint32_t i = 0; i < n_out; ++i) {
+    out[i] = as_buf(outputs[i]);
+    if (!out[i]) return set_error(NF_ERROR_INVALID_ARG, "dispatch: null output buffer");
+    out_d[i] = &out[i]->desc;
+  }
+  const uint8_t* pc = nullptr;
+  uint32_t pc_size = 0;
+  if (reads_push_constants(op_name) && n_in > 0) {
+    const nf_task_desc* td = enclosing_task(inputs);
+    pc_size = td->push_constants_size;
+    pc = td->push_constants;
+  }
+  Plan pl;
+  std::string why;
+  nf_status st = make_plan(op_name, in_d, n_in, out_d, n_out, pc, pc_size, p->tuning, &pl, &why);
+  if (st != NF_OK) return set_error(st, std::string("dispatch ") + op_name + ": " + why);
+
+  hipError_t e;
+  uint64_t seq;
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (!p->initialized) return set_error(NF_ERROR_INVALID_ARG, "dispatch: provider not initialised");
+    seq = ++p->issued_seq;
+    TimingRec* rec = nullptr;
+    if (p->timing.load(std::memory_order_relaxed)) {
+      ensure_ring(p);
+      rec = &p->ring[p->timing_head.fetch_add(1, std::memory_order_relaxed) % kTimingRing];
+      std::strncpy(rec->op, op_name, 63);
+      rec->op[63] = '\0';
+      rec->dtype = (uint8_t)out_d[0]->dtype;
+      rec->elems = (uint32_t)(pl.path == Path::Dequant ? pl.count : (uint64_t)pl.M * pl.N);
+      (void)hipEventRecord(rec->start, p->stream);
+    }
+    e = run_plan(pl, in, out, p->stream);
+    if (rec) (void)hipEventRecord(rec->stop, p->stream);
+    for (uint32_t i = 0; i < n_out; ++i) out[i]->last_write_seq.store(seq);
+  }
+  // Buffer flags are updated outside the provider lock (map takes the
+  // buffer lock first, then the provider lock).
+  for (uint32_t i = 0; i < n_out; ++i) {
+    std::lock_guard<std::mutex> bl(out[i]->mu);
+    out[i]->host_valid = false;
+  }
+  if (e != hipSuccess) return map_hip(e, (std::string("launch ") + pl.kernel).c_str());
+  return NF_OK;
+}
+
+nf_status hip_synchronize(nf_provider self) {
+  Provider* p = as_prov(self);
+  if (!p) return set_error(NF_ERROR_INVALID_ARG, "synchronize: null provider");
+  return drain(p);
+}
+
+/* ---- memory vtable ------------------------------------------------- */
+
+nf_status mem_alloc(nf_provider self, const nf_buffer_alloc_request* req, nf_buffer_ops* ops,
+                    nf_buffer* buf) {
+  if (!req || !ops || !buf) return set_error(NF_ERROR_INVALID_ARG, "mem alloc: null argument");
+  nf_status st = alloc_buffer(as_prov(self), &req->desc, buf);
+  if (st != NF_OK) return st;
+  *ops = make_ops();
+  return NF_OK;
+}
+
+nf_status mem_import(nf_provider self, uint64_t token, nf_mem_domain domain, const nf_tensor_desc* desc,
+                     nf_buffer_ops* ops, nf_buffer* buf) {
+  if (!ops) return set_error(NF_ERROR_INVALID_ARG, "mem import: null ops");
+  nf_status st = buf_import(self, token, domain, desc, buf);
+  if (st != NF_OK) return st;
+  *ops = make_ops();
+  return NF_OK;
+}
+
+nf_status mem_can_import(nf_provider, nf_mem_domain domain) {
+  return domain == NF_MEM_DOMAIN_DEVICE ? NF_OK : NF_ERROR_UNSUPPORTED_OP;
+}
+
+/* ---- async DDI ----------------------------------------------------- */
+
+struct Token {
+  hipEvent_t ev = nullptr;
+};
+
+nf_status ddi_dispatch_async(nf_provider self, const char* op, const nf_buffer* in, uint32_t n_in,
+                             nf_buffer* out, uint32_t n_out, nf_completion_token* token) {
+  if (!token) return set_error(NF_ERROR_INVALID_ARG, "dispatch_async: null token");
+  nf_status st = hip_dispatch(self, op, in, n_in, out, n_out);
+  if (st != NF_OK) return st;
+  Provider* p = as_prov(self);
+  Token* t = new Token;
+  hipError_t e = hipEventCreateWithFlags(&t->ev, hipEventDisableTiming);
+  if (e == hipSuccess) {
+    std::lock_guard<std::mutex> lk(p->mu);
+    e = hipEventRecord(t->ev, p->stream);
+  }
+  if (e != hipSuccess) {
+    if (t->ev) (void)hipEventDestroy(t->ev);
+    delete t;
+    return map_hip(e, "dispatch_async: event");
+  }
+  *token = reinterpret_cast<nf_completion_token>(t);
+  return NF_OK;
+}
+
+// A token is consumed by the wait/poll call that observes its completion.
+nf_status ddi_wait(nf_provider, nf_completion_token token, uint64_t timeout_ms) {
+  Token* t = reinterpret_cast<Token*>(token);
+  if (!t) return set_error(NF_ERROR_INVALID_ARG, "wait: null token");
+  const auto t0 = std::chrono::steady_clock::now();
+  for (;;) {
+    hipError_t e = hipEventQuery(t->ev);
+    if (e == hipSuccess) break;
+    if (e != hipErrorNotReady) return map_hip(e, "wait: hipEventQuery");
+    if (timeout_ms != UINT64_MAX &&
+        std::chrono::steady_clock::now() - t0 >= std::chrono::milliseconds(timeout_ms))
+      return set_error(NF_ERROR_TIMEOUT, "wait: timed out");
+    std::this_thread::sleep_for(std::chrono::microseconds(20));
+  }
+  (void)hipEventDestroy(t->ev);
+  delete t;
+  return NF_OK;
+}
+
+nf_status ddi_poll(nf_provider, nf_completion_token token) {
+  Token* t = reinterpret_cast<Token*>(token);
+  if (!t) return set_error(NF_ERROR_INVALID_ARG, "poll: null token");
+  hipError_t e = hipEventQuery(t->ev);
+  if (e == hipErrorNotReady) return NF_ERROR_TIMEOUT;
+  if (e != hipSuccess) return map_hip(e, "poll: hipEventQuery");
+  (void)hipEventDestroy(t->ev);
+  delete t;
+  return NF_OK;
+}
+
+nf_status ddi_query_caps(nf_provider self, nf_driver_caps* caps) {
+  Provider* p = as_prov(self);
+  if (!p || !caps) return set_error(NF_ERROR_INVALID_ARG, "query_caps: null argument");
+  std::memset(caps, 0, sizeof(*caps));
+  caps->max_concurrent = 1;  // one in-order stream
+  std::lock_guard<std::mutex> lk(p->mu);
+  if (p->initialized) caps->memory_bytes = p->props.totalGlobalMem;
+  caps->flops = 2516600000000000ull;  // MI355X dense fp16 MFMA peak, FLOP/s
+  caps->supported_dtypes = (1u << NF_DTYPE_F32) | (1u << NF_DTYPE_F16) | (1u << NF_DTYPE_Q4_0) |
+                           (1u << NF_DTYPE_Q8_0);
+  caps->flags = NF_CAP_ASYNC | NF_CAP_FP16 | NF_CAP_INT8;
+  return NF_OK;
+}
+
+uint32_t env_u32(const char* name, uint32_t dflt) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return dflt;
+  char* end = nullptr;
+  unsigned long x = std::strtoul(v, &end, 10);
+  return (end && *end == '\0') ? (uint32_t)x : dflt;
+}
+
+}  // namespace
+}  // namespace nfhip
+
+using namespace nfhip;
+
+extern "C" {
+
+NF_API nf_status nf_plugin_register(nf_provider_vtable* vt, nf_provider* out) {
+  if (!vt || !out) return NF_ERROR_INVALID_ARG;
+  vt->get_name = hip_get_name;
+  vt->get_abi_version = hip_get_abi_version;
+  vt->init = hip_init;
+  vt->shutdown = hip_shutdown;
+  vt->buffer_alloc = hip_buffer_alloc;
+  vt->buffer_free = hip_buffer_free;
+  vt->buffer_map = hip_buffer_map;
+  vt->buffer_unmap = hip_buffer_unmap;
+  vt->dispatch = hip_dispatch;
+  vt->synchronize = hip_synchronize;
+  g_prov.tuning.gemv_max_m_f32 = env_u32("NF_HIP_GEMV_MAX_M_F32", g_prov.tuning.gemv_max_m_f32);
+  g_prov.tuning.gemv_max_m_f16 = env_u32("NF_HIP_GEMV_MAX_M_F16", g_prov.tuning.gemv_max_m_f16);
+  *out = reinterpret_cast<nf_provider>(&g_prov);
+  return NF_OK;
+}
+
+NF_API nf_status nf_plugin_register_mem(nf_provider_mem_vtable* mem_vt) {
+  if (!mem_vt) return NF_ERROR_INVALID_ARG;
+  mem_vt->alloc = mem_alloc;
+  mem_vt->import_buffer = mem_import;
+  mem_vt->can_import = mem_can_import;
+  return NF_OK;
+}
+
+NF_API nf_status nf_plugin_register_ddi(nf_ddi_vtable* ddi) {
+  if (!ddi) return NF_ERROR_INVALID_ARG;
+  ddi->dispatch_async = ddi_dispatch_async;
+  ddi->wait_completion = ddi_wait;
+  ddi->poll_completion = ddi_poll;
+  ddi->query_caps = ddi_query_caps;
+  return NF_OK;
+}
+
+NF_API void nf_hip_enable_timing(bool enable) {
+  g_prov.timing.store(enable, std::memory_order_relaxed);
+  if (enable) g_prov.timing_head.store(0, std::memory_order_relaxed);
+}
+
+NF_API uint32_t nf_hip_get_timing_count(void) {
+  const uint32_t head = g_prov.timing_head.load(std::memory_order_relaxed);
+  return head > kTimingRing ? kTimingRing : head;
+}
+
+NF_API void nf_hip_get_timings_ext(char (*op_names)[64], double* gpu_ms, uint8_t* dtypes,
+                                   uint32_t* elem_counts, uint32_t max_count) {
+  const uint32_t head = g_prov.timing_head.load(std::memory_order_relaxed);
+  uint32_t count = head > kTimingRing ? kTimingRing : head;
+  if (count > max_count) count = max_count;
+  const uint32_t start = head > kTimingRing ? head % kTimingRing : 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    TimingRec& r = g_prov.ring[(start + i) % kTimingRing];
+    float ms = 0.f;
+    if (r.stop && hipEventSynchronize(r.stop) == hipSuccess) (void)hipEventElapsedTime(&ms, r.start, r.stop);
+    if (op_names) std::strncpy(op_names[i], r.op, 64);
+    if (gpu_ms) gpu_ms[i] = ms;
+    if (dtypes) dtypes[i] = r.dtype;
+    if (elem_counts) elem_counts[i] = r.elems;
+  }
+}
+
+NF_API void nf_hip_get_timings(char (*op_names)[64], double* gpu_ms, uint32_t max_count) {
+  nf_hip_get_timings_ext(op_names, gpu_ms, nullptr, nullptr, max_count);
+}
+
+NF_API nf_status nf_hip_plan_dispatch(const char* op_name, const nf_tensor_desc* in_descs,
+                                      uint32_t n_in, const nf_tensor_desc* out_descs, uint32_t n_out,
+                                      const void* push_constants, uint32_t push_constants_size,
+                                      nf_hip_plan* plan) {
+  if (!plan) return NF_ERROR_INVALID_ARG;
+  if (n_in > NF_MAX_TASK_INPUTS || n_out > NF_MAX_TASK_OUTPUTS || (n_in && !in_descs) ||
+      (n_out && !out_descs))
+    return set_error(NF_ERROR_INVALID_ARG, "plan: bad descriptor arrays");
+  const nf_tensor_desc* in_d[NF_MAX_TASK_INPUTS] = {};
+  const nf_tensor_desc* out_d[NF_MAX_TASK_OUTPUTS] = {};
+  for (uint32_t i = 0; i < n_in; ++i) in_d[i] = &in_descs[i];
+  for (uint32_t i = 0; i < n_out; ++i) out_d[i] = &out_descs[i];
+  Plan pl;
+  std::string why;
+  nf_status st = make_plan(op_name, in_d, n_in, out_d, n_out,
+                           static_cast<const uint8_t*>(push_constants), push_constants_size,
+                           g_prov.tuning, &pl, &why);
+  if (st != NF_OK) return set_error(st, why);
+  std::memset(plan, 0, sizeof(*plan));
+  std::strncpy(plan->kernel, pl.kernel.c_str(), 63);
+  plan->M = pl.M;
+  plan->N = pl.N;
+  plan->K = pl.K;
+  plan->count = pl.count;
+  plan->weight_bytes = pl.weight_bytes;
+  plan->act_bytes = pl.act_bytes;
+  plan->out_bytes = pl.out_bytes;
+  plan->flops = pl.flops;
+  return NF_OK;
+}
+
+NF_API void nf_hip_set_gemv_max_m(uint32_t f32_path, uint32_t f16_path) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  g_prov.tuning.gemv_max_m_f32 = f32_path;
+  g_prov.tuning.gemv_max_m_f16 = f16_path;
+}
+
+NF_API void nf_hip_get_gemv_max_m(uint32_t* f32_path, uint32_t* f16_path) {
+  if (f32_path) *f32_path = g_prov.tuning.gemv_max_m_f32;
+  if (f16_path) *f16_path = g_prov.tuning.gemv_max_m_f16;
+}
+
+NF_API nf_status nf_hip_run_tasks(nf_provider self, const nf_task_desc* tasks, uint32_t n_tasks,
+                                  uint32_t repeat) {
+  if (!self || (n_tasks && !tasks)) return NF_ERROR_INVALID_ARG;
+  for (uint32_t r = 0; r < repeat; ++r) {
+    for (uint32_t i = 0; i < n_tasks; ++i) {
+      const nf_task_desc& t = tasks[i];
+      nf_status st = hip_dispatch(self, t.op_name, t.inputs, t.n_inputs,
+                                  const_cast<nf_buffer*>(t.outputs), t.n_outputs);
+      if (st != NF_OK) return st;
+    }
+  }
+  return NF_OK;
+}
+
+NF_API nf_status nf_hip_get_stream(nf_provider self, void** stream) {
+  Provider* p = as_prov(self);
+  if (!p || !stream) return NF_ERROR_INVALID_ARG;
+  std::lock_guard<std::mutex> lk(p->mu);
+  if (!p->initialized) return set_error(NF_ERROR_INVALID_ARG, "get_stream: provider not initialised");
+  *stream = reinterpret_cast<void*>(p->stream);
+  return NF_OK;
+}
+
+NF_API nf_status nf_hip_buffer_device_ptr(nf_buffer buf, void** dev_ptr) {
+  if (!buf || !dev_ptr) return NF_ERROR_INVALID_ARG;
+  *dev_ptr = as_buf(buf)->dev;
+  return NF_OK;
+}
+
+NF_API const char* nf_hip_last_error(void) { return t_last_error.c_str(); }
+
+}  // extern "C"

@@ -1,0 +1,73 @@
+/*
+ * nf_oracle.h — CPU oracle for the quantized linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: tests/, the
+ * smoke() entry and bench.py's cpu_baseline leg call it to compute expected
+ * results and to time the reference's CPU algorithm.  The product path
+ * (libnf_plugin_hip.so) never links, loads or calls it.
+ *
+ * Each function restates the reference's CPU code or kernel semantics
+ * (citations below are relative to the reference repository):
+ *   nf_oracle_f16_to_f32      tests/driver/dequant_test.cpp:77-98
+ *   nf_oracle_f32_to_f16_trunc tests/driver/dequant_test.cpp:100-109 (the
+ *                             tests' truncating, flush-to-zero input encoder;
+ *                             used only to rebuild the tests' own inputs)
+ *   nf_oracle_f32_to_f16_rne  IEEE 754 roundTiesToEven with subnormals — the
+ *                             conversion the kernels' half(x) performs
+ *                             (plugins/metal/src/metal_provider.mm:749,758,1457,1467)
+ *   nf_oracle_dequant_*_f32   ref_dequant_q4_0/q8_0, dequant_test.cpp:112-128
+ *   nf_oracle_dequant_*_f16   dequant_q4_0_f16/q8_0_f16, metal_provider.mm:741-759
+ *   nf_oracle_linear_*        naive sequential-k loop, dequant_test.cpp:313-319,
+ *                             with B stored [N,K] (dequant_test.cpp:321-325)
+ *   nf_oracle_fused_*         dequant_q4_0_linear_tiled[_f16] semantics,
+ *                             metal_provider.mm:1396-1468: weight element (n,k)
+ *                             is flat element n*K+k of the block stream.
+ *
+ * Parity pins are in tests/test_oracle.py.
+ */
+#ifndef NF_ORACLE_H
+#define NF_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { NF_ORACLE_Q4_0 = 0, NF_ORACLE_Q8_0 = 1 };
+
+float nf_oracle_f16_to_f32(uint16_t h);
+uint16_t nf_oracle_f32_to_f16_rne(float f);
+uint16_t nf_oracle_f32_to_f16_trunc(float f);
+
+void nf_oracle_f16_to_f32_n(const uint16_t *in, float *out, uint64_t n);
+void nf_oracle_f32_to_f16_rne_n(const float *in, uint16_t *out, uint64_t n);
+
+/* Dequantize `count` elements (blocks are consumed in order; a trailing
+ * partial block is allowed). */
+void nf_oracle_dequant_q4_0_f32(const uint8_t *blocks, uint64_t count, float *out);
+void nf_oracle_dequant_q8_0_f32(const uint8_t *blocks, uint64_t count, float *out);
+void nf_oracle_dequant_q4_0_f16(const uint8_t *blocks, uint64_t count, uint16_t *out);
+void nf_oracle_dequant_q8_0_f16(const uint8_t *blocks, uint64_t count, uint16_t *out);
+
+/* C[M,N] = A[M,K] * B[N,K]^T, fp32 accumulation in k order. */
+void nf_oracle_linear_f32(const float *A, const float *B, float *C,
+                          uint32_t M, uint32_t N, uint32_t K);
+/* f16 A and B, fp32 accumulation of exact products, C rounded to fp16. */
+void nf_oracle_linear_f16(const uint16_t *A, const uint16_t *B, uint16_t *C,
+                          uint32_t M, uint32_t N, uint32_t K);
+
+/* Fused dequant + linear over the output columns n in [n0, n1); the other
+ * columns of C are left untouched.  qfmt is NF_ORACLE_Q4_0 / NF_ORACLE_Q8_0.
+ * threads > 1 partitions the columns across pthreads (same arithmetic). */
+void nf_oracle_fused_f32(const float *A, const uint8_t *W, int qfmt, float *C,
+                         uint32_t M, uint32_t N, uint32_t K,
+                         uint32_t n0, uint32_t n1, uint32_t threads);
+void nf_oracle_fused_f16(const uint16_t *A, const uint8_t *W, int qfmt, uint16_t *C,
+                         uint32_t M, uint32_t N, uint32_t K,
+                         uint32_t n0, uint32_t n1, uint32_t threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

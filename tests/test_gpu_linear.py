@@ -1,0 +1,225 @@
+"""Fused dequant+linear and dense linear parity on the GPU, through the C ABI.
+
+Every case compares the HIP result with the CPU oracle (the restated
+reference dequant + sequential-k loop) on identical seeded inputs, within
+max relative error 1e-3 (mixed and normwise, tests/helpers.py).  Shapes:
+the reference's own fused cases (fused_matmul_test.cpp:294-297), its
+linear_tiled case (dequant_test.cpp:300-394), decode edge cases (M=1,
+N not a multiple of any tile, ragged K), config shapes, and both sides of the
+GEMV/MFMA switch.  Config-sized prefill shapes are checked on a sample of
+output columns (the oracle computes only those), which is exact for the
+sampled entries.
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_close
+from neurofabric_amd import abi
+from neurofabric_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+QDT = {"q4_0": abi.NF_DTYPE_Q4_0, "q8_0": abi.NF_DTYPE_Q8_0}
+
+
+def run_fused(provider, fmt, A, W, M, N, K, f16):
+    op = f"dequant_{fmt}_linear" + ("_f16" if f16 else "")
+    a = provider.alloc_array(A, abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32)
+    w = provider.alloc_array(W, QDT[fmt])
+    c = provider.alloc(abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32, M * N * (2 if f16 else 4))
+    provider.dispatch(op, [a, w], [c], M, N, K)
+    provider.synchronize()
+    got = c.download(np.float16 if f16 else np.float32).reshape(M, N)
+    for b in (a, w, c):
+        b.release()
+    return got
+
+
+def check_fused(provider, oracle_mod, fmt, M, N, K, f16, seed=0, cols=None, threads=8):
+    W = syn.weights(fmt, N, K, seed=seed)
+    A = syn.activations(M, K, seed=seed + 1, dtype=np.float16 if f16 else np.float32)
+    got = run_fused(provider, fmt, A, W, M, N, K, f16)
+    ref = oracle_mod.fused(A, W, fmt, M, N, K, f16=f16, cols=cols, threads=threads)
+    if f16:
+        ref = ref.view(np.float16)
+    if cols:
+        got, ref = got[:, cols[0]:cols[1]], ref[:, cols[0]:cols[1]]
+    return assert_close(got.astype(np.float32), ref.astype(np.float32), what=f"{fmt} f16={f16} {M}x{N}x{K}")
+
+
+SMALL = [(4, 8, 32), (5, 7, 64), (64, 128, 256), (1, 1, 32), (1, 3, 64), (2, 100, 96), (3, 257, 128),
+         (9, 33, 160), (16, 64, 512), (17, 31, 64), (1, 4096, 64)]
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("shape", SMALL, ids=lambda s: "x".join(map(str, s)))
+def test_fused_small_shapes(provider, oracle_mod, fmt, f16, shape):
+    check_fused(provider, oracle_mod, fmt, *shape, f16=f16, seed=sum(shape))
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("shape", [(2, 5, 48), (3, 9, 80), (1, 7, 33)], ids=lambda s: "x".join(map(str, s)))
+def test_fused_ragged_k_flat_indexing(provider, oracle_mod, fmt, f16, shape):
+    M, N, K = shape
+    nblk = (N * K + 31) // 32
+    W = syn.weights(fmt, 1, nblk * 32, seed=K)
+    A = syn.activations(M, K, seed=N, dtype=np.float16 if f16 else np.float32)
+    got = run_fused(provider, fmt, A, W, M, N, K, f16)
+    ref = oracle_mod.fused(A, W, fmt, M, N, K, f16=f16)
+    ref = ref.view(np.float16) if f16 else ref
+    assert_close(got.astype(np.float32), ref.astype(np.float32), what=f"ragged {shape}")
+
+
+def test_config0_gemv_full(provider, oracle_mod):
+    """C0: x[1,2048] f32, W Q4_0 [5632,2048] -> y[1,5632], whole output."""
+    check_fused(provider, oracle_mod, "q4_0", 1, 5632, 2048, f16=False, seed=0)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("NK", [(256, 2048), (2048, 5632), (32000, 2048)], ids=["kv", "down", "lm_head"])
+def test_config1_tinyllama_shapes(provider, oracle_mod, M, NK):
+    N, K = NK
+    cols = None if N * M <= 64 * 2048 else (N // 2 - 512, N // 2 + 512)
+    check_fused(provider, oracle_mod, "q4_0", M, N, K, f16=False, seed=N + M, cols=cols)
+
+
+@pytest.mark.parametrize("M", [1, 8, 64])
+def test_config3_q8_0_decode(provider, oracle_mod, M):
+    check_fused(provider, oracle_mod, "q8_0", M, 1024, 4096, f16=False, seed=M)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (512, 11008, 4096), (512, 4096, 11008)])
+def test_config2_prefill_sampled_columns(provider, oracle_mod, M, N, K):
+    check_fused(provider, oracle_mod, "q4_0", M, N, K, f16=True, seed=K, cols=(N - 256, N), threads=8)
+
+
+@pytest.mark.parametrize("f16", [True], ids=["f16"])
+def test_gemv_and_mfma_paths_agree(provider, oracle_mod, f16):
+    """The same input through the skinny and the MFMA kernel (switch point
+    forced both ways) agrees with the oracle."""
+    M, N, K = 24, 384, 1024
+    old = provider.get_gemv_max_m()
+    try:
+        outs = []
+        for max_m in (1 << 30, 1):
+            provider.set_gemv_max_m(max_m if not f16 else old[0], max_m if f16 else old[1])
+            W = syn.q4_0_weights(N, K, seed=3)
+            A = syn.activations(M, K, seed=4, dtype=np.float16 if f16 else np.float32)
+            outs.append(run_fused(provider, "q4_0", A, W, M, N, K, f16).astype(np.float32))
+        ref = oracle_mod.fused(A, W, "q4_0", M, N, K, f16=f16)
+        ref = (ref.view(np.float16) if f16 else ref).astype(np.float32)
+        for o in outs:
+            assert_close(o, ref)
+    finally:
+        provider.set_gemv_max_m(*old)
+
+
+# ---- the reference's fused-vs-separate test (fused_matmul_test.cpp:134-285) ----------
+
+def _quantize_like_reference_test(src, oracle_mod):
+    """Test-only quantizer of fused_matmul_test.cpp:87-104: d = amax/7 encoded
+    with the truncating encoder, codes round(x/d)+8 clamped to 0..15."""
+    blocks = src.reshape(-1, 32)
+    out = []
+    for b in blocks:
+        amax = float(np.max(np.abs(b)))
+        d = np.float32(amax / 7.0)
+        dh = oracle_mod.f32_to_f16_trunc(float(d))
+        df = float(np.array([dh], np.uint16).view(np.float16)[0])
+        inv = 1.0 / df if df != 0.0 else 0.0
+        codes = np.clip(np.round(b.astype(np.float32) * np.float32(inv)).astype(np.int64) + 8, 0, 15)
+        out.append(syn.pack_q4_0(np.array([dh], np.uint16).view(np.float16), codes[None, :]))
+    return np.concatenate(out).reshape(-1)
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 8, 32), (5, 7, 64), (64, 128, 256)])
+def test_reference_fused_vs_separate_f32(provider, oracle_mod, M, N, K):
+    rng = np.random.default_rng(42)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    kn = K * N
+    kn_pad = (kn + 31) // 32 * 32
+    bsrc = np.zeros(kn_pad, np.float32)
+    bsrc[:kn] = rng.uniform(-1, 1, kn)
+    Wq = _quantize_like_reference_test(bsrc, oracle_mod)
+    a = provider.alloc_array(A, abi.NF_DTYPE_F32)
+    w = provider.alloc_array(Wq, abi.NF_DTYPE_Q4_0)
+    dq = provider.alloc(abi.NF_DTYPE_F32, kn_pad * 4)
+    sep = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    fused = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    provider.check(provider.dispatch_bare("dequant_q4_0", [w], [dq]), "dequant")
+    provider.synchronize()
+    provider.dispatch("linear_tiled", [a, dq], [sep], M, N, K)
+    provider.dispatch("dequant_q4_0_linear", [a, w], [fused], M, N, K)
+    provider.synchronize()
+    s, f = sep.download(np.float32), fused.download(np.float32)
+    assert np.max(np.abs(s - f)) < 1e-3  # the reference's own criterion
+    ref = oracle_mod.fused(A, Wq, "q4_0", M, N, K)
+    assert_close(f.reshape(M, N), ref)
+    for b in (a, w, dq, sep, fused):
+        b.release()
+
+
+def test_reference_fused_vs_separate_f16(provider, oracle_mod):
+    M, N, K = 64, 128, 256
+    rng = np.random.default_rng(99)
+    A32 = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    A16 = np.array([oracle_mod.f32_to_f16_trunc(float(v)) for v in A32.reshape(-1)], np.uint16)
+    bsrc = rng.uniform(-1, 1, K * N).astype(np.float32)
+    Wq = _quantize_like_reference_test(bsrc, oracle_mod)
+    a = provider.alloc_array(A16, abi.NF_DTYPE_F16)
+    w = provider.alloc_array(Wq, abi.NF_DTYPE_Q4_0)
+    dq = provider.alloc(abi.NF_DTYPE_F16, K * N * 2)
+    sep = provider.alloc(abi.NF_DTYPE_F16, M * N * 2)
+    fused = provider.alloc(abi.NF_DTYPE_F16, M * N * 2)
+    provider.check(provider.dispatch_bare("dequant_q4_0_f16", [w], [dq]), "dequant_f16")
+    provider.synchronize()
+    provider.dispatch("linear", [a, dq], [sep], M, N, K)
+    provider.dispatch("dequant_q4_0_linear_f16", [a, w], [fused], M, N, K)
+    provider.synchronize()
+    s = sep.download(np.float16).astype(np.float32)
+    f = fused.download(np.float16).astype(np.float32)
+    assert np.max(np.abs(s - f)) < 0.1  # the reference's own criterion
+    ref = oracle_mod.fused(A16, Wq, "q4_0", M, N, K, f16=True).view(np.float16).astype(np.float32)
+    assert_close(f.reshape(M, N), ref)
+    for b in (a, w, dq, sep, fused):
+        b.release()
+
+
+# ---- dense linear ---------------------------------------------------------------------
+
+def test_dense_linear_tiled_reference_case(provider, oracle_mod):
+    """dequant_test.cpp:300-394: A 64x32, B 48x32 (transposed), f32."""
+    M, N, K = 64, 48, 32
+    A = ((np.arange(M * K) % 17) * np.float32(0.1) - np.float32(0.8)).astype(np.float32).reshape(M, K)
+    Bl = ((np.arange(K * N) % 13) * np.float32(0.15) - np.float32(0.9)).astype(np.float32).reshape(K, N)
+    B = np.ascontiguousarray(Bl.T)
+    a, b = provider.alloc_array(A, abi.NF_DTYPE_F32), provider.alloc_array(B, abi.NF_DTYPE_F32)
+    c = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    provider.dispatch("linear_tiled", [a, b], [c], M, N, K)
+    got = c.download(np.float32).reshape(M, N)
+    assert_close(got, oracle_mod.linear_f32(A, B, M, N, K))
+    for x in (a, b, c):
+        x.release()
+
+
+@pytest.mark.parametrize("adt,bdt,cdt", [("f16", "f16", "f16"), ("f16", "f16", "f32"), ("f32", "f32", "f32"),
+                                         ("f32", "f16", "f32")])
+def test_dense_linear_dtype_mixes(provider, oracle_mod, adt, bdt, cdt):
+    M, N, K = 33, 70, 96
+    rng = np.random.default_rng(7)
+    np_t = {"f16": np.float16, "f32": np.float32}
+    nf_t = {"f16": abi.NF_DTYPE_F16, "f32": abi.NF_DTYPE_F32}
+    A = rng.standard_normal((M, K)).astype(np_t[adt])
+    B = rng.standard_normal((N, K)).astype(np_t[bdt])
+    a, b = provider.alloc_array(A, nf_t[adt]), provider.alloc_array(B, nf_t[bdt])
+    c = provider.alloc(nf_t[cdt], M * N * (2 if cdt == "f16" else 4))
+    provider.dispatch("linear", [a, b], [c], M, N, K)
+    got = c.download(np_t[cdt]).reshape(M, N).astype(np.float32)
+    ref = oracle_mod.linear_f32(A.astype(np.float32), B.astype(np.float32), M, N, K)
+    if cdt == "f16":
+        ref = ref.astype(np.float16).astype(np.float32)
+    assert_close(got, ref)
+    for x in (a, b, c):
+        x.release()

@@ -1,0 +1,50 @@
+"""The reference's own driver test, compiled from its source by
+oracle/Makefile (`make -C oracle ref`) and linked against this provider,
+plus the register -> init -> shutdown lifecycle repeated in one process
+(cuda_stub_test.cpp:33-140 pattern).  Both run in child processes so the
+session provider of the other GPU tests is untouched."""
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+REPO = Path(__file__).resolve().parents[1]
+REF_DEQUANT = REPO / "oracle" / "_ref" / "dequant_test"
+
+
+@pytest.mark.skipif(not REF_DEQUANT.exists(), reason="reference test binary not built (needs the reference sources)")
+def test_reference_dequant_test_binary_passes():
+    """tests/driver/dequant_test.cpp: Q4_0/Q8_0 dequant vs its CPU reference,
+    linear_tiled 64x48x32 and dequant->linear through PipelineEngine."""
+    r = subprocess.run([str(REF_DEQUANT)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0
+    assert "OK: all Phase 17 dequant tests passed" in r.stdout
+
+
+LIFECYCLE = r"""
+import sys
+sys.path.insert(0, %r)
+from neurofabric_amd.plugin import Provider
+from neurofabric_amd import abi
+import numpy as np
+for i in range(3):
+    p = Provider()
+    p.init()
+    assert p.name == "amd_hip" and p.abi_version == abi.NF_ABI_VERSION
+    b = p.alloc(abi.NF_DTYPE_U8, 256)
+    b.upload(np.full(256, 0x42, np.uint8))
+    assert (b.download(np.uint8) == 0x42).all()
+    b.release()
+    p.shutdown()
+    p.shutdown()  # idempotent
+print("lifecycle ok")
+"""
+
+
+def test_register_init_shutdown_repeated():
+    r = subprocess.run([sys.executable, "-c", LIFECYCLE % str(REPO)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "lifecycle ok" in r.stdout

@@ -1,0 +1,194 @@
+"""Host-side boundary tests that need no GPU.
+
+The provider library loads, exports exactly the entry points its headers
+declare, fills the vtables, reports the ABI version the loader gates on
+(plugin_loader.cpp:48-54), and its planner (shared with dispatch) applies the
+reference's selection rules and this provider's size/dtype validation.
+"""
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from neurofabric_amd import abi
+from neurofabric_amd.plugin import NfError, Provider, load_library, plan, push_constants
+
+REPO = Path(__file__).resolve().parents[1]
+LIB = REPO / "neurofabric_amd" / "_lib" / "libnf_plugin_hip.so"
+
+
+def _declared_symbols():
+    names = set()
+    for h in (REPO / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        text = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("#"))
+        for m in re.finditer(r"NF_API\s+[\w\s\*]*?\b(\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return load_library()
+
+
+def test_exports_match_headers():
+    declared = _declared_symbols()
+    assert {"nf_plugin_register", "nf_plugin_register_mem", "nf_plugin_register_ddi"} <= declared
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], check=True, capture_output=True,
+                         text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert exported == declared
+
+
+def test_every_declared_symbol_resolves(lib):
+    for name in _declared_symbols():
+        assert getattr(lib, name) is not None
+
+
+def test_register_fills_vtables():
+    prov = Provider()
+    for f, _ in abi.nf_provider_vtable._fields_:
+        assert C.cast(getattr(prov.vt, f), C.c_void_p).value, f
+    for f, _ in abi.nf_provider_mem_vtable._fields_:
+        assert C.cast(getattr(prov.mem, f), C.c_void_p).value, f
+    for f, _ in abi.nf_ddi_vtable._fields_:
+        assert C.cast(getattr(prov.ddi, f), C.c_void_p).value, f
+    assert prov.name == "amd_hip"
+    assert prov.abi_version == abi.NF_ABI_VERSION
+    assert Provider().handle.value == prov.handle.value  # process-wide singleton
+
+
+def test_unknown_op_is_unsupported_before_any_device_work():
+    prov = Provider()
+    st = prov.vt.dispatch(prov.handle, b"no_such_op", None, 0, None, 0)
+    assert st == abi.NF_ERROR_UNSUPPORTED_OP
+    assert "no_such_op" in prov.last_error()
+
+
+def _gpu_count():
+    try:
+        import torch
+        return torch.cuda.device_count()
+    except Exception:
+        return 0
+
+
+@pytest.mark.skipif(_gpu_count() > 0, reason="checks the no-device error path")
+def test_init_without_device_reports_device_lost():
+    prov = Provider()
+    with pytest.raises(NfError) as e:
+        prov.init()
+    assert e.value.status == abi.NF_ERROR_DEVICE_LOST
+    with pytest.raises(NfError) as e2:
+        prov.alloc(abi.NF_DTYPE_F32, 64)
+    assert e2.value.status == abi.NF_ERROR_INVALID_ARG
+
+
+# ---- planner: selection and validation ------------------------------------------------
+
+D = abi.make_desc
+
+
+def _fused(lib, M, N, K, a=abi.NF_DTYPE_F32, c=abi.NF_DTYPE_F32, w_bytes=None, op="dequant_q4_0_linear",
+           pc=None, bs=18):
+    w = w_bytes if w_bytes is not None else N * K // 32 * bs
+    ea = 2 if a == abi.NF_DTYPE_F16 else 4
+    ec = 2 if c == abi.NF_DTYPE_F16 else 4
+    return plan(lib, op, [D(a, M * K * ea), D(abi.NF_DTYPE_Q4_0, w)], [D(c, M * N * ec)], M, N, K, pc)
+
+
+def test_plan_decode_gemv_c0(lib):
+    p = _fused(lib, 1, 5632, 2048)
+    assert p["kernel"] == "gemv_q4_0_f32"
+    assert (p["weight_bytes"], p["act_bytes"], p["out_bytes"]) == (6488064, 8192, 22528)
+    assert p["flops"] == 2 * 5632 * 2048
+
+
+def test_plan_prefill_uses_mfma(lib):
+    p = _fused(lib, 512, 4096, 4096, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
+    assert p["kernel"] == "gemm_mfma_q4_0_f16"
+    assert p["flops"] == 2 * 512 * 4096 * 4096
+
+
+def test_plan_path_follows_output_dtype(lib):
+    # metal_provider.mm:2997 — the op-name suffix does not pick the path.
+    assert _fused(lib, 2, 64, 64, op="dequant_q4_0_linear_f16")["kernel"] == "gemv_q4_0_f32"
+    assert _fused(lib, 2, 64, 64, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)["kernel"] == "gemv_q4_0_f16"
+
+
+def test_plan_q8_0_and_ragged_k(lib):
+    p = plan(lib, "dequant_q8_0_linear", [D(abi.NF_DTYPE_F32, 4 * 64 * 4), D(abi.NF_DTYPE_Q8_0, 7 * 2 * 34)],
+             [D(abi.NF_DTYPE_F32, 4 * 7 * 4)], 4, 7, 64)
+    assert p["kernel"] == "gemv_q8_0_f32" and p["weight_bytes"] == 7 * 2 * 34
+    p = _fused(lib, 2, 5, 48, w_bytes=(5 * 48 + 31) // 32 * 18)
+    assert p["kernel"] == "generic_q4_0_f32"
+
+
+@pytest.mark.parametrize("case", ["no_pc", "zero_m", "short_w", "short_a", "short_c", "a_dtype", "c_dtype"])
+def test_plan_rejects_bad_arguments(lib, case):
+    M, N, K = 4, 8, 64
+    kw = {}
+    if case == "no_pc":
+        with pytest.raises(NfError) as e:
+            plan(lib, "dequant_q4_0_linear", [D(0, M * K * 4), D(6, N * K // 32 * 18)], [D(0, M * N * 4)])
+        assert e.value.status == abi.NF_ERROR_INVALID_ARG
+        return
+    if case == "zero_m":
+        kw["pc"] = push_constants(0, N, K)
+    if case == "short_w":
+        kw["w_bytes"] = N * K // 32 * 18 - 1
+    with pytest.raises(NfError) as e:
+        if case == "short_a":
+            plan(lib, "dequant_q4_0_linear", [D(0, M * K * 4 - 4), D(6, N * K // 32 * 18)], [D(0, M * N * 4)], M, N, K)
+        elif case == "short_c":
+            plan(lib, "dequant_q4_0_linear", [D(0, M * K * 4), D(6, N * K // 32 * 18)], [D(0, M * N * 4 - 1)], M, N, K)
+        elif case == "a_dtype":
+            _fused(lib, M, N, K, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F32)
+        elif case == "c_dtype":
+            plan(lib, "dequant_q4_0_linear", [D(0, M * K * 4), D(6, N * K // 32 * 18)], [D(abi.NF_DTYPE_I32, M * N * 4)], M, N, K)
+        else:
+            _fused(lib, M, N, K, **kw)
+    assert e.value.status == abi.NF_ERROR_INVALID_ARG
+
+
+def test_plan_dequant_count_from_output_size(lib):
+    # metal_provider.mm:2667 — count = out.size_bytes / element size
+    p = plan(lib, "dequant_q4_0", [D(abi.NF_DTYPE_Q4_0, 8 * 18)], [D(abi.NF_DTYPE_F32, 256 * 4)])
+    assert (p["kernel"], p["count"]) == ("dequant_q4_0_f32", 256)
+    p = plan(lib, "dequant_q8_0_f16", [D(abi.NF_DTYPE_Q8_0, 3 * 34)], [D(abi.NF_DTYPE_F16, 70 * 2)])
+    assert (p["kernel"], p["count"], p["weight_bytes"]) == ("dequant_q8_0_f16", 70, 3 * 34)
+    with pytest.raises(NfError):
+        plan(lib, "dequant_q4_0", [D(abi.NF_DTYPE_Q4_0, 7 * 18)], [D(abi.NF_DTYPE_F32, 256 * 4)])
+
+
+def test_plan_dense_linear_dtypes(lib):
+    M, N, K = 3, 5, 16
+    p = plan(lib, "linear", [D(abi.NF_DTYPE_F16, M * K * 2), D(abi.NF_DTYPE_F16, N * K * 2)],
+             [D(abi.NF_DTYPE_F32, M * N * 4)], M, N, K)
+    assert p["kernel"] == "linear_f16f16_f32"
+    p = plan(lib, "linear_tiled", [D(abi.NF_DTYPE_F32, M * K * 4), D(abi.NF_DTYPE_U8, N * K * 4)],
+             [D(abi.NF_DTYPE_F32, M * N * 4)], M, N, K)
+    assert p["kernel"] == "linear_f32f32_f32"  # untyped B takes A's element type
+
+
+def test_plan_unknown_op(lib):
+    with pytest.raises(NfError) as e:
+        plan(lib, "rms_norm", [D(0, 4)], [D(0, 4)])
+    assert e.value.status == abi.NF_ERROR_UNSUPPORTED_OP
+
+
+def test_crossover_setter_roundtrip():
+    prov = Provider()
+    old = prov.get_gemv_max_m()
+    try:
+        prov.set_gemv_max_m(3, 5)
+        assert prov.get_gemv_max_m() == (3, 5)
+        p = _fused(prov.lib, 4, 64, 64, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)
+        assert p["kernel"] == "gemv_q4_0_f16"
+        p = _fused(prov.lib, 6, 64, 64, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)
+        assert p["kernel"] == "gemm_mfma_q4_0_f16"
+    finally:
+        prov.set_gemv_max_m(*old)
