@@ -41,6 +41,11 @@ NF_DTYPE_Q8_0 = 7
 NF_MEM_DOMAIN_CPU = 0
 NF_MEM_DOMAIN_UNIFIED = 1
 NF_MEM_DOMAIN_DEVICE = 2
+NF_MEM_DOMAIN_DMA_BUF = 3
+NF_MEM_DOMAIN_EXTERNAL = 4
+NF_MEM_DOMAIN_MMAP = 5
+NF_MEM_DOMAIN_CXL = 6
+NF_MEM_DOMAIN_CXL_SHARED = 7
 
 NF_CACHE_FLUSH = 0x01
 NF_CACHE_INVALIDATE = 0x02
