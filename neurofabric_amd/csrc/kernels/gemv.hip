@@ -1,16 +1,410 @@
 // gemv.hip — decode-shaped fused dequant + matmul (small M).
 //
-// C[m, n] = sum_k A[m, k] * deq(W)[n, k] with fp32 accumulation; the f16
-// path rounds each dequantized weight to fp16 first and rounds C to fp16
-// (metal_provider.mm:1396-1468).  HBM-bound: every weight byte is read once.
+// C[m, n] = sum_k A[m, k] * deq(W)[n, k], fp32 accumulation.  f32 path:
+// exact f32 weights d*q; f16 path: each weight rounded to fp16 first,
+// RNE(d*q), f16 activations, C rounded to fp16 (metal_provider.mm:1396-1468).
+// Reassociation is allowed (block scales are factored out of each block's
+// partial sum); dequantized values are never approximated.
 //
-// Work split: one wavefront per output row n; its 64 lanes stride over the
-// row's 32-element blocks; a CTA of 4 waves covers 4 rows and MT activation
-// rows (grid.y tiles M).  Partial sums are combined with a wave reduction.
+// The kernel is HBM-bound: every weight byte is read exactly once.
+//
+// Pair kernel (K % 64 == 0):
+//   * A "pair" is two consecutive blocks = 64 elements: 36 B of Q4_0
+//     (9 dwords) or 68 B of Q8_0 (17 dwords).  Row strides are multiples of
+//     the pair size, so every pair starts on a 4-byte boundary and one lane
+//     fetches it with dword-aligned dwordx4 loads (2 x16 + 1 x4 for Q4_0,
+//     4 x16 + 1 x4 for Q8_0).  Consecutive lanes read consecutive pairs, so
+//     a wave's loads cover one contiguous span of the row.
+//   * The first block of a pair starts 2 bytes into the pair: its code
+//     dwords are realigned with v_alignbyte; the second block's codes are
+//     already dword aligned.
+//   * The activations (M rows of K) are staged once per workgroup in LDS,
+//     64-element pair by pair, with the 16-byte chunks of a pair XOR-
+//     swizzled by the pair index so the 16 lanes of a ds_read_b128 phase hit
+//     16 different bank groups.
+//   * A row is covered by a group of L lanes (L = 16, 32 or 64, chosen on the
+//     host so the pairs of a row spread evenly); a wave holds 64/L groups and
+//     each group works on R2 rows at once, reading each activation chunk
+//     from LDS once for all R2 rows.  The next pair's weights are loaded
+//     before the current pair is computed.
+//   * Partial sums are reduced across the L lanes of a group with xor
+//     shuffles; lane 0 of the group writes the R2 x M outputs.
+//
+// Unpacking (per 32-bit word of codes = 8 Q4_0 codes / 4 Q8_0 codes):
+//   f32, Q4_0: low and high nibbles are masked into bytes 0..15; bytes 0..15
+//       read as OCP/FNUZ fp8 e4m3 are exactly n * u (u = 2^-9 or 2^-10, the
+//       value of byte 0x01, measured in-kernel), so v_cvt_pk_f32_fp8 turns two
+//       codes into two exact floats per instruction.  The "-8" offset is
+//       applied once per block: sum (n-8) x = (sum n*u*x - 8*u*sum x) / u,
+//       with sum x per block precomputed during staging.
+//   f32, Q8_0: v_cvt_f32_i32 with SDWA byte select and sign extension.
+//   f16: bytes are placed under 0x64 (fp16 1024 + n), shifted to the signed
+//       code with one packed f16 add (exact), and multiplied by the fp16 scale
+//       with one packed f16 multiply — RNE(d*q), the same bits as
+//       dequant_*_f16 — then v_dot2c_f32_f16 accumulates in fp32.
+//
+// Block kernel (fallback for K % 64 == 32): one wave per output row, lanes
+// stride over the row's 32-element blocks.
 #include "../launch.hpp"
 #include "common.hpp"
 
 namespace nfk {
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+
+template <class QF> struct PairFmt;
+template <> struct PairFmt<Q4_0> {
+  static constexpr int kBytes = 36, kDwords = 9, kQd = 4;  // kQd: code dwords per block
+};
+template <> struct PairFmt<Q8_0> {
+  static constexpr int kBytes = 68, kDwords = 17, kQd = 8;
+};
+
+template <class QF>
+__device__ __forceinline__ void load_pair(const uint8_t* p, uint32_t (&w)[PairFmt<QF>::kDwords]) {
+  const u32x4a4* v = reinterpret_cast<const u32x4a4*>(p);
+#pragma unroll
+  for (int i = 0; i < PairFmt<QF>::kDwords / 4; ++i) {
+    const u32x4 t = v[i];
+    w[4 * i + 0] = t.x;
+    w[4 * i + 1] = t.y;
+    w[4 * i + 2] = t.z;
+    w[4 * i + 3] = t.w;
+  }
+  w[PairFmt<QF>::kDwords - 1] = reinterpret_cast<const uint32_t*>(p)[PairFmt<QF>::kDwords - 1];
+}
+
+// Code dword t of block `blk` (0 or 1) of a loaded pair, and its fp16 scale bits.
+template <class QF>
+__device__ __forceinline__ uint32_t code_dword(const uint32_t* w, int blk, int t) {
+  constexpr int qd = PairFmt<QF>::kQd;
+  // block 0: codes start at byte 2 of the pair (realigned from two dwords);
+  // block 1: scale in the upper half of dword qd, codes in dwords qd+1...
+  if (blk == 0) return __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2);
+  return w[qd + 1 + t];
+}
+
+template <class QF>
+__device__ __forceinline__ uint32_t scale_bits(const uint32_t* w, int blk) {
+  constexpr int qd = PairFmt<QF>::kQd;
+  return blk == 0 ? (w[0] & 0xFFFFu) : (w[qd] >> 16);
+}
+
+// ---- LDS activation layout ------------------------------------------------
+// f32: 16 chunks of 4 floats per pair; f16: 8 chunks of 8 halves per pair.
+template <typename XT> struct XChunk;
+template <> struct XChunk<float> {
+  typedef float4v T;
+  static constexpr int kPerPair = 16, kElems = 4;
+};
+template <> struct XChunk<half_t> {
+  typedef half8 T;
+  static constexpr int kPerPair = 8, kElems = 8;
+};
+
+template <typename XT>
+__device__ __forceinline__ int xslot(int m, int P, int pair, int c) {
+  constexpr int cp = XChunk<XT>::kPerPair;
+  return (m * P + pair) * cp + (c ^ (pair & (cp - 1)));
+}
+
+// ---- per-pair compute -----------------------------------------------------
+
+// f32 activations, Q4_0.
+template <int R2, int MM>
+__device__ __forceinline__ void pair_f32_q4(const uint32_t (&w)[R2][9], const float4v* __restrict__ xs,
+                                            const float* __restrict__ sxs, int P, int pair,
+                                            float inv_unit, float (&acc)[R2][MM]) {
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    float s[R2][MM];
+#pragma unroll
+    for (int j = 0; j < R2; ++j)
+#pragma unroll
+      for (int m = 0; m < MM; ++m) s[j][m] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float4v xl[MM], xh[MM];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        xl[m] = xs[xslot<float>(m, P, pair, blk * 8 + t)];
+        xh[m] = xs[xslot<float>(m, P, pair, blk * 8 + 4 + t)];
+      }
+#pragma unroll
+      for (int j = 0; j < R2; ++j) {
+        const uint32_t q = code_dword<Q4_0>(w[j], blk, t);
+        const uint32_t lo = q & 0x0F0F0F0Fu;
+        const uint32_t hi = (q >> 4) & 0x0F0F0F0Fu;
+        const float2v a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+        const float2v b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+        const float2v c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+        const float2v e = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+          float v = s[j][m];
+          v = __builtin_fmaf(a.x, xl[m].x, v);
+          v = __builtin_fmaf(a.y, xl[m].y, v);
+          v = __builtin_fmaf(b.x, xl[m].z, v);
+          v = __builtin_fmaf(b.y, xl[m].w, v);
+          v = __builtin_fmaf(c.x, xh[m].x, v);
+          v = __builtin_fmaf(c.y, xh[m].y, v);
+          v = __builtin_fmaf(e.x, xh[m].z, v);
+          v = __builtin_fmaf(e.y, xh[m].w, v);
+          s[j][m] = v;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < R2; ++j) {
+      const float d = h2f_bits((uint16_t)scale_bits<Q4_0>(w[j], blk)) * inv_unit;
+#pragma unroll
+      for (int m = 0; m < MM; ++m)
+        acc[j][m] = __builtin_fmaf(d, s[j][m] - sxs[(m * P + pair) * 2 + blk], acc[j][m]);
+    }
+  }
+}
+
+// f32 activations, Q8_0.
+template <int R2, int MM>
+__device__ __forceinline__ void pair_f32_q8(const uint32_t (&w)[R2][17], const float4v* __restrict__ xs,
+                                            int P, int pair, float (&acc)[R2][MM]) {
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    float s[R2][MM];
+#pragma unroll
+    for (int j = 0; j < R2; ++j)
+#pragma unroll
+      for (int m = 0; m < MM; ++m) s[j][m] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      float4v xv[MM];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) xv[m] = xs[xslot<float>(m, P, pair, blk * 8 + t)];
+#pragma unroll
+      for (int j = 0; j < R2; ++j) {
+        const uint32_t q = code_dword<Q8_0>(w[j], blk, t);
+        const float f0 = (float)(int8_t)(q);
+        const float f1 = (float)(int8_t)(q >> 8);
+        const float f2 = (float)(int8_t)(q >> 16);
+        const float f3 = (float)((int32_t)q >> 24);
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+          float v = s[j][m];
+          v = __builtin_fmaf(f0, xv[m].x, v);
+          v = __builtin_fmaf(f1, xv[m].y, v);
+          v = __builtin_fmaf(f2, xv[m].z, v);
+          v = __builtin_fmaf(f3, xv[m].w, v);
+          s[j][m] = v;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < R2; ++j) {
+      const float d = h2f_bits((uint16_t)scale_bits<Q8_0>(w[j], blk));
+#pragma unroll
+      for (int m = 0; m < MM; ++m) acc[j][m] = __builtin_fmaf(d, s[j][m], acc[j][m]);
+    }
+  }
+}
+
+__device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+__device__ __forceinline__ uint32_t as_u32(half2v h) { return __builtin_bit_cast(uint32_t, h); }
+
+// f16 activations (weights rounded to fp16 exactly as dequant_*_f16).
+template <class QF, int R2, int MM>
+__device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kDwords],
+                                         const half8* __restrict__ xs, int P, int pair,
+                                         float (&acc)[R2][MM]) {
+  constexpr bool kQ4 = PairFmt<QF>::kQd == 4;
+  constexpr int qd = PairFmt<QF>::kQd;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    half8 xv[MM][4];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xv[m][c] = xs[xslot<half_t>(m, P, pair, blk * 4 + c)];
+#pragma unroll
+    for (int j = 0; j < R2; ++j) {
+      const uint32_t db = scale_bits<QF>(w[j], blk);
+      const half2v d2 = as_h2(db | (db << 16));
+#pragma unroll
+      for (int t = 0; t < qd; ++t) {
+        const uint32_t q = code_dword<QF>(w[j], blk, t);
+        if constexpr (kQ4) {
+          // bytes 0..3 of q: low nibbles -> elements 4t..4t+3, high -> 16+4t..
+          const uint32_t lo = q & 0x0F0F0F0Fu;
+          const uint32_t hi = (q >> 4) & 0x0F0F0F0Fu;
+          const half2v off = {(half_t)-1032.f, (half_t)-1032.f};
+          const half2v w0 = (as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + off) * d2;
+          const half2v w1 = (as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + off) * d2;
+          const half2v w2 = (as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) + off) * d2;
+          const half2v w3 = (as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) + off) * d2;
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            // elements 4t..4t+3 live in chunk t/2, halves 4*(t&1)..; 16+4t.. in chunk 2+t/2
+            const half8 xl = xv[m][t >> 1];
+            const half8 xh = xv[m][2 + (t >> 1)];
+            const int o = (t & 1) * 4;
+            float v = acc[j][m];
+            v = __builtin_amdgcn_fdot2(w0, half2v{xl[o + 0], xl[o + 1]}, v, false);
+            v = __builtin_amdgcn_fdot2(w1, half2v{xl[o + 2], xl[o + 3]}, v, false);
+            v = __builtin_amdgcn_fdot2(w2, half2v{xh[o + 0], xh[o + 1]}, v, false);
+            v = __builtin_amdgcn_fdot2(w3, half2v{xh[o + 2], xh[o + 3]}, v, false);
+            acc[j][m] = v;
+          }
+        } else {
+          // Q8_0: 4 signed codes -> elements 4t..4t+3 (chunk t/2, halves 4*(t&1)..)
+          const uint32_t u = q ^ 0x80808080u;  // code + 128, unsigned
+          const half2v off = {(half_t)-1152.f, (half_t)-1152.f};
+          const half2v w0 = (as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + off) * d2;
+          const half2v w1 = (as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + off) * d2;
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            const half8 xc = xv[m][t >> 1];
+            const int o = (t & 1) * 4;
+            float v = acc[j][m];
+            v = __builtin_amdgcn_fdot2(w0, half2v{xc[o + 0], xc[o + 1]}, v, false);
+            v = __builtin_amdgcn_fdot2(w1, half2v{xc[o + 2], xc[o + 3]}, v, false);
+            acc[j][m] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---- the pair kernel ------------------------------------------------------
+
+template <class QF, typename XT, int R2, int MM>
+__global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A,
+                                                        const uint8_t* __restrict__ W,
+                                                        XT* __restrict__ C, int M, int N, int K,
+                                                        int log2L) {
+  constexpr bool kF32 = sizeof(XT) == 4;
+  constexpr bool kQ4 = PairFmt<QF>::kQd == 4;
+  constexpr bool kSx = kF32 && kQ4;  // block sums of x needed for the nibble offset
+  constexpr int CP = XChunk<XT>::kPerPair;
+  constexpr int EPC = XChunk<XT>::kElems;
+  typedef typename XChunk<XT>::T ChunkT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int P = K >> 6;
+  ChunkT* xs = reinterpret_cast<ChunkT*>(smem);
+  float* sxs = reinterpret_cast<float*>(smem + (size_t)MM * P * CP * 16);
+  const int tid = threadIdx.x;
+
+  // fp8 e4m3 value of byte 0x01 (the unit step of the nibble trick)
+  const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1u, false)[0];
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int L = 1 << log2L;
+  const int R = 64 >> log2L;
+  const int g = lane >> log2L, li = lane & (L - 1);
+  const int rows_per_pass = 4 * R * R2;
+  const int pass_stride = gridDim.x * rows_per_pass;
+  const size_t row_bytes = (size_t)P * PairFmt<QF>::kBytes;
+  constexpr int DW = PairFmt<QF>::kDwords;
+
+  // Weights of (row r0.., pair) into w; rows beyond N read as zero.
+  auto load = [&](int r0, int pair, uint32_t (&w)[R2][DW]) {
+#pragma unroll
+    for (int j = 0; j < R2; ++j) {
+      if (r0 + j < N) {
+        load_pair<QF>(W + (size_t)(r0 + j) * row_bytes + (size_t)pair * PairFmt<QF>::kBytes, w[j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < DW; ++i) w[j][i] = 0u;
+      }
+    }
+  };
+
+  // The first weights are requested before A is staged, so the two memory
+  // round trips overlap.
+  int base = blockIdx.x * rows_per_pass;
+  int row0 = base + (wave * R + g) * R2;
+  uint32_t wc[R2][DW];
+  if (base < N && li < P) load(row0, li, wc);
+
+  // ---- stage A into LDS (and the per-block sums of x) ----
+  const int total = MM * P * CP;
+  for (int c0 = 0; c0 < total; c0 += 256) {
+    const int ci = c0 + tid;
+    ChunkT v = {};
+    int m = 0, pair = 0, c = 0;
+    if (ci < total) {
+      m = ci / (P * CP);
+      const int r = ci - m * P * CP;
+      pair = r / CP;
+      c = r - pair * CP;
+      if (m < M) v = *reinterpret_cast<const ChunkT*>(A + (size_t)m * K + (size_t)pair * 64 + c * EPC);
+      xs[xslot<XT>(m, P, pair, c)] = v;
+    }
+    if constexpr (kSx) {
+      float s = v[0] + v[1] + v[2] + v[3];
+      s += __shfl_xor(s, 1, 64);
+      s += __shfl_xor(s, 2, 64);
+      s += __shfl_xor(s, 4, 64);
+      if ((tid & 7) == 0 && ci < total) sxs[(m * P + pair) * 2 + (c >> 3)] = s * (8.0f * unit);
+    }
+  }
+  __syncthreads();
+
+  const float inv_unit = 1.0f / unit;
+  for (; base < N; base += pass_stride, row0 += pass_stride) {
+    float acc[R2][MM];
+#pragma unroll
+    for (int j = 0; j < R2; ++j)
+#pragma unroll
+      for (int m = 0; m < MM; ++m) acc[j][m] = 0.f;
+
+    for (int pair = li; pair < P; pair += L) {
+      // Prefetch the next pair of this pass, or the first pair of the next pass.
+      uint32_t wn[R2][DW];
+      const bool more = pair + L < P;
+      const int nrow0 = more ? row0 : row0 + pass_stride;
+      const int npair = more ? pair + L : li;
+      const bool pf = more || base + pass_stride < N;
+      if (pf) load(nrow0, npair, wn);
+      if constexpr (kF32) {
+        if constexpr (kQ4) {
+          pair_f32_q4<R2, MM>(wc, reinterpret_cast<const float4v*>(xs), sxs, P, pair, inv_unit, acc);
+        } else {
+          pair_f32_q8<R2, MM>(wc, reinterpret_cast<const float4v*>(xs), P, pair, acc);
+        }
+      } else {
+        pair_f16<QF, R2, MM>(wc, reinterpret_cast<const half8*>(xs), P, pair, acc);
+      }
+      if (pf) {
+#pragma unroll
+        for (int j = 0; j < R2; ++j)
+#pragma unroll
+          for (int i = 0; i < DW; ++i) wc[j][i] = wn[j][i];
+      }
+    }
+    // reduce across the L lanes of the group
+#pragma unroll
+    for (int j = 0; j < R2; ++j)
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        float v = acc[j][m];
+        for (int off = L >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        acc[j][m] = v;
+      }
+    if (li == 0) {
+#pragma unroll
+      for (int j = 0; j < R2; ++j) {
+        if (row0 + j >= N) continue;
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+          if (m < M) C[(size_t)m * N + row0 + j] = (XT)acc[j][m];
+      }
+    }
+  }
+}
+
+// ---- block kernel (odd number of blocks per row) ----------------------------
 
 template <typename AT>
 __device__ __forceinline__ float dot32(const AT* __restrict__ x, const float w[32]);
@@ -44,9 +438,9 @@ __device__ __forceinline__ float dot32<half_t>(const half_t* __restrict__ x, con
 }
 
 template <class QF, typename AT, int MT>
-__global__ __launch_bounds__(256) void gemv_kernel(const AT* __restrict__ A,
-                                                   const uint8_t* __restrict__ W,
-                                                   AT* __restrict__ C, int M, int N, int K) {
+__global__ __launch_bounds__(256) void gemv_block_kernel(const AT* __restrict__ A,
+                                                         const uint8_t* __restrict__ W,
+                                                         AT* __restrict__ C, int M, int N, int K) {
   constexpr bool kHalfW = sizeof(AT) == 2;
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -79,21 +473,92 @@ __global__ __launch_bounds__(256) void gemv_kernel(const AT* __restrict__ A,
 }
 
 template <class QF, typename AT>
-hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N,
-                         uint32_t K, hipStream_t s) {
+hipError_t gemv_block_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N,
+                               uint32_t K, hipStream_t s) {
   const dim3 block(256);
   const int mt = M == 1 ? 1 : (M == 2 ? 2 : (M <= 4 ? 4 : 8));
   const dim3 grid((N + 3) / 4, (M + mt - 1) / mt);
+  if (grid.y > 65535) return hipErrorInvalidConfiguration;
   const AT* a = static_cast<const AT*>(A);
   const uint8_t* w = static_cast<const uint8_t*>(W);
   AT* c = static_cast<AT*>(C);
   switch (mt) {
-    case 1: gemv_kernel<QF, AT, 1><<<grid, block, 0, s>>>(a, w, c, M, N, K); break;
-    case 2: gemv_kernel<QF, AT, 2><<<grid, block, 0, s>>>(a, w, c, M, N, K); break;
-    case 4: gemv_kernel<QF, AT, 4><<<grid, block, 0, s>>>(a, w, c, M, N, K); break;
-    default: gemv_kernel<QF, AT, 8><<<grid, block, 0, s>>>(a, w, c, M, N, K); break;
+    case 1: gemv_block_kernel<QF, AT, 1><<<grid, block, 0, s>>>(a, w, c, M, N, K); break;
+    case 2: gemv_block_kernel<QF, AT, 2><<<grid, block, 0, s>>>(a, w, c, M, N, K); break;
+    case 4: gemv_block_kernel<QF, AT, 4><<<grid, block, 0, s>>>(a, w, c, M, N, K); break;
+    default: gemv_block_kernel<QF, AT, 8><<<grid, block, 0, s>>>(a, w, c, M, N, K); break;
   }
   return hipGetLastError();
+}
+
+// Host-side geometry of the pair kernel.
+struct PairGeom {
+  int log2L = 5, R2 = 1, MM = 1;
+  unsigned grid = 1;
+  size_t lds = 0;
+};
+
+// Lanes per row: the largest of 64/32/16 whose round-robin split of the P
+// pairs keeps >= 95% of the lanes busy, else the best split.
+inline int pick_log2L(int P) {
+  int best = 6;
+  double best_u = 0.0;
+  for (int lg = 6; lg >= 4; --lg) {
+    const int L = 1 << lg;
+    const int it = (P + L - 1) / L;
+    const double u = (double)P / (double)(L * it);
+    if (u >= 0.95) return lg;
+    if (u > best_u + 1e-9) {
+      best_u = u;
+      best = lg;
+    }
+  }
+  return best;
+}
+
+template <class QF, typename XT, int R2, int MM>
+hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const void* W, void* C, uint32_t M,
+                            uint32_t N, uint32_t K, hipStream_t s) {
+  gemv_pair_kernel<QF, XT, R2, MM><<<dim3(g.grid), dim3(256), g.lds, s>>>(
+      static_cast<const XT*>(A), static_cast<const uint8_t*>(W), static_cast<XT*>(C), (int)M, (int)N,
+      (int)K, g.log2L);
+  return hipGetLastError();
+}
+
+template <class QF, typename XT>
+hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
+                         hipStream_t s) {
+  constexpr bool kF32 = sizeof(XT) == 4;
+  const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
+  if (K % 64 != 0 || M > 4 || !aligned) return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
+  PairGeom g;
+  const int P = (int)(K / 64);
+  g.MM = M == 1 ? 1 : (M == 2 ? 2 : 4);
+  const size_t xbytes = (size_t)g.MM * P * 64 * (kF32 ? 4 : 2);
+  const size_t sxbytes = (kF32 && PairFmt<QF>::kQd == 4) ? (size_t)g.MM * P * 2 * 4 : 0;
+  g.lds = xbytes + sxbytes;
+  if (g.lds > 64 * 1024) return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
+  g.log2L = pick_log2L(P);
+  const int R = 64 >> g.log2L;
+  // Two rows per lane group when that still leaves >= 2 workgroups per CU.
+  const long rows2 = 4L * R * 2;
+  g.R2 = ((long)N + rows2 - 1) / rows2 >= 512 ? 2 : 1;
+  const long rows_per_pass = 4L * R * g.R2;
+  long wgs = ((long)N + rows_per_pass - 1) / rows_per_pass;
+  const long cap = 256L * 8;  // grid-stride beyond 8 workgroups per CU
+  g.grid = (unsigned)(wgs < cap ? wgs : cap);
+  if (g.R2 == 2) {
+    switch (g.MM) {
+      case 1: return gemv_pair_launch<QF, XT, 2, 1>(g, A, W, C, M, N, K, s);
+      case 2: return gemv_pair_launch<QF, XT, 2, 2>(g, A, W, C, M, N, K, s);
+      default: return gemv_pair_launch<QF, XT, 2, 4>(g, A, W, C, M, N, K, s);
+    }
+  }
+  switch (g.MM) {
+    case 1: return gemv_pair_launch<QF, XT, 1, 1>(g, A, W, C, M, N, K, s);
+    case 2: return gemv_pair_launch<QF, XT, 1, 2>(g, A, W, C, M, N, K, s);
+    default: return gemv_pair_launch<QF, XT, 1, 4>(g, A, W, C, M, N, K, s);
+  }
 }
 
 }  // namespace nfk
