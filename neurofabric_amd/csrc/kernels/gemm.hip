@@ -2,20 +2,489 @@
 //
 // f16 path (metal_provider.mm:1433-1468 semantics): A f16 [M,K]; W quantized
 // [N,K]; each weight is dequantized to fp16 as RNE(d*q) — the same bits
-// dequant_*_f16 produces — staged in LDS, and multiplied on
-// v_mfma_f32_16x16x32_f16 with fp32 accumulation; C is rounded to fp16.
+// dequant_*_f16 produces — and multiplied with fp32 accumulation; C is
+// rounded to fp16.
 //
-// CTA tile 64(M) x 64(N), 4 waves each owning a 32x32 sub-tile (2x2 MFMA
-// 16x16 fragments); one Q4_0/Q8_0 block (32 k) per main-loop step.
+// Big-tile kernel (K % 64 == 0), the MFMA-bound prefill path:
+//   * CTA tile 256(M) x 256(N), K step 64 (two 32-element blocks = one
+//     Q4_0/Q8_0 pair per weight row), 4 waves in a 2x2 arrangement, each
+//     owning a 128x128 sub-tile = 4x4 v_mfma_f32_32x32x16_f16 tiles with
+//     fp32 accumulators (256 per lane, held in AGPRs).
+//   * A tile and dequantized W tile live in LDS as fp16, double buffered,
+//     rows padded to 144 B so the 16 lanes of a ds_read_b128 phase (16
+//     consecutive rows, same 16-B column) land in 16 distinct bank groups.
+//   * Each of the 256 threads fetches the next step's A chunks (8 x 16 B)
+//     and one weight pair (36 B Q4_0 / 68 B Q8_0, dword-aligned loads)
+//     before the current step's MFMAs are issued, then dequantizes the pair
+//     (exact packed-f16 arithmetic) into the other LDS buffer; one barrier
+//     per K step.
+//   * Dequantization happens once per CTA per weight element; its VALU cost
+//     relative to the MFMA work shrinks with the 256-row M tile.
 //
-// MFMA 16x16x32 operand layout used here (lane l of a wave64):
-//   A: row l%16, k = 8*(l/16) .. +7   (8 halves, 16 B)
-//   B: col l%16, k = 8*(l/16) .. +7
-//   D: col l%16, rows 4*(l/16) .. +3 (4 floats)
+// MFMA 32x32x16 f16 operand layout (lane l of a wave64):
+//   A: row l%32, k = 8*(l/32) .. +7     (8 halves, one ds_read_b128)
+//   B: col l%32, k = 8*(l/32) .. +7
+//   D: col l%32, row (r/4)*8 + (l/32)*4 + r%4 for accumulator r = 0..15
+//
+// Small-tile kernel (any K % 32 == 0): CTA tile 64x64, 4 waves of 32x32
+// built from v_mfma_f32_16x16x32_f16, one block per K step.
+#include <cstdlib>
+
 #include "../launch.hpp"
 #include "common.hpp"
 
 namespace nfk {
+
+typedef uint32_t u32x4a4_g __attribute__((ext_vector_type(4), aligned(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// dequantization of one pair (64 weights of one row) into 8 chunks of 8 fp16
+
+__device__ __forceinline__ half2v h2_of(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+__device__ __forceinline__ uint32_t u32_of(half2v h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Q4_0 code dword q (bytes = qs[4t..4t+3]) -> fp16 weights of elements
+// 4t..4t+3 (lo[0..1]) and 16+4t..16+4t+3 (hi[0..1]), each RNE(d*(n-8)).
+__device__ __forceinline__ void q4_word_f16(uint32_t q, half2v d2, uint32_t lo[2], uint32_t hi[2]) {
+  const uint32_t l = q & 0x0F0F0F0Fu;
+  const uint32_t h = (q >> 4) & 0x0F0F0F0Fu;
+  const half2v off = {(half_t)-1032.f, (half_t)-1032.f};
+  lo[0] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, l, 0x04010400u)) + off) * d2);
+  lo[1] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, l, 0x04030402u)) + off) * d2);
+  hi[0] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, h, 0x04010400u)) + off) * d2);
+  hi[1] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, h, 0x04030402u)) + off) * d2);
+}
+
+// Q8_0 code dword (4 signed codes) -> 2 fp16x2 = RNE(d*q).
+__device__ __forceinline__ void q8_word_f16(uint32_t q, half2v d2, uint32_t out[2]) {
+  const uint32_t u = q ^ 0x80808080u;  // code + 128
+  const half2v off = {(half_t)-1152.f, (half_t)-1152.f};
+  out[0] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + off) * d2);
+  out[1] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + off) * d2);
+}
+
+template <class QF> struct GPair;
+template <> struct GPair<Q4_0> {
+  static constexpr int kBytes = 36, kDwords = 9;
+};
+template <> struct GPair<Q8_0> {
+  static constexpr int kBytes = 68, kDwords = 17;
+};
+
+template <class QF>
+__device__ __forceinline__ void gload_pair(const uint8_t* p, uint32_t (&w)[GPair<QF>::kDwords]) {
+  const u32x4a4_g* v = reinterpret_cast<const u32x4a4_g*>(p);
+#pragma unroll
+  for (int i = 0; i < GPair<QF>::kDwords / 4; ++i) {
+    const u32x4 t = v[i];
+    w[4 * i + 0] = t.x;
+    w[4 * i + 1] = t.y;
+    w[4 * i + 2] = t.z;
+    w[4 * i + 3] = t.w;
+  }
+  w[GPair<QF>::kDwords - 1] = reinterpret_cast<const uint32_t*>(p)[GPair<QF>::kDwords - 1];
+}
+
+// 64 fp16 weights (natural element order) of a loaded pair, as 32 dwords.
+template <class QF>
+__device__ __forceinline__ void dequant_pair_f16(const uint32_t (&w)[GPair<QF>::kDwords], uint32_t (&o)[32]);
+
+template <>
+__device__ __forceinline__ void dequant_pair_f16<Q4_0>(const uint32_t (&w)[9], uint32_t (&o)[32]) {
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const uint32_t db = blk == 0 ? (w[0] & 0xFFFFu) : (w[4] >> 16);
+    const half2v d2 = h2_of(db | (db << 16));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t q = blk == 0 ? __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2) : w[5 + t];
+      uint32_t lo[2], hi[2];
+      q4_word_f16(q, d2, lo, hi);
+      // elements 4t..4t+3 -> dwords 2t, 2t+1; 16+4t.. -> dwords 8+2t, 8+2t+1
+      o[blk * 16 + 2 * t + 0] = lo[0];
+      o[blk * 16 + 2 * t + 1] = lo[1];
+      o[blk * 16 + 8 + 2 * t + 0] = hi[0];
+      o[blk * 16 + 8 + 2 * t + 1] = hi[1];
+    }
+  }
+}
+
+template <>
+__device__ __forceinline__ void dequant_pair_f16<Q8_0>(const uint32_t (&w)[17], uint32_t (&o)[32]) {
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const uint32_t db = blk == 0 ? (w[0] & 0xFFFFu) : (w[8] >> 16);
+    const half2v d2 = h2_of(db | (db << 16));
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const uint32_t q = blk == 0 ? __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2) : w[9 + t];
+      uint32_t v[2];
+      q8_word_f16(q, d2, v);
+      o[blk * 16 + 2 * t + 0] = v[0];
+      o[blk * 16 + 2 * t + 1] = v[1];
+    }
+  }
+}
+
+// 32 fp16 weights (natural element order) of block `h` (0 or 1) of a loaded pair.
+template <class QF>
+__device__ __forceinline__ void dequant_block_f16(const uint32_t (&w)[GPair<QF>::kDwords], int h,
+                                                  uint32_t (&o)[16]);
+
+template <>
+__device__ __forceinline__ void dequant_block_f16<Q4_0>(const uint32_t (&w)[9], int h, uint32_t (&o)[16]) {
+  const uint32_t db = h == 0 ? (w[0] & 0xFFFFu) : (w[4] >> 16);
+  const half2v d2 = h2_of(db | (db << 16));
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t q = h == 0 ? __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2) : w[5 + t];
+    uint32_t lo[2], hi[2];
+    q4_word_f16(q, d2, lo, hi);
+    o[2 * t + 0] = lo[0];
+    o[2 * t + 1] = lo[1];
+    o[8 + 2 * t + 0] = hi[0];
+    o[8 + 2 * t + 1] = hi[1];
+  }
+}
+
+template <>
+__device__ __forceinline__ void dequant_block_f16<Q8_0>(const uint32_t (&w)[17], int h, uint32_t (&o)[16]) {
+  const uint32_t db = h == 0 ? (w[0] & 0xFFFFu) : (w[8] >> 16);
+  const half2v d2 = h2_of(db | (db << 16));
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t q = h == 0 ? __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2) : w[9 + t];
+    uint32_t v[2];
+    q8_word_f16(q, d2, v);
+    o[2 * t + 0] = v[0];
+    o[2 * t + 1] = v[1];
+  }
+}
+
+// Half of block `h`'s code words (part 0: the first half, part 1: the
+// second) -> their fp16 weights in o[] (same positions as dequant_block_f16).
+template <class QF>
+__device__ __forceinline__ void dequant_block_part_f16(const uint32_t (&w)[GPair<QF>::kDwords], int h,
+                                                       int part, uint32_t (&o)[16]);
+
+template <>
+__device__ __forceinline__ void dequant_block_part_f16<Q4_0>(const uint32_t (&w)[9], int h, int part,
+                                                             uint32_t (&o)[16]) {
+  const uint32_t db = h == 0 ? (w[0] & 0xFFFFu) : (w[4] >> 16);
+  const half2v d2 = h2_of(db | (db << 16));
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int t = part * 2 + tt;
+    const uint32_t q = h == 0 ? __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2) : w[5 + t];
+    uint32_t lo[2], hi[2];
+    q4_word_f16(q, d2, lo, hi);
+    o[2 * t + 0] = lo[0];
+    o[2 * t + 1] = lo[1];
+    o[8 + 2 * t + 0] = hi[0];
+    o[8 + 2 * t + 1] = hi[1];
+  }
+}
+
+template <>
+__device__ __forceinline__ void dequant_block_part_f16<Q8_0>(const uint32_t (&w)[17], int h, int part,
+                                                             uint32_t (&o)[16]) {
+  const uint32_t db = h == 0 ? (w[0] & 0xFFFFu) : (w[8] >> 16);
+  const half2v d2 = h2_of(db | (db << 16));
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = part * 4 + tt;
+    const uint32_t q = h == 0 ? __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2) : w[9 + t];
+    uint32_t v[2];
+    q8_word_f16(q, d2, v);
+    o[2 * t + 0] = v[0];
+    o[2 * t + 1] = v[1];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// tiled MFMA kernel
+
+constexpr int kBK = 64;
+constexpr int kPitch = kBK + 8;  // halves per LDS row (144 B)
+
+// W staging per thread: one 32-element block of a row's pair.  Block h of
+// a Q4_0 pair lives in dwords 4h..4h+4 (5 dwords), of a Q8_0 pair in dwords
+// 8h..8h+8 (9 dwords); both windows start on a 4-byte boundary.
+template <class QF> struct WBlk;
+template <> struct WBlk<Q4_0> {
+  static constexpr int kDwords = 5, kStride = 4, kLoads = 2;  // kLoads: load instructions
+};
+template <> struct WBlk<Q8_0> {
+  static constexpr int kDwords = 9, kStride = 8, kLoads = 3;
+};
+// Dense fp16 B ([N,K] halves): streamed into LDS like A, no register staging.
+struct F16B {};
+template <> struct GPair<F16B> {
+  static constexpr int kBytes = 128, kDwords = 32;
+};
+template <> struct WBlk<F16B> {
+  static constexpr int kDwords = 1, kStride = 0, kLoads = 0;
+};
+
+template <class QF>
+__device__ __forceinline__ void load_wblk(const uint8_t* p, uint32_t (&w)[WBlk<QF>::kDwords]) {
+  const u32x4a4_g* v = reinterpret_cast<const u32x4a4_g*>(p);
+#pragma unroll
+  for (int i = 0; i < WBlk<QF>::kDwords / 4; ++i) {
+    const u32x4 t = v[i];
+    w[4 * i + 0] = t.x;
+    w[4 * i + 1] = t.y;
+    w[4 * i + 2] = t.z;
+    w[4 * i + 3] = t.w;
+  }
+  w[WBlk<QF>::kDwords - 1] = reinterpret_cast<const uint32_t*>(p)[WBlk<QF>::kDwords - 1];
+}
+
+// fp16 weights of the loaded block (h selects the pair position) in natural
+// element order, 16 dwords.
+template <class QF>
+__device__ __forceinline__ void dequant_wblk(const uint32_t (&w)[WBlk<QF>::kDwords], int h, uint32_t (&o)[16]);
+
+template <>
+__device__ __forceinline__ void dequant_wblk<Q4_0>(const uint32_t (&w)[5], int h, uint32_t (&o)[16]) {
+  const uint32_t db = h ? (w[0] >> 16) : (w[0] & 0xFFFFu);
+  const half2v d2 = h2_of(db | (db << 16));
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t q = h ? w[t + 1] : __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2);
+    uint32_t lo[2], hi[2];
+    q4_word_f16(q, d2, lo, hi);
+    o[2 * t + 0] = lo[0];
+    o[2 * t + 1] = lo[1];
+    o[8 + 2 * t + 0] = hi[0];
+    o[8 + 2 * t + 1] = hi[1];
+  }
+}
+
+template <>
+__device__ __forceinline__ void dequant_wblk<Q8_0>(const uint32_t (&w)[9], int h, uint32_t (&o)[16]) {
+  const uint32_t db = h ? (w[0] >> 16) : (w[0] & 0xFFFFu);
+  const half2v d2 = h2_of(db | (db << 16));
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t q = h ? w[t + 1] : __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2);
+    uint32_t v[2];
+    q8_word_f16(q, d2, v);
+    o[2 * t + 0] = v[0];
+    o[2 * t + 1] = v[1];
+  }
+}
+
+// 16 bytes per lane, global -> LDS without registers (global_load_lds_dwordx4):
+// lane i of the wave writes lds_base + 16*i.  The builtin only exists in the
+// device pass; the host pass must not see it or the kernel stub is dropped.
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, lds_base, 16, 0, 0);
+#endif
+}
+
+// LDS tile layout: rows of 64 halves (128 B, no padding); the 16-B chunk c of
+// row r sits at chunk slot c ^ ((r >> 1) & 7).  The 16 lanes of one
+// ds_read_b128 phase (16 consecutive rows, same chunk) then cover all 16
+// 16-B positions of the 256-B bank window, and a wave's direct-to-LDS load
+// (64 lanes x 16 B, contiguous) fills 8 whole rows.
+__device__ __forceinline__ int tile_off(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 7)) << 3); }
+
+// CTA tile BM x BN, WGM x WGN waves, each owning (BM/WGM) x (BN/WGN) =
+// TM x TN tiles of 32x32; K step 64, two LDS stages.
+//
+// Per K step s (LDS stage s&1):
+//   * A rows for step s+1 stream straight into the other stage with
+//     global_load_lds_dwordx4 (no registers, no VALU);
+//   * W blocks for step s+2 are fetched into one of two register sets;
+//   * the MFMAs of step s run from LDS;
+//   * W of step s+1 (fetched one step earlier) is dequantized to fp16 and
+//     written into the other stage;
+//   * one barrier.
+template <class QF, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half_t* __restrict__ A,
+                                                                    const uint8_t* __restrict__ W,
+                                                                    half_t* __restrict__ C, int M,
+                                                                    int N, int K) {
+  constexpr int NWAVE = WGM * WGN;
+  constexpr int NT = 64 * NWAVE;
+  constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;
+  constexpr int A_DMA = BM / 8 / NWAVE;  // direct-to-LDS loads (8 rows each) per wave per step
+  constexpr int STAGE = (BM + BN) * 64;  // halves
+  constexpr int WD = WBlk<QF>::kDwords;
+  static_assert(BM % (8 * NWAVE) == 0, "A rows per wave");
+  static_assert(BN * 2 <= NT || WBlk<QF>::kLoads == 0, "W staging: one block per thread");
+  extern __shared__ __attribute__((aligned(16))) half_t lds[];  // [2][A rows | B rows][64]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave / WGN) * (BM / WGM), wn = (wave % WGN) * (BN / WGN);
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int nk = K / kBK;
+
+  // A: lane -> (row within its 8-row group, chunk slot); the global chunk is
+  // the one the swizzle places in that slot.  Rows past M read row M-1
+  // (their outputs are never stored).
+  const half_t* asrc[A_DMA];
+#pragma unroll
+  for (int i = 0; i < A_DMA; ++i) {
+    const int r = (wave * A_DMA + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int gr = m0 + r < M ? m0 + r : M - 1;
+    asrc[i] = A + (size_t)gr * K + c * 8;
+  }
+  // Dense fp16 B: rows stream into LDS with the same mapping as A; rows past
+  // N read row N-1 (their outputs are never stored).
+  constexpr bool kDenseB = WBlk<QF>::kLoads == 0;
+  constexpr int B_DMA = kDenseB ? BN / 8 / NWAVE : 0;
+  const half_t* bsrc[B_DMA > 0 ? B_DMA : 1];
+  if constexpr (kDenseB) {
+    static_assert(BN % (8 * NWAVE) == 0, "B rows per wave");
+    const half_t* Bh = reinterpret_cast<const half_t*>(W);
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) {
+      const int r = (wave * B_DMA + i) * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int gr = n0 + r < N ? n0 + r : N - 1;
+      bsrc[i] = Bh + (size_t)gr * K + c * 8;
+    }
+  }
+  // W: thread -> (row, block); extra threads duplicate a row (identical writes).
+  const int w_row = (tid >> 1) % BN, w_half = tid & 1;
+  const bool w_valid = n0 + w_row < N;
+  const uint8_t* wsrc = nullptr;
+  if constexpr (!kDenseB) {
+    const size_t row_bytes = (size_t)(K / 64) * GPair<QF>::kBytes;
+    wsrc = W + (size_t)(w_valid ? n0 + w_row : 0) * row_bytes + w_half * 4 * WBlk<QF>::kStride;
+  }
+
+  auto dma_a = [&](int ks, int buf) {
+    half_t* dst = lds + (size_t)buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i)
+      lds_dma16(asrc[i] + (size_t)ks * kBK, dst + (wave * A_DMA + i) * 8 * 64);
+    if constexpr (kDenseB) {
+#pragma unroll
+      for (int i = 0; i < B_DMA; ++i)
+        lds_dma16(bsrc[i] + (size_t)ks * kBK, dst + (BM + (wave * B_DMA + i) * 8) * 64);
+    }
+  };
+  auto load_w = [&](int ks, uint32_t (&w)[WD]) {
+    if constexpr (!kDenseB) load_wblk<QF>(wsrc + (size_t)ks * GPair<QF>::kBytes, w);
+  };
+  auto stage_w = [&](int buf, const uint32_t (&w)[WD]) {
+    if constexpr (!kDenseB) {
+      uint32_t o[16];
+      dequant_wblk<QF>(w, w_half, o);
+      half_t* Bs = lds + (size_t)buf * STAGE + BM * 64;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        u32x4 v = {o[4 * c + 0], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]};
+        if (!w_valid) v = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(Bs + tile_off(w_row, w_half * 4 + c)) = v;
+      }
+    }
+  };
+
+  float16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
+
+  const int r32 = lane & 31, kc = lane >> 5;  // operand row, k-chunk within a 16-k slice
+  auto compute = [&](int buf) {
+    const half_t* As = lds + (size_t)buf * STAGE;
+    const half_t* Bs = As + BM * 64;
+    half8 a[2][TM], b[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[0][i] = *reinterpret_cast<const half8*>(As + tile_off(wm + 32 * i + r32, kc));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[0][j] = *reinterpret_cast<const half8*>(Bs + tile_off(wn + 32 * j + r32, kc));
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int cur = kk & 1;
+      if (kk + 1 < kBK / 16) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          a[cur ^ 1][i] = *reinterpret_cast<const half8*>(As + tile_off(wm + 32 * i + r32, 2 * (kk + 1) + kc));
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          b[cur ^ 1][j] = *reinterpret_cast<const half8*>(Bs + tile_off(wn + 32 * j + r32, 2 * (kk + 1) + kc));
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+    }
+    // Order for the scheduler: the first slice's operand reads, then per
+    // slice the next slice's reads ahead of this slice's MFMAs, so the MFMA
+    // pipe always has a slice queued while operands load.
+    __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      if (kk + 1 < kBK / 16) __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+    }
+  };
+
+  // Loads are unconditional (step indices clamped to the last step): a
+  // conditional load into a register set would force a copy, and the copy a
+  // wait for every outstanding load.  Past the end, the extra loads and
+  // stores only touch the idle stage.
+  uint32_t wr[2][WD] = {};
+  dma_a(0, 0);
+  load_w(0, wr[0]);
+  load_w(nk > 1 ? 1 : 0, wr[1]);
+  stage_w(0, wr[0]);
+  __syncthreads();
+
+  // End-of-step barrier: this wave's LDS writes and its A loads for the next
+  // step must be complete; the W loads for two steps ahead (issued after the
+  // A loads, kWLoads instructions) may stay in flight.  __syncthreads() would
+  // wait for every outstanding load.
+  auto step_barrier = [&]() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(WBlk<QF>::kLoads) : "memory");
+  };
+  auto half_step = [&](int s, int buf, uint32_t (&wload)[WD], const uint32_t (&wstage)[WD]) {
+    dma_a(s + 1 < nk ? s + 1 : s, buf ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(s + 2 < nk ? s + 2 : nk - 1, wload);  // wload held W(s), staged last step
+    __builtin_amdgcn_sched_barrier(0);
+    compute(buf);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_w(buf ^ 1, wstage);  // W(s+1)
+    __builtin_amdgcn_sched_barrier(0);
+    step_barrier();
+  };
+  int ks = 0;
+  for (; ks + 1 < nk; ks += 2) {
+    half_step(ks, 0, wr[0], wr[1]);
+    half_step(ks + 1, 1, wr[1], wr[0]);
+  }
+  if (ks < nk) half_step(ks, 0, wr[0], wr[1]);
+
+  // epilogue: round to fp16 and store
+  const int col = lane & 31, rq = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int gn = n0 + wn + 32 * j + col;
+      if (gn >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + wm + 32 * i + (r >> 2) * 8 + rq + (r & 3);
+        if (gm < M) C[(size_t)gm * N + gn] = (half_t)acc[i][j][r];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// small-tile kernel (any K % 32 == 0)
 
 constexpr int kTile = 64;
 constexpr int kLdsPad = 8;  // halves; keeps 16-B alignment of row starts
@@ -31,10 +500,10 @@ __device__ __forceinline__ half8 quarter_f16(const uint8_t* blk, int quarter) {
 }
 
 template <class QF>
-__global__ __launch_bounds__(256) void gemm_f16_kernel(const half_t* __restrict__ A,
-                                                       const uint8_t* __restrict__ W,
-                                                       half_t* __restrict__ C, int M, int N,
-                                                       int K) {
+__global__ __launch_bounds__(256) void gemm_small_kernel(const half_t* __restrict__ A,
+                                                         const uint8_t* __restrict__ W,
+                                                         half_t* __restrict__ C, int M, int N,
+                                                         int K) {
   __shared__ __attribute__((aligned(16))) half_t As[kTile][32 + kLdsPad];
   __shared__ __attribute__((aligned(16))) half_t Ws[kTile][32 + kLdsPad];
   const int tid = threadIdx.x;
@@ -90,23 +559,92 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(const half_t* __restrict_
       }
 }
 
+// Tile shape for the tiled MFMA kernel: 0 = 256x256 (8 waves, one CTA per
+// CU), 1 = 256x128 (8 waves, one CTA per CU), 2 = 128x128 (4 waves, two CTAs
+// per CU).  Score = fraction of CTA slots busy over the whole run (the last
+// round is usually partial) x the tile's relative per-CU efficiency, which
+// measured on MI355X at about 0.8 for the two smaller tiles against 256x256;
+// ties go to 128x128, whose two CTAs per CU hide each other's barriers.
+// NF_HIP_GEMM_TILE overrides the choice.
+inline int pick_tile(uint32_t M, uint32_t N) {
+  static const int forced = [] {
+    const char* e = std::getenv("NF_HIP_GEMM_TILE");
+    return e ? std::atoi(e) : -1;
+  }();
+  if (forced >= 0 && forced <= 2) return forced;
+  constexpr long kCUs = 256;
+  auto fill = [](long tiles, long slots) {
+    const long rounds = (tiles + slots - 1) / slots;
+    return (double)tiles / (double)(rounds * slots);
+  };
+  const long mt256 = (M + 255) / 256, mt128 = (M + 127) / 128;
+  const long nt256 = (N + 255) / 256, nt128 = (N + 127) / 128;
+  const double s0 = fill(mt256 * nt256, kCUs);
+  const double s1 = 0.8 * fill(mt256 * nt128, kCUs);
+  const double s2 = 0.8 * fill(mt128 * nt128, 2 * kCUs);
+  if (s0 > s1 && s0 > s2) return 0;
+  return s1 > s2 ? 1 : 2;
+}
+
+template <class QF, int BM, int BN, int WGM, int WGN>
+hipError_t gemm_tile_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_t M, uint32_t N,
+                            uint32_t K, hipStream_t s) {
+  const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+  if (grid.y > 65535) return hipErrorInvalidConfiguration;
+  const size_t lds = (size_t)2 * (BM + BN) * 64 * sizeof(half_t);
+  // More than 64 KB of dynamic LDS must be allowed explicitly, once per kernel.
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  gemm_tile_kernel<QF, BM, BN, WGM, WGN><<<grid, dim3(64 * WGM * WGN), lds, s>>>(a, w, c, M, N, K);
+  return hipGetLastError();
+}
+
 }  // namespace nfk
 
 namespace nfhip {
 
+// Dense fp16 x fp16 -> fp16 linear on the tiled MFMA kernel (B stored [N,K]).
+hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t M, uint32_t N, uint32_t K,
+                                 hipStream_t s) {
+  const nfk::half_t* a = static_cast<const nfk::half_t*>(A);
+  const uint8_t* b = static_cast<const uint8_t*>(B);
+  nfk::half_t* c = static_cast<nfk::half_t*>(C);
+  if (K % 64 != 0 || (uintptr_t)A % 16 != 0 || (uintptr_t)B % 16 != 0) return hipErrorInvalidValue;
+  switch (nfk::pick_tile(M, N)) {
+    case 0: return nfk::gemm_tile_launch<nfk::F16B, 256, 256, 2, 4>(a, b, c, M, N, K, s);
+    case 1: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 4, 2>(a, b, c, M, N, K, s);
+    default: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2>(a, b, c, M, N, K, s);
+  }
+}
+
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                             uint32_t N, uint32_t K, hipStream_t s) {
   if (t != EType::F16) return hipErrorInvalidValue;  // f32 path uses the skinny kernels
-  const dim3 block(256);
-  const dim3 grid((N + nfk::kTile - 1) / nfk::kTile, (M + nfk::kTile - 1) / nfk::kTile);
-  if (grid.y > 65535) return hipErrorInvalidConfiguration;
   const nfk::half_t* a = static_cast<const nfk::half_t*>(A);
   const uint8_t* w = static_cast<const uint8_t*>(W);
   nfk::half_t* c = static_cast<nfk::half_t*>(C);
+  const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
+  if (K % 64 == 0 && aligned) {
+    switch (nfk::pick_tile(M, N)) {
+      case 0:
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 256, 2, 4>(a, w, c, M, N, K, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 256, 2, 4>(a, w, c, M, N, K, s);
+      case 1:
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 4, 2>(a, w, c, M, N, K, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 4, 2>(a, w, c, M, N, K, s);
+      default:
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2>(a, w, c, M, N, K, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2>(a, w, c, M, N, K, s);
+    }
+  }
+  const dim3 grid((N + nfk::kTile - 1) / nfk::kTile, (M + nfk::kTile - 1) / nfk::kTile);
+  if (grid.y > 65535) return hipErrorInvalidConfiguration;
   if (q == QFmt::Q4_0)
-    nfk::gemm_f16_kernel<nfk::Q4_0><<<grid, block, 0, s>>>(a, w, c, M, N, K);
+    nfk::gemm_small_kernel<nfk::Q4_0><<<grid, dim3(256), 0, s>>>(a, w, c, M, N, K);
   else
-    nfk::gemm_f16_kernel<nfk::Q8_0><<<grid, block, 0, s>>>(a, w, c, M, N, K);
+    nfk::gemm_small_kernel<nfk::Q8_0><<<grid, dim3(256), 0, s>>>(a, w, c, M, N, K);
   return hipGetLastError();
 }
 

@@ -92,6 +92,10 @@ hipError_t launch_generic(QFmt q, EType t, const void* A, const void* W, void* C
 
 hipError_t launch_dense(EType a, EType b, EType c, const void* A, const void* B, void* C,
                         uint32_t M, uint32_t N, uint32_t K, hipStream_t s) {
+  // fp16 x fp16 -> fp16 with enough rows for MFMA tiles: the tiled MFMA kernel.
+  if (a == EType::F16 && b == EType::F16 && c == EType::F16 && M >= 32 && K % 64 == 0 &&
+      (uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0)
+    return launch_dense_mfma_f16(A, B, C, M, N, K, s);
   if (a == EType::F32) {
     return b == EType::F32 ? nfk::dense_c<float, float>(c, A, B, C, M, N, K, s)
                            : nfk::dense_c<float, nfk::half_t>(c, A, B, C, M, N, K, s);
