@@ -2,25 +2,37 @@
 """bench.py — throughput of the Q4_0/Q8_0 fused dequant+matmul path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode graph|eager] [--m M]
+                    [--no-extra] [--no-cpu] [--sweep]
 
 Headline workload: one TinyLlama-1.1B decode step
 = the 155 Q4_0 projections of 22 layers + lm_head, f32 activations, batch M
-(default 1), dispatched through the provider's C ABI.  A "step" is one pass
-over those 155 linears; K steps are timed with HIP events on the provider's
-stream (the stream every dispatch is launched on), after W warm-up steps.
-`value` is GB/s of algorithmic bytes (Q4_0 weight blocks + activations +
-outputs, each counted once per linear) per second, whole job, inputs resident
-in HBM.  The 582 MB of weights per step exceed 2x the 256 MB Infinity Cache,
-so nothing is served from cache across steps.
+(default 1), every projection dispatched through the provider's C ABI
+(nf_provider_vtable.dispatch semantics, via nf_hip_run_tasks).  A step is one
+pass over those 155 linears; W warm-up steps, then K steps timed with HIP
+events on the provider's stream.  Weights, activations and outputs are
+resident in HBM before timing starts; the 582 MB of weights per step exceed
+2x the 256 MB Infinity Cache, so steps do not hit in cache.
 
-Also reported (same JSON line): the decode step at M=4 and 16, the C0 single
-GEMV, and Llama-2-7B-shaped Q4_0 prefill GEMMs in TFLOP/s; the
-reference CPU path (the oracle's restated dequant + sequential-k loop) timed
-on this host's cores on a bounded sample.
+  value      = algorithmic bytes per step (Q4_0 blocks 18 B/32 weights +
+               activations + outputs, each counted once per linear) / step time
+  roofline   = the dominant kernel (the Q4_0 f32 decode GEMV, every launch of
+               the step): achieved = algorithmic bytes per launch / mean launch
+               duration over the timed region (graph replay: kernels run back
+               to back); traffic = measured HBM bytes per launch
+               from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/
+               (scaled by a copy-kernel calibration), when present
+  cpu_baseline = the oracle (the restated reference CPU dequant + sequential-k
+               loop, oracle/) timed on this host, 1 thread, on whole decode
+               steps repeated for >= 10 s
 
-Dispatch modes: `graph` captures the step's dispatches (one
-nf_hip_run_tasks call) into a HIP graph and replays it; `eager` calls
-nf_hip_run_tasks every step (host validation + launch per linear).
+Extras in the same JSON line: decode steps at M=4 and 16, configs[0] (one
+5632x2048 GEMV over 80 rotated weight copies), a Llama-3-8B Q8_0 decode step
+(configs[3], 32 layers + lm_head) at M=1/16/64, Llama-2-7B Q4_0 prefill GEMMs
+(configs[2]) in TFLOP/s, and with --sweep the configs[4] GEMV-vs-MFMA sweep
+over M = 1..256 on the 28672x8192 gate projection.
+
+Modes: `graph` captures the step's dispatches (one nf_hip_run_tasks call)
+into a HIP graph and replays it; `eager` calls nf_hip_run_tasks every step.
 """
 from __future__ import annotations
 
@@ -40,6 +52,7 @@ sys.path.insert(0, str(REPO))
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2516.6    # MI355X dense fp16 MFMA
 METRIC = "Q4_0 GEMV achieved GB/s (% HBM peak); prefill dequant-GEMM TFLOP/s"
+PMC_SUMMARY = REPO / "profiles" / "gemv_q4_0_f32_tinyllama_decode_pmc.json"
 
 
 def log(*a):
@@ -53,16 +66,44 @@ def parse(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--m", type=int, default=1, help="decode batch of the headline step")
+    ap.add_argument("--roof-steps", type=int, default=5, help="eager steps timed per dispatch (<= 6)")
     ap.add_argument("--no-extra", action="store_true", help="only the headline decode step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--sweep", action="store_true", help="configs[4] GEMV/MFMA crossover sweep")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run 4 device-to-device copies of BYTES (reference for HBM byte counters)")
     return ap.parse_args(argv)
+
+
+def calibrate_copy(nbytes: int) -> int:
+    """Device-to-device copies of a known size on the provider stream, so the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counters can be scaled to bytes."""
+    from neurofabric_amd import abi, hiprt
+    from neurofabric_amd.plugin import Provider
+    prov = Provider()
+    prov.init()
+    src = prov.alloc(abi.NF_DTYPE_U8, nbytes)
+    dst = prov.alloc(abi.NF_DTYPE_U8, nbytes)
+    hip = hiprt.lib()
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    hip.hipMemcpyAsync.restype = C.c_int
+    stream = prov.stream()
+    for _ in range(4):
+        hiprt.check(hip.hipMemcpyAsync(C.c_void_p(dst.device_ptr()), C.c_void_p(src.device_ptr()), nbytes, 3,
+                                       C.c_void_p(stream)), "hipMemcpyAsync")
+    prov.synchronize()
+    src.release()
+    dst.release()
+    print(json.dumps({"calibrate_copy_bytes": nbytes, "copies": 4}), flush=True)
+    return 0
 
 
 # ---------------------------------------------------------------------------
 # workloads
 
 class Step:
-    """A list of prepared dispatches plus the buffers they reference."""
+    """A list of prepared task descriptors plus the buffers they reference."""
 
     def __init__(self, prov):
         self.prov = prov
@@ -105,26 +146,43 @@ class Step:
         self.buffers.clear()
 
 
-def decode_step(prov, M: int, fmt: str = "q4_0") -> Step:
-    """22 x {q, k, v, o, gate, up, down} + lm_head, f32 activations."""
+class WeightSet:
+    """Distinct weight buffers for a list of projections (same bytes per
+    shape), uploaded once and reused by steps at different batch sizes."""
+
+    def __init__(self, prov, shapes, fmt: str, seed_base: int = 0):
+        from neurofabric_amd import abi, synthetic as syn
+        self.fmt, self.shapes = fmt, list(shapes)
+        qdt = abi.NF_DTYPE_Q4_0 if fmt == "q4_0" else abi.NF_DTYPE_Q8_0
+        cache = {}
+        self.bufs = []
+        for (_, N, K) in self.shapes:
+            if (N, K) not in cache:
+                cache[(N, K)] = syn.weights(fmt, N, K, seed=seed_base + N * 7 + K)
+            self.bufs.append(prov.alloc_array(cache[(N, K)], qdt))
+
+    def release(self):
+        for b in self.bufs:
+            b.release()
+        self.bufs = []
+
+
+def model_step(prov, ws: WeightSet, M: int, f16: bool = False) -> Step:
+    """One decode step over a weight set: shared activation/output buffers
+    per K/N, one dispatch per projection."""
     from neurofabric_amd import abi, synthetic as syn
     st = Step(prov)
-    qdt = abi.NF_DTYPE_Q4_0 if fmt == "q4_0" else abi.NF_DTYPE_Q8_0
-    cache = {}
-    shapes = syn.tinyllama_step_shapes()
+    adt = abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32
+    elt = 2 if f16 else 4
     acts, outs = {}, {}
-    for i, (name, N, K) in enumerate(shapes):
-        if (N, K) not in cache:
-            cache[(N, K)] = syn.weights(fmt, N, K, seed=N * 7 + K)
-        w = prov.alloc_array(cache[(N, K)], qdt)  # a distinct buffer per layer
-        st.buffers.append(w)
+    for (name, N, K), w in zip(ws.shapes, ws.bufs):
         if K not in acts:
-            acts[K] = prov.alloc_array(syn.activations(M, K, seed=K), abi.NF_DTYPE_F32)
+            acts[K] = prov.alloc_array(syn.activations(M, K, seed=K, dtype=np.float16 if f16 else np.float32), adt)
             st.buffers.append(acts[K])
         if N not in outs:
-            outs[N] = prov.alloc(abi.NF_DTYPE_F32, M * N * 4)
+            outs[N] = prov.alloc(adt, M * N * elt)
             st.buffers.append(outs[N])
-        st.add(f"dequant_{fmt}_linear", [acts[K], w], [outs[N]], M, N, K)
+        st.add(f"dequant_{ws.fmt}_linear" + ("_f16" if f16 else ""), [acts[K], w], [outs[N]], M, N, K)
     return st.finish()
 
 
@@ -175,10 +233,26 @@ def time_step(prov, st: Step, steps: int, warmup: int, mode: str) -> dict:
             "us_per_launch": ms * 1e3 / len(st.tasks)}
 
 
+def time_dispatches(prov, st: Step, steps: int) -> dict:
+    """Per-dispatch GPU durations of `steps` eager passes (timing ring)."""
+    steps = max(1, min(steps, 1024 // len(st.tasks)))
+    prov.run_tasks(st.tasks, 1)  # warm
+    prov.synchronize()
+    prov.enable_timing(True)
+    prov.run_tasks(st.tasks, steps)
+    prov.synchronize()
+    rec = prov.timings()
+    prov.enable_timing(False)
+    ms = np.array([r[1] for r in rec], np.float64)
+    return {"launches": len(ms), "mean_launch_us": float(ms.mean() * 1e3),
+            "median_launch_us": float(np.median(ms) * 1e3), "sum_ms": float(ms.sum()),
+            "steps": steps}
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline (the oracle: restated reference CPU dequant + sequential-k loop)
 
-def cpu_baseline(threads: int) -> dict:
+def cpu_baseline(threads: int, seconds: float) -> dict:
     from neurofabric_amd import synthetic as syn
     from oracle import oracle as orc
     shapes = syn.tinyllama_step_shapes()
@@ -186,18 +260,72 @@ def cpu_baseline(threads: int) -> dict:
     for _, N, K in shapes:
         if (N, K) not in cache:
             cache[(N, K)] = (syn.q4_0_weights(N, K, seed=N * 7 + K), syn.activations(1, K, seed=K))
-    total_bytes = 0
+    step_bytes = sum(cache[(N, K)][0].nbytes + K * 4 + N * 4 for _, N, K in shapes)
+    reps = 0
     t0 = time.perf_counter()
-    for _, N, K in shapes:
-        W, A = cache[(N, K)]
-        orc.fused(A, W, "q4_0", 1, N, K, threads=threads)
-        total_bytes += W.nbytes + A.nbytes + N * 4
+    while True:
+        for _, N, K in shapes:
+            W, A = cache[(N, K)]
+            orc.fused(A, W, "q4_0", 1, N, K, threads=threads)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
     dt = time.perf_counter() - t0
-    return {"value": total_bytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "seconds": dt,
-            "sample": "one full configs[1] decode step (155 Q4_0 linears, M=1, f32) through the oracle's "
-                      "restated reference CPU path (dequant + sequential-k fp32 loop), "
-                      f"{threads} thread(s)"}
+    return {"value": step_bytes * reps / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "seconds": dt, "steps": reps, "tokens_per_s": reps / dt,
+            "sample": f"{reps} whole configs[1] decode steps (155 Q4_0 linears, M=1, f32 activations, "
+                      f"{step_bytes / 1e6:.1f} MB of algorithmic bytes each) through the oracle's "
+                      f"restatement of the reference CPU path (dequant + sequential-k fp32 loop), "
+                      f"{threads} thread(s), {dt:.1f} s"}
+
+
+# ---------------------------------------------------------------------------
+# extras
+
+def llama3_q8_step_shapes(layers: int = 32):
+    from neurofabric_amd import synthetic as syn
+    out = []
+    for layer in range(layers):
+        for name, n, k in syn.LLAMA3_8B_Q8[:-1]:
+            out.append((f"l{layer}.{name}", n, k))
+    out.append(syn.LLAMA3_8B_Q8[-1])
+    return out
+
+
+def crossover_sweep(prov, N=28672, K=8192, Ms=(1, 2, 4, 8, 16, 32, 64, 128, 256)) -> dict:
+    """the gate projection through both kernel families at each M
+    (f16 activations), by pinning the GEMV/MFMA switch point."""
+    f32_max, f16_max = prov.get_gemv_max_m()
+    rows = []
+    try:
+        for M in Ms:
+            row = {"M": M}
+            for path, limit in (("gemv", 1 << 30), ("mfma", 0)):
+                prov.set_gemv_max_m(f32_max, limit)
+                st = rotated_linear(prov, "q4_0", M, N, K, True, 4)
+                r = time_step(prov, st, 5, 1, "eager")
+                us = r["us_per_launch"]
+                row[path] = {"us": us, "GB_s": st.bytes / len(st.tasks) / (us * 1e-6) / 1e9,
+                             "TFLOP_s": st.flops / len(st.tasks) / (us * 1e-6) / 1e12,
+                             "kernels": sorted(st.kernels)}
+                st.release()
+            row["faster"] = "gemv" if row["gemv"]["us"] <= row["mfma"]["us"] else "mfma"
+            rows.append(row)
+            log(f"[bench] sweep M={M}: gemv {row['gemv']['us']:.1f} us, mfma {row['mfma']['us']:.1f} us")
+    finally:
+        prov.set_gemv_max_m(f32_max, f16_max)
+    switch = next((r["M"] for r in rows if r["faster"] == "mfma"), None)
+    return {"shape": f"{N}x{K} Q4_0, f16 activations", "rows": rows, "first_M_where_mfma_wins": switch}
+
+
+def load_pmc_summary():
+    if PMC_SUMMARY.exists():
+        try:
+            d = json.loads(PMC_SUMMARY.read_text())
+            return d
+        except (OSError, ValueError):
+            return None
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -205,44 +333,82 @@ def cpu_baseline(threads: int) -> dict:
 def main(argv=None) -> int:
     args = parse(argv)
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards by output rows with no collective, see DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path "
+              "shards by weight rows across GPUs, which this build does not run", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
+    from neurofabric_amd import synthetic as syn
     from neurofabric_amd.plugin import Provider
     prov = Provider()
     prov.init()
 
     log(f"[bench] headline: configs[1] decode step M={args.m} mode={args.mode}")
-    st = decode_step(prov, args.m)
+    tiny = WeightSet(prov, syn.tinyllama_step_shapes(), "q4_0")
+    st = model_step(prov, tiny, args.m)
     r = time_step(prov, st, args.steps, args.warmup, args.mode)
     gbs = st.bytes / (r["ms_per_step"] * 1e-3) / 1e9
     log(f"[bench] M={args.m}: {r['ms_per_step']*1e3:.1f} us/step, {gbs:.1f} GB/s, "
         f"{r['us_per_launch']:.2f} us/launch, kernels={sorted(st.kernels)}")
-    head = {"step": r, "bytes_per_step": st.bytes, "weight_bytes_per_step": st.weight_bytes,
-            "kernels": sorted(st.kernels), "tokens_per_s": args.m / (r["ms_per_step"] * 1e-3)}
+    # Dominant kernel = the decode GEMV (every dispatch of the step).  Its mean
+    # launch duration is the timed region's HIP-event time on the provider
+    # stream / launches: graph replay leaves no host gaps between kernels (the
+    # rocprofv3 kernel trace of this command shows them back to back), so
+    # this is kernel time.  Per-dispatch event pairs (the timing ring) add
+    # ~2 us of event overhead per launch; they are reported as a cross-check.
+    bytes_per_launch = st.bytes / len(st.tasks)
+    avg_launch_us = r["us_per_launch"]
+    achieved = bytes_per_launch / (avg_launch_us * 1e-6) / 1e9
+    ring = time_dispatches(prov, st, args.roof_steps)
+    log(f"[bench] dominant kernel: {avg_launch_us:.2f} us/launch, {achieved:.1f} GB/s per launch "
+        f"(event-ring cross-check {ring['mean_launch_us']:.2f} us)")
     launches = len(st.tasks)
+    kernels = sorted(st.kernels)
     st.release()
 
-    extra = {}
+    extra = {"headline_step": {"us_per_step": r["ms_per_step"] * 1e3, "wall_us_per_step": r["wall_ms_per_step"] * 1e3,
+                               "launches": launches, "bytes_per_step": bytes_per_launch * launches,
+                               "tokens_per_s": args.m / (r["ms_per_step"] * 1e-3)}}
     if not args.no_extra:
         for M in (4, 16):
             if M == args.m:
                 continue
-            s2 = decode_step(prov, M)
+            s2 = model_step(prov, tiny, M)
             r2 = time_step(prov, s2, max(10, args.steps // 2), args.warmup, args.mode)
-            extra[f"decode_m{M}"] = {"GB_s": s2.bytes / (r2["ms_per_step"] * 1e-3) / 1e9,
-                                     "us_per_step": r2["ms_per_step"] * 1e3,
-                                     "tokens_per_s": M / (r2["ms_per_step"] * 1e-3),
-                                     "kernels": sorted(s2.kernels)}
-            log(f"[bench] decode M={M}: {extra[f'decode_m{M}']}")
+            extra[f"c1_decode_m{M}"] = {"GB_s": s2.bytes / (r2["ms_per_step"] * 1e-3) / 1e9,
+                                        "us_per_step": r2["ms_per_step"] * 1e3,
+                                        "tokens_per_s": M / (r2["ms_per_step"] * 1e-3),
+                                        "kernels": sorted(s2.kernels)}
+            log(f"[bench] decode M={M}: {extra[f'c1_decode_m{M}']}")
             s2.release()
+    tiny.release()
+    if not args.no_extra:
         # one GEMV shape, 80 rotated copies (519 MB > 2x MALL)
         s0 = rotated_linear(prov, "q4_0", 1, 5632, 2048, False, 80)
         r0 = time_step(prov, s0, 20, 3, args.mode)
-        extra["c0_gemv_5632x2048"] = {"GB_s": s0.bytes / (r0["ms_per_step"] * 1e-3) / 1e9,
-                                      "us_per_launch": r0["us_per_launch"], "kernels": sorted(s0.kernels)}
+        d0 = time_dispatches(prov, s0, 6)
+        extra["c0_gemv_5632x2048"] = {"GB_s_step": s0.bytes / (r0["ms_per_step"] * 1e-3) / 1e9,
+                                      "us_per_launch_step": r0["us_per_launch"],
+                                      "us_per_launch_kernel": d0["mean_launch_us"],
+                                      "GB_s_kernel": s0.bytes / len(s0.tasks) / (d0["mean_launch_us"] * 1e-6) / 1e9,
+                                      "kernels": sorted(s0.kernels)}
         log(f"[bench] C0: {extra['c0_gemv_5632x2048']}")
         s0.release()
+        # Llama-3-8B Q8_0 decode step, 32 layers + lm_head
+        c3 = {}
+        llama3 = WeightSet(prov, llama3_q8_step_shapes(), "q8_0")
+        for M in (1, 16, 64):
+            s3 = model_step(prov, llama3, M)
+            r3 = time_step(prov, s3, 10, 2, args.mode)
+            c3[f"m{M}"] = {"GB_s": s3.bytes / (r3["ms_per_step"] * 1e-3) / 1e9,
+                           "us_per_step": r3["ms_per_step"] * 1e3,
+                           "tokens_per_s": M / (r3["ms_per_step"] * 1e-3),
+                           "weight_GB_per_step": s3.weight_bytes / 1e9, "kernels": sorted(s3.kernels)}
+            log(f"[bench] C3 Q8_0 decode M={M}: {c3[f'm{M}']}")
+            s3.release()
+        llama3.release()
+        extra["c3_llama3_8b_q8_0_decode"] = c3
+        # Llama-2-7B prefill GEMMs
         pre = {}
         for (name, N, K) in [("qkvo_4096x4096", 4096, 4096), ("gate_up_11008x4096", 11008, 4096),
                              ("down_4096x11008", 4096, 11008)]:
@@ -255,18 +421,23 @@ def main(argv=None) -> int:
                 log(f"[bench] prefill {name} M={M}: {tf:.1f} TFLOP/s")
                 sp.release()
         extra["c2_prefill_f16"] = pre
+    if args.sweep:
+        extra["c4_crossover"] = crossover_sweep(prov)
 
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (1 thread) ...")
-        cpu = cpu_baseline(1)
-        log(f"[bench] cpu 1 thread: {cpu['value']:.3f} GB/s in {cpu['seconds']:.1f} s")
+        cpu = cpu_baseline(1, args.cpu_seconds)
+        log(f"[bench] cpu 1 thread: {cpu['value']:.3f} GB/s over {cpu['seconds']:.1f} s")
         ncores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-        allc = cpu_baseline(min(ncores, 64))
+        allc = cpu_baseline(min(ncores, 64), min(args.cpu_seconds, 5.0))
         extra["cpu_all_cores"] = allc
         log(f"[bench] cpu {allc['cores']} threads: {allc['value']:.3f} GB/s")
 
-    gbs_launch = (head["bytes_per_step"] / launches) / (r["us_per_launch"] * 1e-6) / 1e9
+    pmc = load_pmc_summary()
+    traffic = None
+    if pmc and pmc.get("kernel_family") == kernels[0]:
+        traffic = pmc.get("hbm_bytes_per_launch")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -278,17 +449,21 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "q4_0 weights, f32 activations/accumulate",
         "data": "synthetic (seeded Q4_0 blocks: fp16 scales |N(0,1)|*0.01, codes U{0..15}; x ~ N(0,1))",
-        "config": {"workload": f"configs[1] TinyLlama-1.1B Q4_0 decode step, M={args.m}, 22 layers + "
-                               f"lm_head = {launches} fused dequant+GEMV dispatches ({args.mode})",
+        "config": {"workload": f"configs[1] TinyLlama-1.1B Q4_0 decode step, M={args.m}: 22 layers x "
+                               f"{{q,k,v,o,gate,up,down}} + lm_head = {launches} fused dequant+GEMV "
+                               f"dispatches ({args.mode})",
                    "batch": args.m, "hidden": 2048, "ffn": 5632, "vocab": 32000,
-                   "tokens_per_s": head["tokens_per_s"]},
-        "roofline": {"bound": "hbm", "kernel": ",".join(head["kernels"]), "achieved": round(gbs_launch, 2),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs_launch / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "bytes_per_launch": head["bytes_per_step"] / launches,
-                     "avg_launch_us": r["us_per_launch"]},
+                   "tokens_per_s": args.m / (r["ms_per_step"] * 1e-3)},
+        "roofline": {"bound": "hbm", "kernel": ",".join(kernels), "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "bytes_per_launch": bytes_per_launch,
+                     "avg_launch_us": avg_launch_us,
+                     "launches_timed": launches * args.steps,
+                     "event_ring_mean_launch_us": ring["mean_launch_us"],
+                     "traffic_source": str(PMC_SUMMARY.relative_to(REPO)) if traffic is not None else None},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "extra": extra,
     }

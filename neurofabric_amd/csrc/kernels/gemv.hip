@@ -27,8 +27,10 @@
 //     each group works on R2 rows at once, reading each activation chunk
 //     from LDS once for all R2 rows.  The next pair's weights are loaded
 //     before the current pair is computed.
-//   * Partial sums are reduced across the L lanes of a group with xor
-//     shuffles; lane 0 of the group writes the R2 x M outputs.
+//   * Partial sums are reduced across the L lanes of a group with DPP adds;
+//     the group's last lane writes the R2 x M outputs.
+//   * The grid is capped at two workgroups per CU; larger row counts loop,
+//     reusing the staged activations.
 //
 // Unpacking (per 32-bit word of codes = 8 Q4_0 codes / 4 Q8_0 codes):
 //   f32, Q4_0: low and high nibbles are masked into bytes 0..15; bytes 0..15
@@ -275,6 +277,28 @@ __device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kD
   }
 }
 
+// ---- cross-lane sums --------------------------------------------------------
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               ROW_MASK, 0xF, false));
+}
+
+// Sum over aligned groups of 2^log2L lanes (16, 32 or 64).  Within a row of
+// 16: quad_perm xor 1, xor 2, row_half_mirror, row_mirror leave the row sum
+// in every lane; row_bcast15 / row_bcast31 then fold rows 0+1 (2+3) and
+// 01+23.  The group sum is in the group's last lane.
+__device__ __forceinline__ float group_sum(float v, int log2L) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  if (log2L >= 5) v += dpp_f<0x142, 0xA>(v);  // row_bcast15 -> rows 1, 3
+  if (log2L >= 6) v += dpp_f<0x143, 0xC>(v);  // row_bcast31 -> rows 2, 3
+  return v;
+}
+
 // ---- the pair kernel ------------------------------------------------------
 
 template <class QF, typename XT, int R2, int MM>
@@ -328,25 +352,26 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   if (base < N && li < P) load(row0, li, wc);
 
   // ---- stage A into LDS (and the per-block sums of x) ----
-  const int total = MM * P * CP;
-  for (int c0 = 0; c0 < total; c0 += 256) {
-    const int ci = c0 + tid;
-    ChunkT v = {};
-    int m = 0, pair = 0, c = 0;
-    if (ci < total) {
-      m = ci / (P * CP);
-      const int r = ci - m * P * CP;
-      pair = r / CP;
-      c = r - pair * CP;
-      if (m < M) v = *reinterpret_cast<const ChunkT*>(A + (size_t)m * K + (size_t)pair * 64 + c * EPC);
-      xs[xslot<XT>(m, P, pair, c)] = v;
-    }
-    if constexpr (kSx) {
-      float s = v[0] + v[1] + v[2] + v[3];
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      s += __shfl_xor(s, 4, 64);
-      if ((tid & 7) == 0 && ci < total) sxs[(m * P + pair) * 2 + (c >> 3)] = s * (8.0f * unit);
+  // One 32-element block per thread per iteration: its sum stays in the
+  // thread (no cross-lane traffic) and the chunk index needs no division.
+  const int nb = K >> 5;
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    for (int b = tid; b < nb; b += 256) {
+      const int pair = b >> 1, half = b & 1;
+      constexpr int CPB = CP / 2;  // chunks per block
+      ChunkT v[CPB];
+#pragma unroll
+      for (int j = 0; j < CPB; ++j)
+        v[j] = m < M ? *reinterpret_cast<const ChunkT*>(A + (size_t)m * K + (size_t)b * 32 + j * EPC) : ChunkT{};
+#pragma unroll
+      for (int j = 0; j < CPB; ++j) xs[xslot<XT>(m, P, pair, half * CPB + j)] = v[j];
+      if constexpr (kSx) {
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPB; ++j) sum += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+        sxs[(m * P + pair) * 2 + half] = sum * (8.0f * unit);
+      }
     }
   }
   __syncthreads();
@@ -383,16 +408,12 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
           for (int i = 0; i < DW; ++i) wc[j][i] = wn[j][i];
       }
     }
-    // reduce across the L lanes of the group
+    // reduce across the L lanes of the group (DPP; the sum lands in lane L-1)
 #pragma unroll
     for (int j = 0; j < R2; ++j)
 #pragma unroll
-      for (int m = 0; m < MM; ++m) {
-        float v = acc[j][m];
-        for (int off = L >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-        acc[j][m] = v;
-      }
-    if (li == 0) {
+      for (int m = 0; m < MM; ++m) acc[j][m] = group_sum(acc[j][m], log2L);
+    if (li == L - 1) {
 #pragma unroll
       for (int j = 0; j < R2; ++j) {
         if (row0 + j >= N) continue;
@@ -540,12 +561,14 @@ hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint
   if (g.lds > 64 * 1024) return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
   g.log2L = pick_log2L(P);
   const int R = 64 >> g.log2L;
-  // Two rows per lane group when that still leaves >= 2 workgroups per CU.
-  const long rows2 = 4L * R * 2;
-  g.R2 = ((long)N + rows2 - 1) / rows2 >= 512 ? 2 : 1;
-  const long rows_per_pass = 4L * R * g.R2;
-  long wgs = ((long)N + rows_per_pass - 1) / rows_per_pass;
-  const long cap = 256L * 8;  // grid-stride beyond 8 workgroups per CU
+  // One row per lane group while one pass of the grid covers all rows within
+  // two workgroups per CU; else two rows per group (more loads in flight per
+  // lane); beyond that the capped grid loops, reusing the staged activations.
+  const long cap = 256L * 2;
+  const long wgs1 = ((long)N + 4L * R - 1) / (4L * R);
+  const long wgs2 = ((long)N + 8L * R - 1) / (8L * R);
+  g.R2 = wgs1 <= cap ? 1 : 2;
+  const long wgs = g.R2 == 1 ? wgs1 : wgs2;
   g.grid = (unsigned)(wgs < cap ? wgs : cap);
   if (g.R2 == 2) {
     switch (g.MM) {

@@ -278,6 +278,23 @@ class Provider:
     def plan(self, op: str, in_descs, out_descs, M=0, N=0, K=0, pc: bytes | None = None) -> dict:
         return plan(self.lib, op, in_descs, out_descs, M, N, K, pc)
 
+    # -- per-dispatch GPU timing ring ----------------------------------
+    def enable_timing(self, on: bool = True) -> None:
+        """Record a HIP-event pair around every dispatch on the provider
+        stream (1024-entry ring, cleared when enabled)."""
+        self.lib.nf_hip_enable_timing(bool(on))
+
+    def timings(self):
+        """[(op_name, gpu_ms, out_dtype, elems)] for the recorded dispatches,
+        oldest first (waits for the last recorded dispatch to finish)."""
+        n = self.lib.nf_hip_get_timing_count()
+        names = (C.c_char * 64 * max(1, n))()
+        ms = (C.c_double * max(1, n))()
+        dts = (C.c_uint8 * max(1, n))()
+        els = (C.c_uint32 * max(1, n))()
+        self.lib.nf_hip_get_timings_ext(names, ms, dts, els, n)
+        return [(bytes(names[i]).split(b"\0", 1)[0].decode(), ms[i], dts[i], els[i]) for i in range(n)]
+
     # -- crossover ------------------------------------------------------
     def set_gemv_max_m(self, f32: int, f16: int) -> None:
         self.lib.nf_hip_set_gemv_max_m(f32, f16)
