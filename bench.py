@@ -292,16 +292,22 @@ def llama3_q8_step_shapes(layers: int = 32):
     return out
 
 
-def crossover_sweep(prov, N=28672, K=8192, Ms=(1, 2, 4, 8, 16, 32, 64, 128, 256)) -> dict:
-    """the gate projection through both kernel families at each M
-    (f16 activations), by pinning the GEMV/MFMA switch point."""
-    f32_max, f16_max = prov.get_gemv_max_m()
+def crossover_sweep(prov, N=28672, K=8192, Ms=(1, 2, 3, 4, 8, 16, 32, 64, 128, 256)) -> dict:
+    """the gate projection through every kernel family at each M
+    (f16 activations), by pinning the switch points: the VALU GEMV, the
+    small-batch MFMA kernel (M <= 64 per launch) and the tiled MFMA GEMM."""
+    g32, g16 = prov.get_gemv_max_m()
+    sk16 = prov.get_skinny_max_m()
+    pins = {"gemv": (1 << 30, 1 << 30), "skinny": (0, 1 << 30), "tiled": (0, 0)}
     rows = []
     try:
         for M in Ms:
             row = {"M": M}
-            for path, limit in (("gemv", 1 << 30), ("mfma", 0)):
-                prov.set_gemv_max_m(f32_max, limit)
+            for path, (gmax, smax) in pins.items():
+                if path == "skinny" and M > 64:
+                    continue
+                prov.set_gemv_max_m(g32, gmax)
+                prov.set_skinny_max_m(smax)
                 st = rotated_linear(prov, "q4_0", M, N, K, True, 4)
                 r = time_step(prov, st, 5, 1, "eager")
                 us = r["us_per_launch"]
@@ -309,13 +315,14 @@ def crossover_sweep(prov, N=28672, K=8192, Ms=(1, 2, 4, 8, 16, 32, 64, 128, 256)
                              "TFLOP_s": st.flops / len(st.tasks) / (us * 1e-6) / 1e12,
                              "kernels": sorted(st.kernels)}
                 st.release()
-            row["faster"] = "gemv" if row["gemv"]["us"] <= row["mfma"]["us"] else "mfma"
+            row["fastest"] = min((k for k in pins if k in row), key=lambda k: row[k]["us"])
             rows.append(row)
-            log(f"[bench] sweep M={M}: gemv {row['gemv']['us']:.1f} us, mfma {row['mfma']['us']:.1f} us")
+            log(f"[bench] sweep M={M}: " + ", ".join(f"{k} {row[k]['us']:.1f} us" for k in pins if k in row))
     finally:
-        prov.set_gemv_max_m(f32_max, f16_max)
-    switch = next((r["M"] for r in rows if r["faster"] == "mfma"), None)
-    return {"shape": f"{N}x{K} Q4_0, f16 activations", "rows": rows, "first_M_where_mfma_wins": switch}
+        prov.set_gemv_max_m(g32, g16)
+        prov.set_skinny_max_m(sk16)
+    return {"shape": f"{N}x{K} Q4_0, f16 activations", "rows": rows,
+            "fastest_by_M": {r["M"]: r["fastest"] for r in rows}}
 
 
 def load_pmc_summary():

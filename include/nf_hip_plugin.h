@@ -99,12 +99,17 @@ NF_API nf_status nf_hip_plan_dispatch(const char *op_name,
                                       const void *push_constants, uint32_t push_constants_size,
                                       nf_hip_plan *plan);
 
-/* Batch-size switch points between the skinny (GEMV) kernels and the MFMA
- * GEMM kernels: dispatch uses the GEMV family while M <= max_m.  Defaults
- * come from measurement; environment overrides NF_HIP_GEMV_MAX_M_F32 and
- * NF_HIP_GEMV_MAX_M_F16 are read at nf_plugin_register. */
+/* Batch-size switch points between the kernel families of the fused ops:
+ * the VALU decode GEMV while M <= gemv_max_m, the small-batch MFMA kernel
+ * above it (up to skinny_max_m for f16 activations; f32 activations stay on
+ * it for every M, 64 rows per launch), the LDS-tiled MFMA GEMM beyond
+ * (f16).  Defaults come from measurement; environment overrides
+ * NF_HIP_GEMV_MAX_M_F32, NF_HIP_GEMV_MAX_M_F16 and NF_HIP_SKINNY_MAX_M_F16
+ * are read at nf_plugin_register. */
 NF_API void nf_hip_set_gemv_max_m(uint32_t f32_path, uint32_t f16_path);
 NF_API void nf_hip_get_gemv_max_m(uint32_t *f32_path, uint32_t *f16_path);
+NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path);
+NF_API uint32_t nf_hip_get_skinny_max_m(void);
 
 /* Dispatch `n_tasks` prepared task descriptors in order, `repeat` times —
  * a compiled step submitted with one call, the way Session::step walks its

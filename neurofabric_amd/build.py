@@ -34,6 +34,7 @@ HIP_SOURCES = [
     CSRC / "kernels" / "dequant.hip",
     CSRC / "kernels" / "gemv.hip",
     CSRC / "kernels" / "gemm.hip",
+    CSRC / "kernels" / "skinny.hip",
     CSRC / "kernels" / "generic.hip",
 ]
 CXX_SOURCES = [CSRC / "plan.cpp"]

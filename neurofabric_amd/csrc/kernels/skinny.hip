@@ -1,0 +1,453 @@
+// skinny.hip — fused dequant + matmul for small batches (2 <= M <= 64) on MFMA.
+//
+// C[m, n] = sum_k A[m, k] * deq(W)[n, k] with fp32 accumulation, for the
+// batch sizes between the decode GEMV (M = 1..2) and the prefill GEMM.  The
+// weight stream is read once; MFMA absorbs the per-row multiply so the cost
+// per weight stays flat in M.
+//
+// MFMA v_mfma_f32_16x16x32 (f16 or bf16 operands): A = activations (16 rows
+// of M), B = weights (16 rows of N), D[m][n] = sum over 32 k.  Lane l:
+//   A: row l%16, eight k values of slot s = l/16;
+//   B: weight row l%16, the same eight k values;
+//   D: weight row l%16, activation rows 4s..4s+3.
+// One instruction covers exactly one 32-element block.  Slot s holds the k
+// values a lane can unpack from one code word: Q4_0 slot s = qs[4s..4s+3],
+// i.e. k = 4s..4s+3 (low nibbles) and 16+4s..16+4s+3 (high nibbles); Q8_0
+// slot s = codes 8s..8s+7.  A is gathered in the same order.
+//
+// f16 activations (the _f16 op): B = RNE(d*q) in fp16 (the bits of
+// dequant_*_f16), one MFMA per block and tile, accumulated across blocks.
+//
+// f32 activations: each activation x is split exactly into three bf16 parts
+// (x = b1 + b2 + b3; 8 significand bits each, same exponent range as f32),
+// B = the integer codes (exact in bf16; Q4_0 nibbles come out of the fp8
+// e4m3 denormal range as n*u, u = 2^-9 or 2^-10), three chained MFMAs give
+// sum_k code*x exactly-multiplied and fp32-accumulated, and the block scale
+// is applied per block: acc += d/u * D.  The Q4_0 offset of -8 starts each
+// block's chain from sum_k (-8u)*x, one extra chain per activation tile that
+// all weight tiles share.
+//
+// Work split: a wave owns T tiles of 16 weight rows and a contiguous range of
+// 64-element pairs along K; the KS waves of a workgroup split K and add their
+// partial sums in LDS (ds_add_f32) before one wave stores C.  Each lane
+// fetches, per pair, only the dwords of its slot (all loads dword aligned);
+// the next pair's weights and activations are loaded before the current
+// pair is computed.
+#include "../launch.hpp"
+#include "common.hpp"
+
+namespace nfk {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float float2s __attribute__((ext_vector_type(2)));
+
+template <class QF> struct SkW;
+template <> struct SkW<Q4_0> {
+  static constexpr int kPairBytes = 36, kLoads = 5;
+};
+template <> struct SkW<Q8_0> {
+  static constexpr int kPairBytes = 68, kLoads = 7;
+};
+
+// The dwords of pair `p` of weight row `row` that slot s needs.
+template <class QF>
+__device__ __forceinline__ void sk_load_w(const uint32_t* __restrict__ pr, int s, uint32_t (&w)[SkW<QF>::kLoads]) {
+  if constexpr (SkW<QF>::kLoads == 5) {
+    w[0] = pr[s];      // block 0 codes, realigned with w[1]
+    w[1] = pr[s + 1];
+    w[2] = pr[5 + s];  // block 1 codes
+    w[3] = pr[0];      // block 0 scale (low half)
+    w[4] = pr[4];      // block 1 scale (high half)
+  } else {
+    w[0] = pr[2 * s];  // block 0 codes: bytes 2+8s .. 9+8s across three dwords
+    w[1] = pr[2 * s + 1];
+    w[2] = pr[2 * s + 2];
+    w[3] = pr[9 + 2 * s];   // block 1 codes
+    w[4] = pr[10 + 2 * s];
+    w[5] = pr[0];      // block 0 scale (low half)
+    w[6] = pr[8];      // block 1 scale (high half)
+  }
+}
+
+template <class QF>
+__device__ __forceinline__ uint32_t sk_scale_bits(const uint32_t (&w)[SkW<QF>::kLoads], int h) {
+  if constexpr (SkW<QF>::kLoads == 5) return h == 0 ? (w[3] & 0xFFFFu) : (w[4] >> 16);
+  else return h == 0 ? (w[5] & 0xFFFFu) : (w[6] >> 16);
+}
+
+__device__ __forceinline__ half2v h2u(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+__device__ __forceinline__ uint32_t u2h(half2v h) { return __builtin_bit_cast(uint32_t, h); }
+
+// B operand, f16 path: RNE(d*q) for the 8 k values of the lane's slot.
+template <class QF>
+__device__ __forceinline__ half8 sk_b_f16(const uint32_t (&w)[SkW<QF>::kLoads], int h) {
+  const uint32_t db = sk_scale_bits<QF>(w, h);
+  const half2v d2 = h2u(db | (db << 16));
+  u32x4 o;
+  if constexpr (SkW<QF>::kLoads == 5) {
+    const uint32_t q = h == 0 ? __builtin_amdgcn_alignbyte(w[1], w[0], 2) : w[2];
+    const uint32_t l = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+    const half2v off = {(half_t)-1032.f, (half_t)-1032.f};
+    o.x = u2h((h2u(__builtin_amdgcn_perm(0x64646464u, l, 0x04010400u)) + off) * d2);
+    o.y = u2h((h2u(__builtin_amdgcn_perm(0x64646464u, l, 0x04030402u)) + off) * d2);
+    o.z = u2h((h2u(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) + off) * d2);
+    o.w = u2h((h2u(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) + off) * d2);
+  } else {
+    const uint32_t qa = h == 0 ? __builtin_amdgcn_alignbyte(w[1], w[0], 2) : w[3];
+    const uint32_t qb = h == 0 ? __builtin_amdgcn_alignbyte(w[2], w[1], 2) : w[4];
+    const half2v off = {(half_t)-1152.f, (half_t)-1152.f};
+    const uint32_t ua = qa ^ 0x80808080u, ub = qb ^ 0x80808080u;
+    o.x = u2h((h2u(__builtin_amdgcn_perm(0x64646464u, ua, 0x04010400u)) + off) * d2);
+    o.y = u2h((h2u(__builtin_amdgcn_perm(0x64646464u, ua, 0x04030402u)) + off) * d2);
+    o.z = u2h((h2u(__builtin_amdgcn_perm(0x64646464u, ub, 0x04010400u)) + off) * d2);
+    o.w = u2h((h2u(__builtin_amdgcn_perm(0x64646464u, ub, 0x04030402u)) + off) * d2);
+  }
+  return __builtin_bit_cast(half8, o);
+}
+
+// Two floats -> their bf16 pair, exact when each float has <= 8 significant
+// bits (upper halves of the f32 patterns).
+__device__ __forceinline__ uint32_t pack_hi16(float a, float b) {
+  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, a), 0x07060302u);
+}
+
+// B operand, f32 path: the codes of the lane's slot as exact bf16 (Q4_0: n*u
+// with n the unsigned nibble; Q8_0: the signed code).
+template <class QF>
+__device__ __forceinline__ bf16x8 sk_b_codes(const uint32_t (&w)[SkW<QF>::kLoads], int h) {
+  u32x4 o;
+  if constexpr (SkW<QF>::kLoads == 5) {
+    const uint32_t q = h == 0 ? __builtin_amdgcn_alignbyte(w[1], w[0], 2) : w[2];
+    const uint32_t l = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+    const float2s a = __builtin_amdgcn_cvt_pk_f32_fp8(l, false);
+    const float2s b = __builtin_amdgcn_cvt_pk_f32_fp8(l, true);
+    const float2s c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+    const float2s e = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+    o.x = pack_hi16(a.x, a.y);
+    o.y = pack_hi16(b.x, b.y);
+    o.z = pack_hi16(c.x, c.y);
+    o.w = pack_hi16(e.x, e.y);
+  } else {
+    const uint32_t qa = h == 0 ? __builtin_amdgcn_alignbyte(w[1], w[0], 2) : w[3];
+    const uint32_t qb = h == 0 ? __builtin_amdgcn_alignbyte(w[2], w[1], 2) : w[4];
+    o.x = pack_hi16((float)(int8_t)qa, (float)(int8_t)(qa >> 8));
+    o.y = pack_hi16((float)(int8_t)(qa >> 16), (float)((int32_t)qa >> 24));
+    o.z = pack_hi16((float)(int8_t)qb, (float)(int8_t)(qb >> 8));
+    o.w = pack_hi16((float)(int8_t)(qb >> 16), (float)((int32_t)qb >> 24));
+  }
+  return __builtin_bit_cast(bf16x8, o);
+}
+
+// Activation slot values: the 8 k values of slot s in block h of pair p.
+template <class QF> struct SkK;
+template <> struct SkK<Q4_0> {  // k = 4s..4s+3 and 16+4s..16+4s+3
+  __device__ static int off0(int s) { return 4 * s; }
+  __device__ static int off1(int s) { return 16 + 4 * s; }
+};
+template <> struct SkK<Q8_0> {  // k = 8s..8s+7
+  __device__ static int off0(int s) { return 8 * s; }
+  __device__ static int off1(int s) { return 8 * s + 4; }
+};
+
+// Exact three-way bf16 split of 8 floats.
+__device__ __forceinline__ void split3(const float (&x)[8], bf16x8& p1, bf16x8& p2, bf16x8& p3) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float2s v = {x[2 * j], x[2 * j + 1]};
+    const bf16x2v h1 = __builtin_convertvector(v, bf16x2v);
+    const float2s r1 = v - __builtin_convertvector(h1, float2s);
+    const bf16x2v h2 = __builtin_convertvector(r1, bf16x2v);
+    const float2s r2 = r1 - __builtin_convertvector(h2, float2s);
+    const bf16x2v h3 = __builtin_convertvector(r2, bf16x2v);
+    p1[2 * j] = h1[0];
+    p1[2 * j + 1] = h1[1];
+    p2[2 * j] = h2[0];
+    p2[2 * j + 1] = h2[1];
+    p3[2 * j] = h3[0];
+    p3[2 * j + 1] = h3[1];
+  }
+}
+
+template <class QF, typename XT, int MT, int T>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) void skinny_kernel(
+    const XT* __restrict__ A, const uint8_t* __restrict__ W, XT* __restrict__ C, int M, int N, int K) {
+  constexpr bool kF32 = sizeof(XT) == 4;
+  constexpr bool kQ4 = SkW<QF>::kLoads == 5;
+  constexpr int WL = SkW<QF>::kLoads;
+  constexpr int PB = SkW<QF>::kPairBytes;
+  constexpr int RW = 16 * T;                // weight rows per wave
+  constexpr int CHP = 4;                    // pairs per chunk
+  constexpr int CB = CHP * PB / 16;         // 16-B pieces per row per chunk (9 / 17)
+  constexpr int J = RW * CB / 64;           // pieces per lane per chunk
+  constexpr int PITCH = CB * 4;             // dwords per staged row
+  static_assert(RW * CB % 64 == 0, "chunk pieces per lane");
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  // [wave][RW][PITCH] staged weight rows, then [MT*T*4][64] partial sums
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int KS = blockDim.x >> 6;
+  const int r16 = lane & 15, s = lane >> 4;
+  const int P = K >> 6;
+  const int NC = P / CHP;  // chunks along K (K % 256 == 0)
+  const int n0 = blockIdx.x * RW;
+  uint32_t* wst = smem + (size_t)wave * RW * PITCH;
+  float* red = reinterpret_cast<float*>(smem + (size_t)KS * RW * PITCH);
+
+  // K range of this wave (whole chunks)
+  const int c_begin = (int)((long)NC * wave / KS), c_end = (int)((long)NC * (wave + 1) / KS);
+
+  for (int i = tid; i < MT * T * 4 * 64; i += blockDim.x) red[i] = 0.f;
+
+  // Weight staging: piece f = lane + 64*j of the wave's RW x CB chunk is row
+  // f / CB, 16-B piece f % CB; consecutive lanes read consecutive bytes of a
+  // row.  Rows past N read row N-1 (their B operands are zeroed below).
+  const size_t row_bytes = (size_t)P * PB;
+  const uint8_t* wsrc[J];
+  int wdst[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int f = lane + 64 * j;
+    const int row = f / CB, pc = f % CB;
+    const int n = n0 + row < N ? n0 + row : N - 1;
+    wsrc[j] = W + (size_t)n * row_bytes + pc * 16;
+    wdst[j] = row * PITCH + pc * 4;
+  }
+  bool wvalid[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) wvalid[t] = n0 + 16 * t + r16 < N;
+
+  // Activation rows past M read row 0: an activation row only feeds its own
+  // output row, and output rows past M are never stored, so no masking.
+  const XT* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r16;
+    xrow[mt] = A + (size_t)(m < M ? m : 0) * K;
+  }
+
+  typedef float XBuf[MT][2][8];
+  typedef uint32_t HBuf[MT][2][4];
+  auto load_x32 = [&](int p, XBuf& xb) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float* base = reinterpret_cast<const float*>(xrow[mt]) + p * 64 + h * 32;
+        const float4v v0 = *reinterpret_cast<const float4v*>(base + SkK<QF>::off0(s));
+        const float4v v1 = *reinterpret_cast<const float4v*>(base + SkK<QF>::off1(s));
+        xb[mt][h][0] = v0.x; xb[mt][h][1] = v0.y; xb[mt][h][2] = v0.z; xb[mt][h][3] = v0.w;
+        xb[mt][h][4] = v1.x; xb[mt][h][5] = v1.y; xb[mt][h][6] = v1.z; xb[mt][h][7] = v1.w;
+      }
+  };
+  auto load_x16 = [&](int p, HBuf& xb) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const half_t* base = reinterpret_cast<const half_t*>(xrow[mt]) + p * 64 + h * 32;
+        const uint2 v0 = *reinterpret_cast<const uint2*>(base + SkK<QF>::off0(s));
+        const uint2 v1 = *reinterpret_cast<const uint2*>(base + SkK<QF>::off1(s));
+        xb[mt][h][0] = v0.x; xb[mt][h][1] = v0.y; xb[mt][h][2] = v1.x; xb[mt][h][3] = v1.y;
+      }
+  };
+  // The slot dwords of staged pair pi (of the chunk) of tile t's row r16.
+  auto read_w = [&](int pi, int t, uint32_t (&w)[WL]) {
+    const uint32_t* pr = wst + (16 * t + r16) * PITCH + pi * (PB / 4);
+    if constexpr (WL == 5) {
+      w[0] = pr[s]; w[1] = pr[s + 1]; w[2] = pr[5 + s]; w[3] = pr[0]; w[4] = pr[4];
+    } else {
+      w[0] = pr[2 * s]; w[1] = pr[2 * s + 1]; w[2] = pr[2 * s + 2];
+      w[3] = pr[9 + 2 * s]; w[4] = pr[10 + 2 * s]; w[5] = pr[0]; w[6] = pr[8];
+    }
+  };
+
+  float4v acc[MT][T];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[mt][t] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1u, false)[0];
+  const float inv_unit = 1.0f / unit;
+
+  auto compute_f32 = [&](int pi, const XBuf& xc) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 a1[MT], a2[MT], a3[MT];
+      float4v base[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        split3(xc[mt][h], a1[mt], a2[mt], a3[mt]);
+        base[mt] = float4v{0.f, 0.f, 0.f, 0.f};
+        if constexpr (kQ4) {
+          // sum_k (-8u) * x, the nibble offset, shared by all weight tiles
+          const __bf16 c8 = (__bf16)(-8.0f * unit);
+          const bf16x8 bc = {c8, c8, c8, c8, c8, c8, c8, c8};
+          base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], bc, base[mt], 0, 0, 0);
+          base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[mt], bc, base[mt], 0, 0, 0);
+          base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[mt], bc, base[mt], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        uint32_t w[WL];
+        read_w(pi, t, w);
+        const bf16x8 b = sk_b_codes<QF>(w, h);
+        float d = h2f_bits((uint16_t)sk_scale_bits<QF>(w, h));
+        if constexpr (kQ4) d *= inv_unit;
+        if (!wvalid[t]) d = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          float4v dd = base[mt];
+          dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], b, dd, 0, 0, 0);
+          dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[mt], b, dd, 0, 0, 0);
+          dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[mt], b, dd, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mt][t][i] = __builtin_fmaf(d, dd[i], acc[mt][t][i]);
+        }
+      }
+    }
+  };
+  auto compute_f16 = [&](int pi, const HBuf& xc) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        uint32_t w[WL];
+        read_w(pi, t, w);
+        half8 b = sk_b_f16<QF>(w, h);
+        if (!wvalid[t]) b = half8{};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4 av = {xc[mt][h][0], xc[mt][h][1], xc[mt][h][2], xc[mt][h][3]};
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, av), b, acc[mt][t], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  // Chunk loop (uniform trip count): the staged registers of chunk c are
+  // written to LDS, chunk c+1 (clamped to the last chunk) is fetched into the
+  // same registers, and chunk c is computed from LDS with the activations of
+  // the next pair loaded one pair ahead.
+  if (c_begin < c_end) {
+    u32x4 wr[J];
+    auto fetch = [&](int c) {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        wr[j] = *reinterpret_cast<const u32x4*>(wsrc[j] + (size_t)c * CHP * PB);
+    };
+    fetch(c_begin);
+    for (int c = c_begin; c < c_end; ++c) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) *reinterpret_cast<u32x4*>(wst + wdst[j]) = wr[j];
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(c + 1 < c_end ? c + 1 : c);
+      __builtin_amdgcn_sched_barrier(0);
+      const int p0 = c * CHP;
+      if constexpr (kF32) {
+        XBuf x0, x1;
+        load_x32(p0, x0);
+#pragma unroll
+        for (int pi = 0; pi < CHP; pi += 2) {
+          load_x32(p0 + pi + 1, x1);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_f32(pi, x0);
+          __builtin_amdgcn_sched_barrier(0);
+          if (pi + 2 < CHP) load_x32(p0 + pi + 2, x0);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_f32(pi + 1, x1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        HBuf x0, x1;
+        load_x16(p0, x0);
+#pragma unroll
+        for (int pi = 0; pi < CHP; pi += 2) {
+          load_x16(p0 + pi + 1, x1);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_f16(pi, x0);
+          __builtin_amdgcn_sched_barrier(0);
+          if (pi + 2 < CHP) load_x16(p0 + pi + 2, x0);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_f16(pi + 1, x1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  }
+
+  // combine the KS partial sums in LDS, then wave 0 stores
+  __syncthreads();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) atomicAdd(&red[((mt * T + t) * 4 + i) * 64 + lane], acc[mt][t][i]);
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int n = n0 + 16 * t + r16;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 16 * mt + 4 * s + i;
+          if (m < M) C[(size_t)m * N + n] = (XT)red[((mt * T + t) * 4 + i) * 64 + lane];
+        }
+      }
+  }
+}
+
+template <class QF, typename XT, int MT, int T>
+hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
+                         hipStream_t s) {
+  constexpr int RW = 16 * T, PITCH = 4 * SkW<QF>::kPairBytes / 4;  // 4 pairs per staged row
+  const long wgs = ((long)N + RW - 1) / RW;
+  const int NC = (int)(K / 256);
+  // K split: enough waves to give every CU several, at most 8 per workgroup
+  // and at least two chunks per wave.
+  int ks = 1;
+  while (ks < 8 && wgs * ks < 2048 && NC / (ks * 2) >= 2) ks *= 2;
+  const size_t lds = (size_t)ks * RW * PITCH * 4 + (size_t)MT * T * 4 * 64 * sizeof(float);
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_kernel<QF, XT, MT, T>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  skinny_kernel<QF, XT, MT, T><<<dim3((unsigned)wgs), dim3(64 * ks), lds, s>>>(
+      static_cast<const XT*>(A), static_cast<const uint8_t*>(W), static_cast<XT*>(C), (int)M, (int)N, (int)K);
+  return hipGetLastError();
+}
+
+template <class QF, typename XT>
+hipError_t skinny_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
+                           hipStream_t s) {
+  if (M <= 16) return skinny_launch<QF, XT, 1, 4>(A, W, C, M, N, K, s);
+  if (M <= 32 || sizeof(XT) == 4) return skinny_launch<QF, XT, 2, 4>(A, W, C, M, N, K, s);
+  return skinny_launch<QF, XT, 4, 4>(A, W, C, M, N, K, s);
+}
+
+}  // namespace nfk
+
+namespace nfhip {
+
+bool skinny_fits(uint32_t M, uint32_t K, const void* A, const void* W) {
+  return M >= 1 && M <= 64 && K % 256 == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)W % 16 == 0;
+}
+
+uint32_t skinny_max_rows(EType t) { return t == EType::F32 ? 32u : 64u; }
+
+hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M, uint32_t N,
+                         uint32_t K, hipStream_t s) {
+  if (q == QFmt::Q4_0)
+    return t == EType::F32 ? nfk::skinny_dispatch<nfk::Q4_0, float>(A, W, C, M, N, K, s)
+                           : nfk::skinny_dispatch<nfk::Q4_0, nfk::half_t>(A, W, C, M, N, K, s);
+  return t == EType::F32 ? nfk::skinny_dispatch<nfk::Q8_0, float>(A, W, C, M, N, K, s)
+                         : nfk::skinny_dispatch<nfk::Q8_0, nfk::half_t>(A, W, C, M, N, K, s);
+}
+
+}  // namespace nfhip

@@ -131,13 +131,20 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
       p.path = Path::Generic;
       p.kernel = "generic_" + tag;
     } else {
-      const uint32_t max_m = (p.c == EType::F16) ? tuning.gemv_max_m_f16 : tuning.gemv_max_m_f32;
-      if (p.M <= max_m) {
+      const bool f16 = p.c == EType::F16;
+      const uint32_t gemv_max = f16 ? tuning.gemv_max_m_f16 : tuning.gemv_max_m_f32;
+      if (p.M <= gemv_max) {
         p.path = Path::Gemv;
         p.kernel = "gemv_" + tag;
-      } else {
+      } else if (K % 256 == 0 && (!f16 || p.M <= tuning.skinny_max_m_f16)) {
+        p.path = Path::Skinny;
+        p.kernel = "skinny_mfma_" + tag;
+      } else if (f16) {
         p.path = Path::GemmMfma;
         p.kernel = "gemm_mfma_" + tag;
+      } else {
+        p.path = Path::Gemv;  // f32 with K % 256 != 0
+        p.kernel = "gemv_" + tag;
       }
     }
     *plan = p;

@@ -18,17 +18,21 @@ enum class QFmt { None, Q4_0, Q8_0 };
 enum class EType { F32, F16 };
 enum class Path {
   Dequant,   // standalone dequantization
-  Gemv,      // skinny kernel (decode), M <= crossover
-  GemmMfma,  // LDS-tiled MFMA kernel (prefill), M > crossover
+  Gemv,      // VALU decode kernel, M <= gemv crossover
+  Skinny,    // small-batch MFMA kernel, gemv crossover < M <= skinny crossover
+  GemmMfma,  // LDS-tiled MFMA kernel (prefill, f16), M > skinny crossover
   Generic,   // flat-index fallback for K % 32 != 0
   Dense      // dense linear (weights already dequantized)
 };
 
-// Default switch points (M <= max_m runs the skinny kernels).  The f32 path
-// has no MFMA kernel yet, so every M stays on the skinny kernels.
+// Switch points between the kernel families of the fused op: the VALU GEMV
+// while M <= gemv_max_m, the small-batch MFMA kernel while M <= skinny_max_m
+// (the f32 path stays there for every larger M, 64 rows per launch), the
+// tiled MFMA GEMM above (f16).  Defaults from the measured sweep.
 struct Tuning {
-  uint32_t gemv_max_m_f32 = 0xFFFFFFFFu;
-  uint32_t gemv_max_m_f16 = 16;
+  uint32_t gemv_max_m_f32 = 2;
+  uint32_t gemv_max_m_f16 = 2;
+  uint32_t skinny_max_m_f16 = 64;
 };
 
 struct Plan {

@@ -400,6 +400,23 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, hipSt
       return launch_dequant(pl.q, pl.c, in[0]->dev, out[0]->dev, pl.count, s);
     case Path::Gemv:
       return launch_gemv(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
+    case Path::Skinny: {
+      if (!skinny_fits(1, pl.K, in[0]->dev, in[1]->dev))  // odd alignment (imported buffers)
+        return pl.c == EType::F16
+                   ? launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s)
+                   : launch_gemv(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
+      // at most skinny_max_rows activation rows per launch
+      const size_t ea = pl.a == EType::F16 ? 2 : 4, ec = pl.c == EType::F16 ? 2 : 4;
+      const uint32_t rows = skinny_max_rows(pl.c);
+      for (uint32_t m0 = 0; m0 < pl.M; m0 += rows) {
+        const uint32_t mc = pl.M - m0 < rows ? pl.M - m0 : rows;
+        const hipError_t e = launch_skinny(pl.q, pl.c, static_cast<const char*>(in[0]->dev) + (size_t)m0 * pl.K * ea,
+                                           in[1]->dev, static_cast<char*>(out[0]->dev) + (size_t)m0 * pl.N * ec, mc,
+                                           pl.N, pl.K, s);
+        if (e != hipSuccess) return e;
+      }
+      return hipSuccess;
+    }
     case Path::GemmMfma:
       return launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
     case Path::Generic:
@@ -613,6 +630,7 @@ NF_API nf_status nf_plugin_register(nf_provider_vtable* vt, nf_provider* out) {
   vt->synchronize = hip_synchronize;
   g_prov.tuning.gemv_max_m_f32 = env_u32("NF_HIP_GEMV_MAX_M_F32", g_prov.tuning.gemv_max_m_f32);
   g_prov.tuning.gemv_max_m_f16 = env_u32("NF_HIP_GEMV_MAX_M_F16", g_prov.tuning.gemv_max_m_f16);
+  g_prov.tuning.skinny_max_m_f16 = env_u32("NF_HIP_SKINNY_MAX_M_F16", g_prov.tuning.skinny_max_m_f16);
   *out = reinterpret_cast<nf_provider>(&g_prov);
   return NF_OK;
 }
@@ -701,6 +719,13 @@ NF_API void nf_hip_set_gemv_max_m(uint32_t f32_path, uint32_t f16_path) {
   g_prov.tuning.gemv_max_m_f32 = f32_path;
   g_prov.tuning.gemv_max_m_f16 = f16_path;
 }
+
+NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  g_prov.tuning.skinny_max_m_f16 = f16_path;
+}
+
+NF_API uint32_t nf_hip_get_skinny_max_m(void) { return g_prov.tuning.skinny_max_m_f16; }
 
 NF_API void nf_hip_get_gemv_max_m(uint32_t* f32_path, uint32_t* f16_path) {
   if (f32_path) *f32_path = g_prov.tuning.gemv_max_m_f32;

@@ -63,6 +63,10 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     lib.nf_hip_set_gemv_max_m.restype = None
     lib.nf_hip_get_gemv_max_m.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]
     lib.nf_hip_get_gemv_max_m.restype = None
+    lib.nf_hip_set_skinny_max_m.argtypes = [C.c_uint32]
+    lib.nf_hip_set_skinny_max_m.restype = None
+    lib.nf_hip_get_skinny_max_m.argtypes = []
+    lib.nf_hip_get_skinny_max_m.restype = C.c_uint32
     lib.nf_hip_get_stream.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
     lib.nf_hip_get_stream.restype = C.c_int
     lib.nf_hip_run_tasks.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32]
@@ -298,6 +302,12 @@ class Provider:
     # -- crossover ------------------------------------------------------
     def set_gemv_max_m(self, f32: int, f16: int) -> None:
         self.lib.nf_hip_set_gemv_max_m(f32, f16)
+
+    def set_skinny_max_m(self, f16: int) -> None:
+        self.lib.nf_hip_set_skinny_max_m(f16)
+
+    def get_skinny_max_m(self) -> int:
+        return self.lib.nf_hip_get_skinny_max_m()
 
     def get_gemv_max_m(self):
         a, b = C.c_uint32(), C.c_uint32()

@@ -95,25 +95,76 @@ def test_config2_prefill_sampled_columns(provider, oracle_mod, M, N, K):
     check_fused(provider, oracle_mod, "q4_0", M, N, K, f16=True, seed=K, cols=(N - 256, N), threads=8)
 
 
-@pytest.mark.parametrize("f16", [True], ids=["f16"])
-def test_gemv_and_mfma_paths_agree(provider, oracle_mod, f16):
-    """The same input through the skinny and the MFMA kernel (switch point
-    forced both ways) agrees with the oracle."""
-    M, N, K = 24, 384, 1024
-    old = provider.get_gemv_max_m()
+def _force_path(provider, path, f16):
+    """Pin the switch points so `path` ('gemv', 'skinny', 'tiled') serves every M."""
+    g32, g16 = provider.get_gemv_max_m()
+    if path == "gemv":
+        provider.set_gemv_max_m(1 << 30, 1 << 30)
+    elif path == "skinny":
+        provider.set_gemv_max_m(0, 0)
+        provider.set_skinny_max_m(1 << 30)
+    else:
+        provider.set_gemv_max_m(0, 0)
+        provider.set_skinny_max_m(0)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("M", [3, 24, 64, 100])
+def test_kernel_paths_agree(provider, oracle_mod, fmt, f16, M):
+    """The same inputs through every kernel family that serves the op (GEMV,
+    small-batch MFMA, and for f16 the tiled MFMA GEMM) each match the oracle
+    within the tolerance; N and M are not multiples of any tile."""
+    N, K = 392, 1024
+    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    W = syn.weights(fmt, N, K, seed=3 + M)
+    A = syn.activations(M, K, seed=4 + M, dtype=np.float16 if f16 else np.float32)
+    ref = oracle_mod.fused(A, W, fmt, M, N, K, f16=f16)
+    ref = (ref.view(np.float16) if f16 else ref).astype(np.float32)
     try:
-        outs = []
-        for max_m in (1 << 30, 1):
-            provider.set_gemv_max_m(max_m if not f16 else old[0], max_m if f16 else old[1])
-            W = syn.q4_0_weights(N, K, seed=3)
-            A = syn.activations(M, K, seed=4, dtype=np.float16 if f16 else np.float32)
-            outs.append(run_fused(provider, "q4_0", A, W, M, N, K, f16).astype(np.float32))
-        ref = oracle_mod.fused(A, W, "q4_0", M, N, K, f16=f16)
-        ref = (ref.view(np.float16) if f16 else ref).astype(np.float32)
-        for o in outs:
-            assert_close(o, ref)
+        for path in ("gemv", "skinny", "tiled") if f16 else ("gemv", "skinny"):
+            _force_path(provider, path, f16)
+            got = run_fused(provider, fmt, A, W, M, N, K, f16).astype(np.float32)
+            assert_close(got, ref, what=f"{path} {fmt} f16={f16} M={M}")
     finally:
-        provider.set_gemv_max_m(*old)
+        provider.set_gemv_max_m(*old[0])
+        provider.set_skinny_max_m(old[1])
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("shape", [(2, 200, 256), (8, 1000, 768), (16, 64, 4096), (17, 257, 2048),
+                                   (33, 130, 512), (64, 96, 1024), (130, 72, 256), (5, 40, 192)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_skinny_mfma_shapes(provider, oracle_mod, fmt, f16, shape):
+    """Small-batch MFMA kernel at ragged M/N, short and long K (the per-wave
+    K split and the LDS combine), rows beyond one launch (32 for f32, 64 for
+    f16); K % 256 != 0 falls back to the GEMV."""
+    M, N, K = shape
+    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    try:
+        _force_path(provider, "skinny", f16)
+        check_fused(provider, oracle_mod, fmt, M, N, K, f16=f16, seed=M * 7 + N)
+    finally:
+        provider.set_gemv_max_m(*old[0])
+        provider.set_skinny_max_m(old[1])
+
+
+def test_skinny_f32_large_activations(provider, oracle_mod):
+    """The exact three-way bf16 split keeps f32 activations far outside the
+    fp16 range (|x| ~ 1e6 and 1e-6) exact before accumulation."""
+    M, N, K = 8, 128, 512
+    W = syn.q4_0_weights(N, K, seed=11)
+    rng = np.random.default_rng(5)
+    A = (rng.standard_normal((M, K)) * np.where(rng.random((M, K)) < 0.5, 1e6, 1e-6)).astype(np.float32)
+    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    try:
+        _force_path(provider, "skinny", False)
+        got = run_fused(provider, "q4_0", A, W, M, N, K, False)
+    finally:
+        provider.set_gemv_max_m(*old[0])
+        provider.set_skinny_max_m(old[1])
+    assert_close(got, oracle_mod.fused(A, W, "q4_0", M, N, K))
 
 
 # ---- the reference's fused-vs-separate test (fused_matmul_test.cpp:134-285) ----------
@@ -200,6 +251,25 @@ def test_dense_linear_tiled_reference_case(provider, oracle_mod):
     provider.dispatch("linear_tiled", [a, b], [c], M, N, K)
     got = c.download(np.float32).reshape(M, N)
     assert_close(got, oracle_mod.linear_f32(A, B, M, N, K))
+    for x in (a, b, c):
+        x.release()
+
+
+@pytest.mark.parametrize("shape", [(32, 136, 128), (300, 1000, 4096), (1024, 256, 640)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_dense_linear_f16_mfma(provider, oracle_mod, shape):
+    """f16 x f16 -> f16 dense linear on the tiled MFMA kernel (B rows streamed
+    into LDS like A), ragged M/N."""
+    M, N, K = shape
+    rng = np.random.default_rng(M + N)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B = rng.standard_normal((N, K)).astype(np.float16)
+    a, b = provider.alloc_array(A, abi.NF_DTYPE_F16), provider.alloc_array(B, abi.NF_DTYPE_F16)
+    c = provider.alloc(abi.NF_DTYPE_F16, M * N * 2)
+    provider.dispatch("linear", [a, b], [c], M, N, K)
+    got = c.download(np.float16).reshape(M, N).astype(np.float32)
+    ref = oracle_mod.linear_f16(A.view(np.uint16), B.view(np.uint16), M, N, K).view(np.float16).astype(np.float32)
+    assert_close(got, ref)
     for x in (a, b, c):
         x.release()
 

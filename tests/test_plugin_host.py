@@ -120,9 +120,17 @@ def test_plan_path_follows_output_dtype(lib):
 
 
 def test_plan_q8_0_and_ragged_k(lib):
+    p = plan(lib, "dequant_q8_0_linear", [D(abi.NF_DTYPE_F32, 4 * 256 * 4), D(abi.NF_DTYPE_Q8_0, 7 * 8 * 34)],
+             [D(abi.NF_DTYPE_F32, 4 * 7 * 4)], 4, 7, 256)
+    assert p["kernel"] == "skinny_mfma_q8_0_f32" and p["weight_bytes"] == 7 * 8 * 34
+    # K % 256 != 0: the small-batch MFMA kernel stages four block pairs at a time
     p = plan(lib, "dequant_q8_0_linear", [D(abi.NF_DTYPE_F32, 4 * 64 * 4), D(abi.NF_DTYPE_Q8_0, 7 * 2 * 34)],
              [D(abi.NF_DTYPE_F32, 4 * 7 * 4)], 4, 7, 64)
-    assert p["kernel"] == "gemv_q8_0_f32" and p["weight_bytes"] == 7 * 2 * 34
+    assert p["kernel"] == "gemv_q8_0_f32"
+    # K % 64 == 32: the block-granular GEMV kernel for f32 at any M
+    p = plan(lib, "dequant_q8_0_linear", [D(abi.NF_DTYPE_F32, 4 * 96 * 4), D(abi.NF_DTYPE_Q8_0, 7 * 3 * 34)],
+             [D(abi.NF_DTYPE_F32, 4 * 7 * 4)], 4, 7, 96)
+    assert p["kernel"] == "gemv_q8_0_f32"
     p = _fused(lib, 2, 5, 48, w_bytes=(5 * 48 + 31) // 32 * 18)
     assert p["kernel"] == "generic_q4_0_f32"
 
@@ -186,9 +194,33 @@ def test_crossover_setter_roundtrip():
     try:
         prov.set_gemv_max_m(3, 5)
         assert prov.get_gemv_max_m() == (3, 5)
-        p = _fused(prov.lib, 4, 64, 64, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)
+        p = _fused(prov.lib, 4, 64, 256, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)
         assert p["kernel"] == "gemv_q4_0_f16"
-        p = _fused(prov.lib, 6, 64, 64, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)
-        assert p["kernel"] == "gemm_mfma_q4_0_f16"
+        p = _fused(prov.lib, 6, 64, 256, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)
+        assert p["kernel"] == "skinny_mfma_q4_0_f16"
+        p = _fused(prov.lib, 6, 64, 256)
+        assert p["kernel"] == "skinny_mfma_q4_0_f32"
     finally:
         prov.set_gemv_max_m(*old)
+    old_s = prov.get_skinny_max_m()
+    try:
+        prov.set_skinny_max_m(5)
+        assert prov.get_skinny_max_m() == 5
+        p = _fused(prov.lib, 6, 64, 256, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)
+        assert p["kernel"] == "gemm_mfma_q4_0_f16"
+        # f32 activations have no tiled GEMM: every M above the GEMV stays skinny
+        assert _fused(prov.lib, 600, 64, 256)["kernel"] == "skinny_mfma_q4_0_f32"
+    finally:
+        prov.set_skinny_max_m(old_s)
+
+
+def test_default_switch_points(lib):
+    """Defaults from the configs[4] sweep: GEMV for M <= 2, the small-batch
+    MFMA kernel up to 64 rows, the tiled GEMM beyond (f16)."""
+    f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
+    assert _fused(lib, 2, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"
+    assert _fused(lib, 3, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
+    assert _fused(lib, 64, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
+    assert _fused(lib, 65, 28672, 8192, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
+    assert _fused(lib, 2, 4096, 4096)["kernel"] == "gemv_q4_0_f32"
+    assert _fused(lib, 16, 4096, 4096)["kernel"] == "skinny_mfma_q4_0_f32"
