@@ -71,6 +71,8 @@ def parse(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--sweep", action="store_true", help="configs[4] GEMV/MFMA crossover sweep")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
+    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4"], default=None,
+                    help="run one configs[i] section alone and print its JSON (profiling aid)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 4 device-to-device copies of BYTES (reference for HBM byte counters)")
     return ap.parse_args(argv)
@@ -325,6 +327,56 @@ def crossover_sweep(prov, N=28672, K=8192, Ms=(1, 2, 3, 4, 8, 16, 32, 64, 128, 2
             "fastest_by_M": {r["M"]: r["fastest"] for r in rows}}
 
 
+def run_c0(prov, mode: str) -> dict:
+    """one 5632x2048 Q4_0 GEMV over 80 rotated weight copies
+    (519 MB > 2x the Infinity Cache)."""
+    s0 = rotated_linear(prov, "q4_0", 1, 5632, 2048, False, 80)
+    r0 = time_step(prov, s0, 20, 3, mode)
+    d0 = time_dispatches(prov, s0, 6)
+    out = {"GB_s_step": s0.bytes / (r0["ms_per_step"] * 1e-3) / 1e9,
+           "us_per_launch_step": r0["us_per_launch"],
+           "us_per_launch_kernel": d0["mean_launch_us"],
+           "GB_s_kernel": s0.bytes / len(s0.tasks) / (d0["mean_launch_us"] * 1e-6) / 1e9,
+           "kernels": sorted(s0.kernels)}
+    log(f"[bench] C0: {out}")
+    s0.release()
+    return out
+
+
+def run_c3(prov, mode: str) -> dict:
+    """Llama-3-8B Q8_0 decode step (32 layers + lm_head) at M=1/16/64."""
+    c3 = {}
+    llama3 = WeightSet(prov, llama3_q8_step_shapes(), "q8_0")
+    for M in (1, 16, 64):
+        s3 = model_step(prov, llama3, M)
+        r3 = time_step(prov, s3, 10, 2, mode)
+        c3[f"m{M}"] = {"GB_s": s3.bytes / (r3["ms_per_step"] * 1e-3) / 1e9,
+                       "us_per_step": r3["ms_per_step"] * 1e3,
+                       "tokens_per_s": M / (r3["ms_per_step"] * 1e-3),
+                       "weight_GB_per_step": s3.weight_bytes / 1e9, "kernels": sorted(s3.kernels)}
+        log(f"[bench] C3 Q8_0 decode M={M}: {c3[f'm{M}']}")
+        s3.release()
+    llama3.release()
+    return c3
+
+
+def run_c2(prov) -> dict:
+    """Llama-2-7B Q4_0 prefill GEMMs, f16 activations, 4 rotated
+    weight copies per shape."""
+    pre = {}
+    for (name, N, K) in [("qkvo_4096x4096", 4096, 4096), ("gate_up_11008x4096", 11008, 4096),
+                         ("down_4096x11008", 4096, 11008)]:
+        for M in (512, 2048):
+            sp = rotated_linear(prov, "q4_0", M, N, K, True, 4)
+            rp = time_step(prov, sp, 5, 2, "eager")
+            tf = sp.flops / (rp["ms_per_step"] * 1e-3) / 1e12
+            pre[f"{name}_m{M}"] = {"TFLOP_s": tf, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS,
+                                   "us_per_launch": rp["us_per_launch"], "kernels": sorted(sp.kernels)}
+            log(f"[bench] prefill {name} M={M}: {tf:.1f} TFLOP/s")
+            sp.release()
+    return pre
+
+
 def load_pmc_summary():
     if PMC_SUMMARY.exists():
         try:
@@ -349,6 +401,11 @@ def main(argv=None) -> int:
     from neurofabric_amd.plugin import Provider
     prov = Provider()
     prov.init()
+    if args.only:
+        sections = {"c0": lambda: run_c0(prov, args.mode), "c2": lambda: run_c2(prov),
+                    "c3": lambda: run_c3(prov, args.mode), "c4": lambda: crossover_sweep(prov)}
+        print(json.dumps({args.only: sections[args.only]()}), flush=True)
+        return 0
 
     log(f"[bench] headline: configs[1] decode step M={args.m} mode={args.mode}")
     tiny = WeightSet(prov, syn.tinyllama_step_shapes(), "q4_0")
@@ -390,44 +447,9 @@ def main(argv=None) -> int:
             s2.release()
     tiny.release()
     if not args.no_extra:
-        # one GEMV shape, 80 rotated copies (519 MB > 2x MALL)
-        s0 = rotated_linear(prov, "q4_0", 1, 5632, 2048, False, 80)
-        r0 = time_step(prov, s0, 20, 3, args.mode)
-        d0 = time_dispatches(prov, s0, 6)
-        extra["c0_gemv_5632x2048"] = {"GB_s_step": s0.bytes / (r0["ms_per_step"] * 1e-3) / 1e9,
-                                      "us_per_launch_step": r0["us_per_launch"],
-                                      "us_per_launch_kernel": d0["mean_launch_us"],
-                                      "GB_s_kernel": s0.bytes / len(s0.tasks) / (d0["mean_launch_us"] * 1e-6) / 1e9,
-                                      "kernels": sorted(s0.kernels)}
-        log(f"[bench] C0: {extra['c0_gemv_5632x2048']}")
-        s0.release()
-        # Llama-3-8B Q8_0 decode step, 32 layers + lm_head
-        c3 = {}
-        llama3 = WeightSet(prov, llama3_q8_step_shapes(), "q8_0")
-        for M in (1, 16, 64):
-            s3 = model_step(prov, llama3, M)
-            r3 = time_step(prov, s3, 10, 2, args.mode)
-            c3[f"m{M}"] = {"GB_s": s3.bytes / (r3["ms_per_step"] * 1e-3) / 1e9,
-                           "us_per_step": r3["ms_per_step"] * 1e3,
-                           "tokens_per_s": M / (r3["ms_per_step"] * 1e-3),
-                           "weight_GB_per_step": s3.weight_bytes / 1e9, "kernels": sorted(s3.kernels)}
-            log(f"[bench] C3 Q8_0 decode M={M}: {c3[f'm{M}']}")
-            s3.release()
-        llama3.release()
-        extra["c3_llama3_8b_q8_0_decode"] = c3
-        # Llama-2-7B prefill GEMMs
-        pre = {}
-        for (name, N, K) in [("qkvo_4096x4096", 4096, 4096), ("gate_up_11008x4096", 11008, 4096),
-                             ("down_4096x11008", 4096, 11008)]:
-            for M in (512, 2048):
-                sp = rotated_linear(prov, "q4_0", M, N, K, True, 4)
-                rp = time_step(prov, sp, 5, 2, "eager")
-                tf = sp.flops / (rp["ms_per_step"] * 1e-3) / 1e12
-                pre[f"{name}_m{M}"] = {"TFLOP_s": tf, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS,
-                                       "us_per_launch": rp["us_per_launch"], "kernels": sorted(sp.kernels)}
-                log(f"[bench] prefill {name} M={M}: {tf:.1f} TFLOP/s")
-                sp.release()
-        extra["c2_prefill_f16"] = pre
+        extra["c0_gemv_5632x2048"] = run_c0(prov, args.mode)
+        extra["c3_llama3_8b_q8_0_decode"] = run_c3(prov, args.mode)
+        extra["c2_prefill_f16"] = run_c2(prov)
     if args.sweep:
         extra["c4_crossover"] = crossover_sweep(prov)
 

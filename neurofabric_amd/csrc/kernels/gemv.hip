@@ -47,6 +47,8 @@
 //
 // Block kernel (fallback for K % 64 == 32): one wave per output row, lanes
 // stride over the row's 32-element blocks.
+#include <cstdlib>
+
 #include "../launch.hpp"
 #include "common.hpp"
 
@@ -105,10 +107,13 @@ template <> struct XChunk<half_t> {
   static constexpr int kPerPair = 8, kElems = 8;
 };
 
+// Chunk c of activation pair gp = m * P + pair (the pair's index over all
+// M rows) lives at slot gp * cp + (c ^ (gp & (cp - 1))).
 template <typename XT>
 __device__ __forceinline__ int xslot(int m, int P, int pair, int c) {
   constexpr int cp = XChunk<XT>::kPerPair;
-  return (m * P + pair) * cp + (c ^ (pair & (cp - 1)));
+  const int gp = m * P + pair;
+  return gp * cp + (c ^ (gp & (cp - 1)));
 }
 
 // ---- per-pair compute -----------------------------------------------------
@@ -311,6 +316,7 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   constexpr bool kSx = kF32 && kQ4;  // block sums of x needed for the nibble offset
   constexpr int CP = XChunk<XT>::kPerPair;
   constexpr int EPC = XChunk<XT>::kElems;
+  constexpr int DW = PairFmt<QF>::kDwords;
   typedef typename XChunk<XT>::T ChunkT;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
@@ -329,99 +335,136 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   const int rows_per_pass = 4 * R * R2;
   const int pass_stride = gridDim.x * rows_per_pass;
   const size_t row_bytes = (size_t)P * PairFmt<QF>::kBytes;
-  constexpr int DW = PairFmt<QF>::kDwords;
 
-  // Weights of (row r0.., pair) into w; rows beyond N read as zero.
-  auto load = [&](int r0, int pair, uint32_t (&w)[R2][DW]) {
+  // Iteration space of a lane group: npass passes over the grid's rows, IP
+  // pair steps per pass (pair = li + L * step).  Both are uniform across the
+  // workgroup, so every lane runs the same straight-line loop; loads past
+  // the end are clamped to the last row / pair and never stored.
+  const int base0 = blockIdx.x * rows_per_pass;
+  const int grp_row = base0 + (wave * R + g) * R2;
+  const int IP = (P + L - 1) >> log2L;
+  const int npass = base0 < N ? (N - 1 - base0) / pass_stride + 1 : 0;
+  const int T = npass * IP;
+
+  int lpass = 0, lk = 0;  // position of the next weight load
+  auto next_load = [&](uint32_t (&w)[R2][DW]) {
+    const int r0 = grp_row + lpass * pass_stride;
+    int pair = li + (lk << log2L);
+    pair = pair < P ? pair : P - 1;
 #pragma unroll
     for (int j = 0; j < R2; ++j) {
-      if (r0 + j < N) {
-        load_pair<QF>(W + (size_t)(r0 + j) * row_bytes + (size_t)pair * PairFmt<QF>::kBytes, w[j]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < DW; ++i) w[j][i] = 0u;
-      }
+      const int r = r0 + j < N ? r0 + j : N - 1;
+      load_pair<QF>(W + (size_t)r * row_bytes + (size_t)pair * PairFmt<QF>::kBytes, w[j]);
+    }
+    if (++lk == IP) {
+      lk = 0;
+      ++lpass;
     }
   };
 
   // The first weights are requested before A is staged, so the two memory
   // round trips overlap.
-  int base = blockIdx.x * rows_per_pass;
-  int row0 = base + (wave * R + g) * R2;
-  uint32_t wc[R2][DW];
-  if (base < N && li < P) load(row0, li, wc);
+  uint32_t wa[R2][DW], wb[R2][DW];
+  if (T > 0) next_load(wa);
 
   // ---- stage A into LDS (and the per-block sums of x) ----
-  // One 32-element block per thread per iteration: its sum stays in the
-  // thread (no cross-lane traffic) and the chunk index needs no division.
-  const int nb = K >> 5;
+  // Thread tid takes 16-byte chunks tid, tid + 256, ... of the M x K
+  // activations, so every load instruction reads contiguous memory.  A
+  // 32-element block is 8 (f32) chunks held by 8 consecutive lanes; its sum
+  // is formed with DPP adds across them (total is a multiple of 8, so the 8
+  // lanes of a block are in or out of range together).  Loads past the end
+  // are clamped to the last chunk and dropped, so no load is predicated and
+  // all eight are in flight together.
+  {
+    const int total = M * P * CP;
+    auto stage = [&](int c0) {
+      ChunkT v[8];
 #pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    for (int b = tid; b < nb; b += 256) {
-      const int pair = b >> 1, half = b & 1;
-      constexpr int CPB = CP / 2;  // chunks per block
-      ChunkT v[CPB];
-#pragma unroll
-      for (int j = 0; j < CPB; ++j)
-        v[j] = m < M ? *reinterpret_cast<const ChunkT*>(A + (size_t)m * K + (size_t)b * 32 + j * EPC) : ChunkT{};
-#pragma unroll
-      for (int j = 0; j < CPB; ++j) xs[xslot<XT>(m, P, pair, half * CPB + j)] = v[j];
-      if constexpr (kSx) {
-        float sum = 0.f;
-#pragma unroll
-        for (int j = 0; j < CPB; ++j) sum += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
-        sxs[(m * P + pair) * 2 + half] = sum * (8.0f * unit);
+      for (int u = 0; u < 8; ++u) {
+        const int c = c0 + u * 256 + tid;
+        v[u] = *reinterpret_cast<const ChunkT*>(A + (size_t)(c < total ? c : total - 1) * EPC);
       }
-    }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = c0 + u * 256 + tid;
+        if (c < total) {
+          const int gp = c / CP, j = c & (CP - 1);
+          xs[gp * CP + (j ^ (gp & (CP - 1)))] = v[u];
+          if constexpr (kSx) {
+            float sum = (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
+            sum += dpp_f<0xB1>(sum);   // quad_perm [1,0,3,2]
+            sum += dpp_f<0x4E>(sum);   // quad_perm [2,3,0,1]
+            sum += dpp_f<0x141>(sum);  // row_half_mirror: every lane of the 8 holds the block sum
+            if ((j & 7) == 0) sxs[gp * 2 + (j >> 3)] = sum * (8.0f * unit);
+          }
+        }
+      }
+    };
+    // The first 2048 chunks (all of them up to M * K = 8192 f32 / 16384
+    // f16 elements) outside the loop, so their loads wait on nothing.
+    stage(0);
+    for (int c0 = 256 * 8; c0 < total; c0 += 256 * 8) stage(c0);
   }
   __syncthreads();
 
   const float inv_unit = 1.0f / unit;
-  for (; base < N; base += pass_stride, row0 += pass_stride) {
-    float acc[R2][MM];
+  float acc[R2][MM];
 #pragma unroll
-    for (int j = 0; j < R2; ++j)
+  for (int j = 0; j < R2; ++j)
 #pragma unroll
-      for (int m = 0; m < MM; ++m) acc[j][m] = 0.f;
+    for (int m = 0; m < MM; ++m) acc[j][m] = 0.f;
 
-    for (int pair = li; pair < P; pair += L) {
-      // Prefetch the next pair of this pass, or the first pair of the next pass.
-      uint32_t wn[R2][DW];
-      const bool more = pair + L < P;
-      const int nrow0 = more ? row0 : row0 + pass_stride;
-      const int npair = more ? pair + L : li;
-      const bool pf = more || base + pass_stride < N;
-      if (pf) load(nrow0, npair, wn);
+  int cpass = 0, ck = 0;  // position of the next compute step
+  auto step = [&](const uint32_t (&w)[R2][DW]) {
+    const int pair = li + (ck << log2L);
+    if (pair < P) {
       if constexpr (kF32) {
         if constexpr (kQ4) {
-          pair_f32_q4<R2, MM>(wc, reinterpret_cast<const float4v*>(xs), sxs, P, pair, inv_unit, acc);
+          pair_f32_q4<R2, MM>(w, reinterpret_cast<const float4v*>(xs), sxs, P, pair, inv_unit, acc);
         } else {
-          pair_f32_q8<R2, MM>(wc, reinterpret_cast<const float4v*>(xs), P, pair, acc);
+          pair_f32_q8<R2, MM>(w, reinterpret_cast<const float4v*>(xs), P, pair, acc);
         }
       } else {
-        pair_f16<QF, R2, MM>(wc, reinterpret_cast<const half8*>(xs), P, pair, acc);
-      }
-      if (pf) {
-#pragma unroll
-        for (int j = 0; j < R2; ++j)
-#pragma unroll
-          for (int i = 0; i < DW; ++i) wc[j][i] = wn[j][i];
+        pair_f16<QF, R2, MM>(w, reinterpret_cast<const half8*>(xs), P, pair, acc);
       }
     }
-    // reduce across the L lanes of the group (DPP; the sum lands in lane L-1)
+    if (++ck == IP) {
+      // end of a pass: reduce across the L lanes of the group (DPP; the sum
+      // lands in lane L-1), store, restart the sums
+      const int r0 = grp_row + cpass * pass_stride;
 #pragma unroll
-    for (int j = 0; j < R2; ++j)
+      for (int j = 0; j < R2; ++j)
 #pragma unroll
-      for (int m = 0; m < MM; ++m) acc[j][m] = group_sum(acc[j][m], log2L);
-    if (li == L - 1) {
+        for (int m = 0; m < MM; ++m) acc[j][m] = group_sum(acc[j][m], log2L);
+      if (li == L - 1) {
 #pragma unroll
-      for (int j = 0; j < R2; ++j) {
-        if (row0 + j >= N) continue;
+        for (int j = 0; j < R2; ++j) {
+          if (r0 + j >= N) continue;
 #pragma unroll
-        for (int m = 0; m < MM; ++m)
-          if (m < M) C[(size_t)m * N + row0 + j] = (XT)acc[j][m];
+          for (int m = 0; m < MM; ++m)
+            if (m < M) C[(size_t)m * N + r0 + j] = (XT)acc[j][m];
+        }
       }
+#pragma unroll
+      for (int j = 0; j < R2; ++j)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) acc[j][m] = 0.f;
+      ck = 0;
+      ++cpass;
     }
+  };
+
+  // Two register sets: the loads for step t+1 are in flight while step t
+  // computes.
+  for (int t = 0; t < T; t += 2) {
+    next_load(wb);
+    __builtin_amdgcn_sched_barrier(0);
+    step(wa);
+    __builtin_amdgcn_sched_barrier(0);
+    next_load(wa);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t + 1 < T) step(wb);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -561,15 +604,20 @@ hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint
   if (g.lds > 64 * 1024) return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
   g.log2L = pick_log2L(P);
   const int R = 64 >> g.log2L;
-  // One row per lane group while one pass of the grid covers all rows within
-  // two workgroups per CU; else two rows per group (more loads in flight per
-  // lane); beyond that the capped grid loops, reusing the staged activations.
-  const long cap = 256L * 2;
+  // One row per lane group while one pass covers all rows within four
+  // workgroups per CU (small launches finish sooner with more, lighter
+  // lanes); else two rows per lane group (more loads in flight per lane)
+  // and a grid capped at two workgroups per CU that loops over the rows,
+  // reusing the staged activations.
+  static const long cap = [] {
+    const char* e = std::getenv("NF_HIP_GEMV_WG_CAP");  // tuning override
+    const long v = e ? std::atol(e) : 0;
+    return v > 0 ? v : 256L * 2;
+  }();
   const long wgs1 = ((long)N + 4L * R - 1) / (4L * R);
   const long wgs2 = ((long)N + 8L * R - 1) / (8L * R);
-  g.R2 = wgs1 <= cap ? 1 : 2;
-  const long wgs = g.R2 == 1 ? wgs1 : wgs2;
-  g.grid = (unsigned)(wgs < cap ? wgs : cap);
+  g.R2 = wgs1 <= 256L * 4 ? 1 : 2;
+  g.grid = (unsigned)(g.R2 == 1 ? wgs1 : (wgs2 < cap ? wgs2 : cap));
   if (g.R2 == 2) {
     switch (g.MM) {
       case 1: return gemv_pair_launch<QF, XT, 2, 1>(g, A, W, C, M, N, K, s);
