@@ -1,4 +1,4 @@
-// skinny.hip — fused dequant + matmul for small batches (2 <= M <= 64) on MFMA.
+// skinny.hip — fused dequant + matmul for small batches (M up to 64) on MFMA.
 //
 // C[m, n] = sum_k A[m, k] * deq(W)[n, k] with fp32 accumulation, for the
 // batch sizes between the decode GEMV (M = 1..2) and the prefill GEMM.  The
@@ -27,12 +27,19 @@
 // block's chain from sum_k (-8u)*x, one extra chain per activation tile that
 // all weight tiles share.
 //
-// Work split: a wave owns T tiles of 16 weight rows and a contiguous range of
-// 64-element pairs along K; the KS waves of a workgroup split K and add their
-// partial sums in LDS (ds_add_f32) before one wave stores C.  Each lane
-// fetches, per pair, only the dwords of its slot (all loads dword aligned);
-// the next pair's weights and activations are loaded before the current
-// pair is computed.
+// Work split: a wave owns 64 weight rows (4 tiles of 16) and a contiguous
+// range of K, in chunks of CHP pairs (64 elements each); the waves of a
+// workgroup split K, park their partial sums in LDS and the workgroup adds
+// them in a fixed order before storing C.  A chunk of weights is fetched with contiguous 4/8/16-byte
+// loads (4 bytes per pair of the chunk, so consecutive lanes read consecutive
+// bytes of a row) into a wave-private LDS area, from which each lane gathers
+// its slot dwords; the activations are gathered straight from global memory
+// (they are L2-resident).  Per chunk the loads are issued as activations,
+// then weights, so chunk c computes while both of chunk c+1 are in flight.
+// At most 32 activation rows per launch keep the two activation register sets
+// and the accumulators in registers; more rows take more launches.
+#include <type_traits>
+
 #include "../launch.hpp"
 #include "common.hpp"
 
@@ -169,50 +176,60 @@ __device__ __forceinline__ void split3(const float (&x)[8], bf16x8& p1, bf16x8& 
   }
 }
 
-template <class QF, typename XT, int MT, int T>
+// Staging piece of a weight chunk: 4 B per pair of the chunk (16 B for
+// 4-pair chunks, 8 B for 2-pair, 4 B for 1-pair), so a row of a chunk is
+// always 9 (Q4_0) or 17 (Q8_0) pieces.
+template <int PS> struct Piece;
+template <> struct Piece<16> { typedef u32x4 T; };
+template <> struct Piece<8> { typedef uint2 T; };
+template <> struct Piece<4> { typedef uint32_t T; };
+
+template <class QF, typename XT, int MT, int CHP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) void skinny_kernel(
     const XT* __restrict__ A, const uint8_t* __restrict__ W, XT* __restrict__ C, int M, int N, int K) {
   constexpr bool kF32 = sizeof(XT) == 4;
   constexpr bool kQ4 = SkW<QF>::kLoads == 5;
   constexpr int WL = SkW<QF>::kLoads;
   constexpr int PB = SkW<QF>::kPairBytes;
+  constexpr int T = 4;                      // 16-row weight tiles per wave
   constexpr int RW = 16 * T;                // weight rows per wave
-  constexpr int CHP = 4;                    // pairs per chunk
-  constexpr int CB = CHP * PB / 16;         // 16-B pieces per row per chunk (9 / 17)
+  constexpr int PS = 4 * CHP;               // staging piece bytes
+  constexpr int CB = CHP * PB / PS;         // pieces per row per chunk (9 / 17)
   constexpr int J = RW * CB / 64;           // pieces per lane per chunk
-  constexpr int PITCH = CB * 4;             // dwords per staged row
+  constexpr int PITCH = CHP * PB / 4;       // dwords per staged row
   static_assert(RW * CB % 64 == 0, "chunk pieces per lane");
+  typedef typename Piece<PS>::T PieceT;
+  constexpr int NV = MT * T * 4;            // accumulator values per lane
+  // Per wave, one LDS area holds the staged weight rows during the K loop
+  // and the wave's partial sums afterwards.
+  constexpr int AREA = RW * PITCH > NV * 64 ? RW * PITCH : NV * 64;  // dwords
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
-  // [wave][RW][PITCH] staged weight rows, then [MT*T*4][64] partial sums
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int KS = blockDim.x >> 6;
   const int r16 = lane & 15, s = lane >> 4;
   const int P = K >> 6;
-  const int NC = P / CHP;  // chunks along K (K % 256 == 0)
+  const int NC = P / CHP;  // chunks along K
   const int n0 = blockIdx.x * RW;
-  uint32_t* wst = smem + (size_t)wave * RW * PITCH;
-  float* red = reinterpret_cast<float*>(smem + (size_t)KS * RW * PITCH);
+  uint32_t* wst = smem + (size_t)wave * AREA;
 
   // K range of this wave (whole chunks)
   const int c_begin = (int)((long)NC * wave / KS), c_end = (int)((long)NC * (wave + 1) / KS);
 
-  for (int i = tid; i < MT * T * 4 * 64; i += blockDim.x) red[i] = 0.f;
-
   // Weight staging: piece f = lane + 64*j of the wave's RW x CB chunk is row
-  // f / CB, 16-B piece f % CB; consecutive lanes read consecutive bytes of a
-  // row.  Rows past N read row N-1 (their B operands are zeroed below).
-  const size_t row_bytes = (size_t)P * PB;
-  const uint8_t* wsrc[J];
-  int wdst[J];
+  // f / CB, piece f % CB; consecutive lanes read consecutive bytes of a row,
+  // and piece f lands at LDS dword f * PS/4 (= row * PITCH + piece * PS/4).
+  // Rows past N read row N-1 (their B operands are zeroed below).  Offsets
+  // are 32-bit (the host keeps a weight matrix below 4 GB on this path).
+  const uint32_t row_bytes = (uint32_t)P * PB;
+  uint32_t wsrc[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int f = lane + 64 * j;
     const int row = f / CB, pc = f % CB;
     const int n = n0 + row < N ? n0 + row : N - 1;
-    wsrc[j] = W + (size_t)n * row_bytes + pc * 16;
-    wdst[j] = row * PITCH + pc * 4;
+    wsrc[j] = (uint32_t)n * row_bytes + (uint32_t)(pc * PS);
   }
   bool wvalid[T];
 #pragma unroll
@@ -220,37 +237,49 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 
   // Activation rows past M read row 0: an activation row only feeds its own
   // output row, and output rows past M are never stored, so no masking.
-  const XT* xrow[MT];
+  uint32_t xrow[MT];  // element offset of the lane's activation row
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + r16;
-    xrow[mt] = A + (size_t)(m < M ? m : 0) * K;
+    xrow[mt] = (uint32_t)(m < M ? m : 0) * (uint32_t)K;
   }
 
-  typedef float XBuf[MT][2][8];
-  typedef uint32_t HBuf[MT][2][4];
-  auto load_x32 = [&](int p, XBuf& xb) {
+  // Activation registers of one chunk: per pair, per tile, per block half,
+  // the 8 k values of the lane's slot (f32: 8 floats, f16: 4 dwords).
+  typedef float XC32[CHP][MT][2][8];
+  typedef uint32_t XC16[CHP][MT][2][4];
+  typedef typename std::conditional<kF32, XC32, XC16>::type XChunkT;
+  auto load_x = [&](int c, XChunkT& xb) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int pi = 0; pi < CHP; ++pi)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float* base = reinterpret_cast<const float*>(xrow[mt]) + p * 64 + h * 32;
-        const float4v v0 = *reinterpret_cast<const float4v*>(base + SkK<QF>::off0(s));
-        const float4v v1 = *reinterpret_cast<const float4v*>(base + SkK<QF>::off1(s));
-        xb[mt][h][0] = v0.x; xb[mt][h][1] = v0.y; xb[mt][h][2] = v0.z; xb[mt][h][3] = v0.w;
-        xb[mt][h][4] = v1.x; xb[mt][h][5] = v1.y; xb[mt][h][6] = v1.z; xb[mt][h][7] = v1.w;
-      }
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int k0 = (c * CHP + pi) * 64 + h * 32;
+          if constexpr (kF32) {
+            const float* base = reinterpret_cast<const float*>(A) + xrow[mt] + k0;
+            const float4v v0 = *reinterpret_cast<const float4v*>(base + SkK<QF>::off0(s));
+            const float4v v1 = *reinterpret_cast<const float4v*>(base + SkK<QF>::off1(s));
+            xb[pi][mt][h][0] = v0.x; xb[pi][mt][h][1] = v0.y; xb[pi][mt][h][2] = v0.z; xb[pi][mt][h][3] = v0.w;
+            xb[pi][mt][h][4] = v1.x; xb[pi][mt][h][5] = v1.y; xb[pi][mt][h][6] = v1.z; xb[pi][mt][h][7] = v1.w;
+          } else {
+            const half_t* base = reinterpret_cast<const half_t*>(A) + xrow[mt] + k0;
+            const uint2 v0 = *reinterpret_cast<const uint2*>(base + SkK<QF>::off0(s));
+            const uint2 v1 = *reinterpret_cast<const uint2*>(base + SkK<QF>::off1(s));
+            xb[pi][mt][h][0] = v0.x; xb[pi][mt][h][1] = v0.y; xb[pi][mt][h][2] = v1.x; xb[pi][mt][h][3] = v1.y;
+          }
+        }
   };
-  auto load_x16 = [&](int p, HBuf& xb) {
+  PieceT wr[J];
+  auto fetch_w = [&](int c) {
+    const uint8_t* wc = W + (size_t)c * CHP * PB;  // uniform
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int j = 0; j < J; ++j) wr[j] = *reinterpret_cast<const PieceT*>(wc + wsrc[j]);
+  };
+  auto write_w = [&]() {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const half_t* base = reinterpret_cast<const half_t*>(xrow[mt]) + p * 64 + h * 32;
-        const uint2 v0 = *reinterpret_cast<const uint2*>(base + SkK<QF>::off0(s));
-        const uint2 v1 = *reinterpret_cast<const uint2*>(base + SkK<QF>::off1(s));
-        xb[mt][h][0] = v0.x; xb[mt][h][1] = v0.y; xb[mt][h][2] = v1.x; xb[mt][h][3] = v1.y;
-      }
+    for (int j = 0; j < J; ++j) *reinterpret_cast<PieceT*>(wst + (lane + 64 * j) * (PS / 4)) = wr[j];
   };
   // The slot dwords of staged pair pi (of the chunk) of tile t's row r16.
   auto read_w = [&](int pi, int t, uint32_t (&w)[WL]) {
@@ -272,174 +301,168 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1u, false)[0];
   const float inv_unit = 1.0f / unit;
 
-  auto compute_f32 = [&](int pi, const XBuf& xc) {
+  // One staged chunk: CHP pairs x 2 blocks x T tiles x MT activation tiles.
+  auto compute = [&](const XChunkT& xc) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      bf16x8 a1[MT], a2[MT], a3[MT];
-      float4v base[MT];
+    for (int pi = 0; pi < CHP; ++pi)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        split3(xc[mt][h], a1[mt], a2[mt], a3[mt]);
-        base[mt] = float4v{0.f, 0.f, 0.f, 0.f};
-        if constexpr (kQ4) {
-          // sum_k (-8u) * x, the nibble offset, shared by all weight tiles
-          const __bf16 c8 = (__bf16)(-8.0f * unit);
-          const bf16x8 bc = {c8, c8, c8, c8, c8, c8, c8, c8};
-          base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], bc, base[mt], 0, 0, 0);
-          base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[mt], bc, base[mt], 0, 0, 0);
-          base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[mt], bc, base[mt], 0, 0, 0);
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (kF32) {
+          bf16x8 a1[MT], a2[MT], a3[MT];
+          float4v base[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            split3(xc[pi][mt][h], a1[mt], a2[mt], a3[mt]);
+            base[mt] = float4v{0.f, 0.f, 0.f, 0.f};
+            if constexpr (kQ4) {
+              // sum_k (-8u) * x, the nibble offset, shared by all weight tiles
+              const __bf16 c8 = (__bf16)(-8.0f * unit);
+              const bf16x8 bc = {c8, c8, c8, c8, c8, c8, c8, c8};
+              base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], bc, base[mt], 0, 0, 0);
+              base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[mt], bc, base[mt], 0, 0, 0);
+              base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[mt], bc, base[mt], 0, 0, 0);
+            }
+          }
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            uint32_t w[WL];
+            read_w(pi, t, w);
+            const bf16x8 b = sk_b_codes<QF>(w, h);
+            float d = h2f_bits((uint16_t)sk_scale_bits<QF>(w, h));
+            if constexpr (kQ4) d *= inv_unit;
+            if (!wvalid[t]) d = 0.f;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              float4v dd = base[mt];
+              dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], b, dd, 0, 0, 0);
+              dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[mt], b, dd, 0, 0, 0);
+              dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[mt], b, dd, 0, 0, 0);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[mt][t][i] = __builtin_fmaf(d, dd[i], acc[mt][t][i]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            uint32_t w[WL];
+            read_w(pi, t, w);
+            half8 b = sk_b_f16<QF>(w, h);
+            if (!wvalid[t]) b = half8{};
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const u32x4 av = {xc[pi][mt][h][0], xc[pi][mt][h][1], xc[pi][mt][h][2], xc[pi][mt][h][3]};
+              acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, av), b, acc[mt][t], 0, 0, 0);
+            }
+          }
         }
       }
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        uint32_t w[WL];
-        read_w(pi, t, w);
-        const bf16x8 b = sk_b_codes<QF>(w, h);
-        float d = h2f_bits((uint16_t)sk_scale_bits<QF>(w, h));
-        if constexpr (kQ4) d *= inv_unit;
-        if (!wvalid[t]) d = 0.f;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          float4v dd = base[mt];
-          dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], b, dd, 0, 0, 0);
-          dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[mt], b, dd, 0, 0, 0);
-          dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[mt], b, dd, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[mt][t][i] = __builtin_fmaf(d, dd[i], acc[mt][t][i]);
-        }
-      }
-    }
-  };
-  auto compute_f16 = [&](int pi, const HBuf& xc) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        uint32_t w[WL];
-        read_w(pi, t, w);
-        half8 b = sk_b_f16<QF>(w, h);
-        if (!wvalid[t]) b = half8{};
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const u32x4 av = {xc[mt][h][0], xc[mt][h][1], xc[mt][h][2], xc[mt][h][3]};
-          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, av), b, acc[mt][t], 0, 0, 0);
-        }
-      }
-    }
   };
 
-  // Chunk loop (uniform trip count): the staged registers of chunk c are
-  // written to LDS, chunk c+1 (clamped to the last chunk) is fetched into the
-  // same registers, and chunk c is computed from LDS with the activations of
-  // the next pair loaded one pair ahead.
+  // Chunk pipeline.  Loads complete in issue order; per chunk the issue
+  // order is x(c), W(c).  Chunk c computes while x(c+1) and W(c+1) are in
+  // flight; the only wait is the LDS write of W(c+1) at the top of the next
+  // chunk, which also covers x(c+1).  Two activation register sets alternate
+  // (the loop is unrolled by two).
   if (c_begin < c_end) {
-    u32x4 wr[J];
-    auto fetch = [&](int c) {
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-        wr[j] = *reinterpret_cast<const u32x4*>(wsrc[j] + (size_t)c * CHP * PB);
-    };
-    fetch(c_begin);
-    for (int c = c_begin; c < c_end; ++c) {
-#pragma unroll
-      for (int j = 0; j < J; ++j) *reinterpret_cast<u32x4*>(wst + wdst[j]) = wr[j];
-      __builtin_amdgcn_sched_barrier(0);
-      fetch(c + 1 < c_end ? c + 1 : c);
-      __builtin_amdgcn_sched_barrier(0);
-      const int p0 = c * CHP;
-      if constexpr (kF32) {
-        XBuf x0, x1;
-        load_x32(p0, x0);
-#pragma unroll
-        for (int pi = 0; pi < CHP; pi += 2) {
-          load_x32(p0 + pi + 1, x1);
-          __builtin_amdgcn_sched_barrier(0);
-          compute_f32(pi, x0);
-          __builtin_amdgcn_sched_barrier(0);
-          if (pi + 2 < CHP) load_x32(p0 + pi + 2, x0);
-          __builtin_amdgcn_sched_barrier(0);
-          compute_f32(pi + 1, x1);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      } else {
-        HBuf x0, x1;
-        load_x16(p0, x0);
-#pragma unroll
-        for (int pi = 0; pi < CHP; pi += 2) {
-          load_x16(p0 + pi + 1, x1);
-          __builtin_amdgcn_sched_barrier(0);
-          compute_f16(pi, x0);
-          __builtin_amdgcn_sched_barrier(0);
-          if (pi + 2 < CHP) load_x16(p0 + pi + 2, x0);
-          __builtin_amdgcn_sched_barrier(0);
-          compute_f16(pi + 1, x1);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+    XChunkT xa, xb;
+    load_x(c_begin, xa);
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order x, W
+    fetch_w(c_begin);
+    for (int c = c_begin; c < c_end; c += 2) {
+      const bool m1 = c + 1 < c_end, m2 = c + 2 < c_end;
+      write_w();
+      if (m1) {
+        load_x(c + 1, xb);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_w(c + 1);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(xa);
+      __builtin_amdgcn_sched_barrier(0);
+      if (!m1) break;
+      write_w();
+      if (m2) {
+        load_x(c + 2, xa);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_w(c + 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(xb);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // combine the KS partial sums in LDS, then wave 0 stores
-  __syncthreads();
+  // Combine the KS partial sums: each wave writes its accumulators into its
+  // own LDS area (value v = ((mt * T + t) * 4 + i) * 64 + lane), then every
+  // thread sums values v = tid, tid + 64*KS, ... over the waves in a fixed
+  // order (deterministic) and stores them.
+  float* part = reinterpret_cast<float*>(wst);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) atomicAdd(&red[((mt * T + t) * 4 + i) * 64 + lane], acc[mt][t][i]);
+      for (int i = 0; i < 4; ++i) part[((mt * T + t) * 4 + i) * 64 + lane] = acc[mt][t][i];
   __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const int n = n0 + 16 * t + r16;
-        if (n >= N) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 16 * mt + 4 * s + i;
-          if (m < M) C[(size_t)m * N + n] = (XT)red[((mt * T + t) * 4 + i) * 64 + lane];
-        }
-      }
+  const float* parts = reinterpret_cast<const float*>(smem);
+  for (int v = tid; v < NV * 64; v += blockDim.x) {
+    float sum = 0.f;
+    for (int w = 0; w < KS; ++w) sum += parts[(size_t)w * AREA + v];
+    const int l = v & 63, q = v >> 6;  // q = (mt * T + t) * 4 + i
+    const int i = q & 3, t = (q >> 2) % T, mt = (q >> 2) / T;
+    const int n = n0 + 16 * t + (l & 15), m = 16 * mt + 4 * (l >> 4) + i;
+    if (n < N && m < M) C[(size_t)m * N + n] = (XT)sum;
   }
 }
 
-template <class QF, typename XT, int MT, int T>
+template <class QF, typename XT, int MT, int CHP>
 hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
                          hipStream_t s) {
-  constexpr int RW = 16 * T, PITCH = 4 * SkW<QF>::kPairBytes / 4;  // 4 pairs per staged row
+  constexpr int RW = 64, PITCH = CHP * SkW<QF>::kPairBytes / 4, NV = MT * 4 * 4;
+  constexpr int AREA = RW * PITCH > NV * 64 ? RW * PITCH : NV * 64;  // dwords per wave
   const long wgs = ((long)N + RW - 1) / RW;
-  const int NC = (int)(K / 256);
+  const int NC = (int)(K / (64 * CHP));
   // K split: enough waves to give every CU several, at most 8 per workgroup
   // and at least two chunks per wave.
   int ks = 1;
   while (ks < 8 && wgs * ks < 2048 && NC / (ks * 2) >= 2) ks *= 2;
-  const size_t lds = (size_t)ks * RW * PITCH * 4 + (size_t)MT * T * 4 * 64 * sizeof(float);
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_kernel<QF, XT, MT, T>),
+  const size_t lds = (size_t)ks * AREA * 4;
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_kernel<QF, XT, MT, CHP>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
-  skinny_kernel<QF, XT, MT, T><<<dim3((unsigned)wgs), dim3(64 * ks), lds, s>>>(
+  skinny_kernel<QF, XT, MT, CHP><<<dim3((unsigned)wgs), dim3(64 * ks), lds, s>>>(
       static_cast<const XT*>(A), static_cast<const uint8_t*>(W), static_cast<XT*>(C), (int)M, (int)N, (int)K);
   return hipGetLastError();
 }
 
+// Activation tiles per launch (16 rows each) and pairs per staged chunk,
+// sized so the two activation register sets and the staged weight pieces
+// stay within the register file.
 template <class QF, typename XT>
 hipError_t skinny_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
                            hipStream_t s) {
-  if (M <= 16) return skinny_launch<QF, XT, 1, 4>(A, W, C, M, N, K, s);
-  if (M <= 32 || sizeof(XT) == 4) return skinny_launch<QF, XT, 2, 4>(A, W, C, M, N, K, s);
-  return skinny_launch<QF, XT, 4, 4>(A, W, C, M, N, K, s);
+  constexpr bool kQ4 = SkW<QF>::kLoads == 5;
+  if constexpr (sizeof(XT) == 4) {
+    if (M <= 16) return skinny_launch<QF, XT, 1, 2>(A, W, C, M, N, K, s);
+    return skinny_launch<QF, XT, 2, 1>(A, W, C, M, N, K, s);
+  } else {
+    if (M <= 16) return skinny_launch<QF, XT, 1, kQ4 ? 4 : 2>(A, W, C, M, N, K, s);
+    return skinny_launch<QF, XT, 2, kQ4 ? 2 : 1>(A, W, C, M, N, K, s);
+  }
 }
 
 }  // namespace nfk
 
 namespace nfhip {
 
-bool skinny_fits(uint32_t M, uint32_t K, const void* A, const void* W) {
-  return M >= 1 && M <= 64 && K % 256 == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)W % 16 == 0;
+bool skinny_fits(uint32_t M, uint32_t N, uint32_t K, const void* A, const void* W) {
+  // 32-bit in-kernel offsets: weight matrix and activation tile below 4 GB
+  const uint64_t wbytes = (uint64_t)N * (K / 32) * 34, abytes = (uint64_t)64 * K * 4;
+  return M >= 1 && M <= 64 && K % 256 == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)W % 16 == 0 &&
+         wbytes < (1ull << 32) && abytes < (1ull << 32);
 }
 
-uint32_t skinny_max_rows(EType t) { return t == EType::F32 ? 32u : 64u; }
+uint32_t skinny_max_rows(EType) { return 32u; }
 
 hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M, uint32_t N,
                          uint32_t K, hipStream_t s) {

@@ -19,7 +19,7 @@ hipError_t launch_gemv(QFmt q, EType t, const void* A, const void* W, void* C, u
 
 // Small-batch (M <= 64) MFMA kernel; skinny_fits() says whether a shape and
 // operand alignment suit it.
-bool skinny_fits(uint32_t M, uint32_t K, const void* A, const void* W);
+bool skinny_fits(uint32_t M, uint32_t N, uint32_t K, const void* A, const void* W);
 uint32_t skinny_max_rows(EType t);  // activation rows per launch
 hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M, uint32_t N,
                          uint32_t K, hipStream_t s);

@@ -401,7 +401,7 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, hipSt
     case Path::Gemv:
       return launch_gemv(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
     case Path::Skinny: {
-      if (!skinny_fits(1, pl.K, in[0]->dev, in[1]->dev))  // odd alignment (imported buffers)
+      if (!skinny_fits(1, pl.N, pl.K, in[0]->dev, in[1]->dev))  // odd alignment (imported buffers)
         return pl.c == EType::F16
                    ? launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s)
                    : launch_gemv(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
