@@ -29,6 +29,7 @@
 // Small-tile kernel (any K % 32 == 0): CTA tile 64x64, 4 waves of 32x32
 // built from v_mfma_f32_16x16x32_f16, one block per K step.
 #include <cstdlib>
+#include <string>
 
 #include "../launch.hpp"
 #include "common.hpp"
@@ -241,18 +242,25 @@ __device__ __forceinline__ void load_wblk(const uint8_t* p, uint32_t (&w)[WBlk<Q
   w[WBlk<QF>::kDwords - 1] = reinterpret_cast<const uint32_t*>(p)[WBlk<QF>::kDwords - 1];
 }
 
-// fp16 weights of the loaded block (h selects the pair position) in natural
-// element order, 16 dwords.
+// fp16 weights of the loaded block in natural element order, 16 dwords.
+// The thread's window starts 0 (h = 0) or 2 (h = 1) bytes before the block's
+// scale, so code dword t is bytes 2+2h+4t.. of the window: one v_perm with a
+// per-thread selector `sel` (0x05040302 or 0x07060504) extracts it, and
+// `sh` (0 or 16) shifts the scale down.  `valid` = false zeroes the scale,
+// and with it the block (rows past N).
 template <class QF>
-__device__ __forceinline__ void dequant_wblk(const uint32_t (&w)[WBlk<QF>::kDwords], int h, uint32_t (&o)[16]);
+__device__ __forceinline__ void dequant_wblk(const uint32_t (&w)[WBlk<QF>::kDwords], uint32_t sel, uint32_t sh,
+                                             bool valid, uint32_t (&o)[16]);
 
 template <>
-__device__ __forceinline__ void dequant_wblk<Q4_0>(const uint32_t (&w)[5], int h, uint32_t (&o)[16]) {
-  const uint32_t db = h ? (w[0] >> 16) : (w[0] & 0xFFFFu);
+__device__ __forceinline__ void dequant_wblk<Q4_0>(const uint32_t (&w)[5], uint32_t sel, uint32_t sh, bool valid,
+                                                   uint32_t (&o)[16]) {
+  uint32_t db = (w[0] >> sh) & 0xFFFFu;
+  db = valid ? db : 0u;
   const half2v d2 = h2_of(db | (db << 16));
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const uint32_t q = h ? w[t + 1] : __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2);
+    const uint32_t q = __builtin_amdgcn_perm(w[t + 1], w[t], sel);
     uint32_t lo[2], hi[2];
     q4_word_f16(q, d2, lo, hi);
     o[2 * t + 0] = lo[0];
@@ -263,12 +271,14 @@ __device__ __forceinline__ void dequant_wblk<Q4_0>(const uint32_t (&w)[5], int h
 }
 
 template <>
-__device__ __forceinline__ void dequant_wblk<Q8_0>(const uint32_t (&w)[9], int h, uint32_t (&o)[16]) {
-  const uint32_t db = h ? (w[0] >> 16) : (w[0] & 0xFFFFu);
+__device__ __forceinline__ void dequant_wblk<Q8_0>(const uint32_t (&w)[9], uint32_t sel, uint32_t sh, bool valid,
+                                                   uint32_t (&o)[16]) {
+  uint32_t db = (w[0] >> sh) & 0xFFFFu;
+  db = valid ? db : 0u;
   const half2v d2 = h2_of(db | (db << 16));
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const uint32_t q = h ? w[t + 1] : __builtin_amdgcn_alignbyte(w[t + 1], w[t], 2);
+    const uint32_t q = __builtin_amdgcn_perm(w[t + 1], w[t], sel);
     uint32_t v[2];
     q8_word_f16(q, d2, v);
     o[2 * t + 0] = v[0];
@@ -292,6 +302,27 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* lds_base) {
 // (64 lanes x 16 B, contiguous) fills 8 whole rows.
 __device__ __forceinline__ int tile_off(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 7)) << 3); }
 
+// Workgroup -> output tile, XCD-aware.  The dispatcher hands consecutive
+// workgroup ids to the 8 XCDs in turn, and each XCD has its own L2.  The
+// tiles are enumerated in groups of GM M-tiles (N-tile outer, M-tile inner,
+// GM = max(1, M-tiles / 8)), and that sequence is cut into 8 contiguous
+// pieces, one per XCD: an XCD then works on about 1/8 of the activation rows
+// against a sweep of weight tiles, so its activation rows stay in its L2 and
+// each weight tile is fetched about once per XCD.
+__device__ __forceinline__ void xcd_tile(int bid, int mt, int nt, int& tm, int& tn) {
+  constexpr int kXcd = 8;
+  const int total = mt * nt;
+  const int per = (total + kXcd - 1) / kXcd;  // tiles of the larger pieces
+  const int tall = total - (per - 1) * kXcd;   // number of larger pieces
+  const int x = bid % kXcd, j = bid / kXcd;
+  const int pid = x < tall ? x * per + j : tall * per + (x - tall) * (per - 1) + j;
+  const int gm = mt / kXcd > 1 ? mt / kXcd : 1;
+  const int group = pid / (gm * nt), within = pid - group * gm * nt;
+  const int rows = mt - group * gm < gm ? mt - group * gm : gm;
+  tm = group * gm + within % rows;
+  tn = within / rows;
+}
+
 // CTA tile BM x BN, WGM x WGN waves, each owning (BM/WGM) x (BN/WGN) =
 // TM x TN tiles of 32x32; K step 64, two LDS stages.
 //
@@ -303,7 +334,7 @@ __device__ __forceinline__ int tile_off(int r, int c) { return r * 64 + ((c ^ ((
 //   * W of step s+1 (fetched one step earlier) is dequantized to fp16 and
 //     written into the other stage;
 //   * one barrier.
-template <class QF, int BM, int BN, int WGM, int WGN>
+template <class QF, int BM, int BN, int WGM, int WGN, int NS>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half_t* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
                                                                     half_t* __restrict__ C, int M,
@@ -313,6 +344,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
   constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;
   constexpr int A_DMA = BM / 8 / NWAVE;  // direct-to-LDS loads (8 rows each) per wave per step
   constexpr int STAGE = (BM + BN) * 64;  // halves
+  static_assert(NS == 2 || NS == 3, "two or three LDS stages");
   constexpr int WD = WBlk<QF>::kDwords;
   static_assert(BM % (8 * NWAVE) == 0, "A rows per wave");
   static_assert(BN * 2 <= NT || WBlk<QF>::kLoads == 0, "W staging: one block per thread");
@@ -321,7 +353,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = (wave / WGN) * (BM / WGM), wn = (wave % WGN) * (BN / WGN);
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  int tm, tn;
+  xcd_tile(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
   const int nk = K / kBK;
 
   // A: lane -> (row within its 8-row group, chunk slot); the global chunk is
@@ -351,9 +385,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
       bsrc[i] = Bh + (size_t)gr * K + c * 8;
     }
   }
-  // W: thread -> (row, block); extra threads duplicate a row (identical writes).
+  // W: thread -> (row, block); extra threads duplicate a row (identical
+  // writes).  Block h's window starts at dword h * kStride of the pair: the
+  // scale is then in its low (h = 0) or high (h = 1) half of window dword 0.
   const int w_row = (tid >> 1) % BN, w_half = tid & 1;
   const bool w_valid = n0 + w_row < N;
+  const uint32_t w_sel = w_half ? 0x07060504u : 0x05040302u, w_sh = w_half ? 16u : 0u;
   const uint8_t* wsrc = nullptr;
   if constexpr (!kDenseB) {
     const size_t row_bytes = (size_t)(K / 64) * GPair<QF>::kBytes;
@@ -377,12 +414,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
   auto stage_w = [&](int buf, const uint32_t (&w)[WD]) {
     if constexpr (!kDenseB) {
       uint32_t o[16];
-      dequant_wblk<QF>(w, w_half, o);
+      dequant_wblk<QF>(w, w_sel, w_sh, w_valid, o);
       half_t* Bs = lds + (size_t)buf * STAGE + BM * 64;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        u32x4 v = {o[4 * c + 0], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]};
-        if (!w_valid) v = u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = {o[4 * c + 0], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]};
         *reinterpret_cast<u32x4*>(Bs + tile_off(w_row, w_half * 4 + c)) = v;
       }
     }
@@ -434,38 +470,42 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
   // Loads are unconditional (step indices clamped to the last step): a
   // conditional load into a register set would force a copy, and the copy a
   // wait for every outstanding load.  Past the end, the extra loads and
-  // stores only touch the idle stage.
+  // stores only touch idle stages.  A runs NS-1 steps ahead in the LDS ring;
+  // W runs two steps ahead in registers and is staged one step ahead.
   uint32_t wr[2][WD] = {};
-  dma_a(0, 0);
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i) dma_a(i < nk ? i : nk - 1, i);
   load_w(0, wr[0]);
   load_w(nk > 1 ? 1 : 0, wr[1]);
   stage_w(0, wr[0]);
   __syncthreads();
 
   // End-of-step barrier: this wave's LDS writes and its A loads for the next
-  // step must be complete; the W loads for two steps ahead (issued after the
-  // A loads, kWLoads instructions) may stay in flight.  __syncthreads() would
-  // wait for every outstanding load.
+  // step must be complete; loads issued during this step for later steps
+  // (the W loads, and with three stages the A loads for step s+2) may stay
+  // in flight.  __syncthreads() would wait for every outstanding load.
+  constexpr int kInFlight = WBlk<QF>::kLoads + (NS == 3 ? A_DMA + B_DMA : 0);
   auto step_barrier = [&]() {
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(WBlk<QF>::kLoads) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kInFlight) : "memory");
   };
-  auto half_step = [&](int s, int buf, uint32_t (&wload)[WD], const uint32_t (&wstage)[WD]) {
-    dma_a(s + 1 < nk ? s + 1 : s, buf ^ 1);
+  auto half_step = [&](int s, uint32_t (&wload)[WD], const uint32_t (&wstage)[WD]) {
+    const int ahead = s + NS - 1;
+    dma_a(ahead < nk ? ahead : nk - 1, ahead % NS);
     __builtin_amdgcn_sched_barrier(0);
     load_w(s + 2 < nk ? s + 2 : nk - 1, wload);  // wload held W(s), staged last step
     __builtin_amdgcn_sched_barrier(0);
-    compute(buf);
+    compute(s % NS);
     __builtin_amdgcn_sched_barrier(0);
-    stage_w(buf ^ 1, wstage);  // W(s+1)
+    stage_w((s + 1) % NS, wstage);  // W(s+1)
     __builtin_amdgcn_sched_barrier(0);
     step_barrier();
   };
   int ks = 0;
   for (; ks + 1 < nk; ks += 2) {
-    half_step(ks, 0, wr[0], wr[1]);
-    half_step(ks + 1, 1, wr[1], wr[0]);
+    half_step(ks, wr[0], wr[1]);
+    half_step(ks + 1, wr[1], wr[0]);
   }
-  if (ks < nk) half_step(ks, 0, wr[0], wr[1]);
+  if (ks < nk) half_step(ks, wr[0], wr[1]);
 
   // epilogue: round to fp16 and store
   const int col = lane & 31, rq = (lane >> 5) * 4;
@@ -568,10 +608,18 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const half_t* __restric
 // NF_HIP_GEMM_TILE overrides the choice.
 inline int pick_tile(uint32_t M, uint32_t N) {
   static const int forced = [] {
-    const char* e = std::getenv("NF_HIP_GEMM_TILE");
-    return e ? std::atoi(e) : -1;
+    const char* e = std::getenv("NF_HIP_GEMM_TILE");  // "256x256", "256x128", "128x128" (or 0, 1, 2)
+    if (!e) return -1;
+    const std::string v(e);
+    if (v == "256x256") return 0;
+    if (v == "256x128") return 1;
+    if (v == "128x128") return 2;
+    if (v == "256x128w4") return 3;
+    if (v == "256x128w4s3") return 4;
+    if (v == "128x128s3") return 5;
+    return std::atoi(e);
   }();
-  if (forced >= 0 && forced <= 2) return forced;
+  if (forced >= 0 && forced <= 5) return forced;
   constexpr long kCUs = 256;
   auto fill = [](long tiles, long slots) {
     const long rounds = (tiles + slots - 1) / slots;
@@ -586,18 +634,19 @@ inline int pick_tile(uint32_t M, uint32_t N) {
   return s1 > s2 ? 1 : 2;
 }
 
-template <class QF, int BM, int BN, int WGM, int WGN>
+template <class QF, int BM, int BN, int WGM, int WGN, int NS = 2>
 hipError_t gemm_tile_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_t M, uint32_t N,
                             uint32_t K, hipStream_t s) {
-  const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-  if (grid.y > 65535) return hipErrorInvalidConfiguration;
-  const size_t lds = (size_t)2 * (BM + BN) * 64 * sizeof(half_t);
+  const long tiles = (long)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
+  if (tiles > (1L << 31) - 1) return hipErrorInvalidConfiguration;
+  const dim3 grid((unsigned)tiles);
+  const size_t lds = (size_t)NS * (BM + BN) * 64 * sizeof(half_t);
   // More than 64 KB of dynamic LDS must be allowed explicitly, once per kernel.
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN>),
+      reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
-  gemm_tile_kernel<QF, BM, BN, WGM, WGN><<<grid, dim3(64 * WGM * WGN), lds, s>>>(a, w, c, M, N, K);
+  gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS><<<grid, dim3(64 * WGM * WGN), lds, s>>>(a, w, c, M, N, K);
   return hipGetLastError();
 }
 
@@ -615,6 +664,9 @@ hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t
   switch (nfk::pick_tile(M, N)) {
     case 0: return nfk::gemm_tile_launch<nfk::F16B, 256, 256, 2, 4>(a, b, c, M, N, K, s);
     case 1: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 4, 2>(a, b, c, M, N, K, s);
+    case 3: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2>(a, b, c, M, N, K, s);
+    case 4: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2, 3>(a, b, c, M, N, K, s);
+    case 5: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2, 3>(a, b, c, M, N, K, s);
     default: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2>(a, b, c, M, N, K, s);
   }
 }
@@ -634,6 +686,15 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
       case 1:
         return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 4, 2>(a, w, c, M, N, K, s)
                                  : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 4, 2>(a, w, c, M, N, K, s);
+      case 3:
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 2, 2>(a, w, c, M, N, K, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 2, 2>(a, w, c, M, N, K, s);
+      case 4:
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 2, 2, 3>(a, w, c, M, N, K, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 2, 2, 3>(a, w, c, M, N, K, s);
+      case 5:
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2, 3>(a, w, c, M, N, K, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2, 3>(a, w, c, M, N, K, s);
       default:
         return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2>(a, w, c, M, N, K, s)
                                  : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2>(a, w, c, M, N, K, s);
