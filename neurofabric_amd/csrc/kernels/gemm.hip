@@ -456,15 +456,26 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
     }
-    // Order for the scheduler: the first slice's operand reads, then per
-    // slice the next slice's reads ahead of this slice's MFMAs, so the MFMA
-    // pipe always has a slice queued while operands load.
+  };
+  // Order for the scheduler: the first slice's operand reads, then per slice
+  // the next slice's reads ahead of this slice's MFMAs, so the MFMA pipe
+  // always has a slice queued while operands load; VALU work of the step
+  // (the weight dequantization) is spread over the MFMA issue shadow, and the
+  // dequantized weights' LDS writes go last.
+  constexpr int kMfma = TM * TN * (kBK / 16);
+  constexpr int kValuPerMfma = (72 + kMfma - 1) / kMfma;
+  auto schedule = [&]() {
     __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
 #pragma unroll
     for (int kk = 0; kk < kBK / 16; ++kk) {
       if (kk + 1 < kBK / 16) __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+#pragma unroll
+      for (int m = 0; m < TM * TN; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (!kDenseB) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
+      }
     }
+    if constexpr (!kDenseB) __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);
   };
 
   // Loads are unconditional (step indices clamped to the last step): a
@@ -495,8 +506,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
     load_w(s + 2 < nk ? s + 2 : nk - 1, wload);  // wload held W(s), staged last step
     __builtin_amdgcn_sched_barrier(0);
     compute(s % NS);
-    __builtin_amdgcn_sched_barrier(0);
-    stage_w((s + 1) % NS, wstage);  // W(s+1)
+    stage_w((s + 1) % NS, wstage);  // W(s+1), dequantized in the MFMA shadow
+    schedule();
     __builtin_amdgcn_sched_barrier(0);
     step_barrier();
   };
@@ -617,9 +628,10 @@ inline int pick_tile(uint32_t M, uint32_t N) {
     if (v == "256x128w4") return 3;
     if (v == "256x128w4s3") return 4;
     if (v == "128x128s3") return 5;
+    if (v == "128x256") return 6;
     return std::atoi(e);
   }();
-  if (forced >= 0 && forced <= 5) return forced;
+  if (forced >= 0 && forced <= 6) return forced;
   constexpr long kCUs = 256;
   auto fill = [](long tiles, long slots) {
     const long rounds = (tiles + slots - 1) / slots;
@@ -667,6 +679,7 @@ hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t
     case 3: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2>(a, b, c, M, N, K, s);
     case 4: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2, 3>(a, b, c, M, N, K, s);
     case 5: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2, 3>(a, b, c, M, N, K, s);
+    case 6: return nfk::gemm_tile_launch<nfk::F16B, 128, 256, 2, 4>(a, b, c, M, N, K, s);
     default: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2>(a, b, c, M, N, K, s);
   }
 }
@@ -695,6 +708,9 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
       case 5:
         return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2, 3>(a, w, c, M, N, K, s)
                                  : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2, 3>(a, w, c, M, N, K, s);
+      case 6:
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 256, 2, 4>(a, w, c, M, N, K, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 256, 2, 4>(a, w, c, M, N, K, s);
       default:
         return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2>(a, w, c, M, N, K, s)
                                  : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2>(a, w, c, M, N, K, s);

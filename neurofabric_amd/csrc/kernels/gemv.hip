@@ -580,9 +580,18 @@ inline int pick_log2L(int P) {
   return best;
 }
 
+// Activations staged per workgroup: up to 120 KB of LDS (above 64 KB the
+// kernel has to opt in, once per instantiation).
+constexpr size_t kPairMaxLds = 120 * 1024;
+
 template <class QF, typename XT, int R2, int MM>
 hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const void* W, void* C, uint32_t M,
                             uint32_t N, uint32_t K, hipStream_t s) {
+  if (g.lds > 64 * 1024) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_pair_kernel<QF, XT, R2, MM>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPairMaxLds);
+    if (attr != hipSuccess) return attr;
+  }
   gemv_pair_kernel<QF, XT, R2, MM><<<dim3(g.grid), dim3(256), g.lds, s>>>(
       static_cast<const XT*>(A), static_cast<const uint8_t*>(W), static_cast<XT*>(C), (int)M, (int)N,
       (int)K, g.log2L);
@@ -601,7 +610,7 @@ hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint
   const size_t xbytes = (size_t)g.MM * P * 64 * (kF32 ? 4 : 2);
   const size_t sxbytes = (kF32 && PairFmt<QF>::kQd == 4) ? (size_t)g.MM * P * 2 * 4 : 0;
   g.lds = xbytes + sxbytes;
-  if (g.lds > 64 * 1024) return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
+  if (g.lds > kPairMaxLds) return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
   g.log2L = pick_log2L(P);
   const int R = 64 >> g.log2L;
   // One row per lane group while one pass covers all rows within four

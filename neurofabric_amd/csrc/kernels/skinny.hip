@@ -186,7 +186,8 @@ template <> struct Piece<4> { typedef uint32_t T; };
 
 template <class QF, typename XT, int MT, int CHP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) void skinny_kernel(
-    const XT* __restrict__ A, const uint8_t* __restrict__ W, XT* __restrict__ C, int M, int N, int K) {
+    const XT* __restrict__ A, const uint8_t* __restrict__ W, XT* __restrict__ C, int M, int N, int K,
+    float* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt) {
   constexpr bool kF32 = sizeof(XT) == 4;
   constexpr bool kQ4 = SkW<QF>::kLoads == 5;
   constexpr int WL = SkW<QF>::kLoads;
@@ -214,8 +215,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const int n0 = blockIdx.x * RW;
   uint32_t* wst = smem + (size_t)wave * AREA;
 
-  // K range of this wave (whole chunks)
-  const int c_begin = (int)((long)NC * wave / KS), c_end = (int)((long)NC * (wave + 1) / KS);
+  // K range of this wave (whole chunks): the KG = gridDim.y workgroups of a
+  // row tile and their KS waves split the chunks evenly.
+  const int KG = gridDim.y, kg = blockIdx.y;
+  const int gw = kg * KS + wave, nw = KG * KS;
+  const int c_begin = (int)((long)NC * gw / nw), c_end = (int)((long)NC * (gw + 1) / nw);
 
   // Weight staging: piece f = lane + 64*j of the wave's RW x CB chunk is row
   // f / CB, piece f % CB; consecutive lanes read consecutive bytes of a row,
@@ -405,33 +409,75 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       for (int i = 0; i < 4; ++i) part[((mt * T + t) * 4 + i) * 64 + lane] = acc[mt][t][i];
   __syncthreads();
   const float* parts = reinterpret_cast<const float*>(smem);
-  for (int v = tid; v < NV * 64; v += blockDim.x) {
-    float sum = 0.f;
-    for (int w = 0; w < KS; ++w) sum += parts[(size_t)w * AREA + v];
+  auto store = [&](int v, float sum) {
     const int l = v & 63, q = v >> 6;  // q = (mt * T + t) * 4 + i
     const int i = q & 3, t = (q >> 2) % T, mt = (q >> 2) / T;
     const int n = n0 + 16 * t + (l & 15), m = 16 * mt + 4 * (l >> 4) + i;
     if (n < N && m < M) C[(size_t)m * N + n] = (XT)sum;
+  };
+  if (KG == 1) {
+    for (int v = tid; v < NV * 64; v += blockDim.x) {
+      float sum = 0.f;
+      for (int w = 0; w < KS; ++w) sum += parts[(size_t)w * AREA + v];
+      store(v, sum);
+    }
+    return;
   }
+  // Split K across workgroups: each workgroup parks its tile sum in the
+  // workspace; the last one to arrive (per-tile counter, agent-scope
+  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1 and
+  // stores C, then resets the counter for the next launch.
+  float* mine = ws_part + ((size_t)blockIdx.x * KG + kg) * (NV * 64);
+  for (int v = tid; v < NV * 64; v += blockDim.x) {
+    float sum = 0.f;
+    for (int w = 0; w < KS; ++w) sum += parts[(size_t)w * AREA + v];
+    mine[v] = sum;
+  }
+  // Every wave waits for its stores to complete (the workgroup barrier alone
+  // does not); one thread then publishes them at agent scope (release) with
+  // the counter update, and in the last workgroup acquires the other
+  // workgroups' tiles for the whole workgroup.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ uint32_t is_last;
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[blockIdx.x], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == (uint32_t)(KG - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  const float* tile = ws_part + (size_t)blockIdx.x * KG * (NV * 64);
+  for (int v = tid; v < NV * 64; v += blockDim.x) {
+    float sum = 0.f;
+    for (int g = 0; g < KG; ++g) sum += tile[(size_t)g * (NV * 64) + v];
+    store(v, sum);
+  }
+  if (tid == 0) __hip_atomic_store(&ws_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <class QF, typename XT, int MT, int CHP>
 hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
-                         hipStream_t s) {
+                         const nfhip::Workspace& ws, hipStream_t s) {
   constexpr int RW = 64, PITCH = CHP * SkW<QF>::kPairBytes / 4, NV = MT * 4 * 4;
   constexpr int AREA = RW * PITCH > NV * 64 ? RW * PITCH : NV * 64;  // dwords per wave
   const long wgs = ((long)N + RW - 1) / RW;
   const int NC = (int)(K / (64 * CHP));
-  // K split: enough waves to give every CU several, at most 8 per workgroup
-  // and at least two chunks per wave.
+  // K split: up to 8 waves per workgroup; for launches with very few row
+  // tiles (under 512 waves), also KG workgroups per row tile, while every
+  // wave keeps at least one chunk; KG is bounded by the workspace.
   int ks = 1;
-  while (ks < 8 && wgs * ks < 2048 && NC / (ks * 2) >= 2) ks *= 2;
+  while (ks < 8 && wgs * ks < 2048 && NC >= 2 * ks) ks *= 2;
+  int kg = 1;
+  while (wgs * ks * kg < 512 && NC >= 2 * ks * kg && kg < 64 && wgs <= (long)ws.cnt_len &&
+         (size_t)wgs * 2 * kg * NV * 64 <= ws.part_floats)
+    kg *= 2;
   const size_t lds = (size_t)ks * AREA * 4;
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_kernel<QF, XT, MT, CHP>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
   if (attr != hipSuccess) return attr;
-  skinny_kernel<QF, XT, MT, CHP><<<dim3((unsigned)wgs), dim3(64 * ks), lds, s>>>(
-      static_cast<const XT*>(A), static_cast<const uint8_t*>(W), static_cast<XT*>(C), (int)M, (int)N, (int)K);
+  skinny_kernel<QF, XT, MT, CHP><<<dim3((unsigned)wgs, (unsigned)kg), dim3(64 * ks), lds, s>>>(
+      static_cast<const XT*>(A), static_cast<const uint8_t*>(W), static_cast<XT*>(C), (int)M, (int)N, (int)K,
+      ws.part, ws.cnt);
   return hipGetLastError();
 }
 
@@ -440,14 +486,19 @@ hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint
 // stay within the register file.
 template <class QF, typename XT>
 hipError_t skinny_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
-                           hipStream_t s) {
+                           const nfhip::Workspace& ws, hipStream_t s) {
   constexpr bool kQ4 = SkW<QF>::kLoads == 5;
+  // Few row tiles: one-pair chunks, so the K split reaches more CUs.
+  const bool small = N < 64u * 128u;
   if constexpr (sizeof(XT) == 4) {
-    if (M <= 16) return skinny_launch<QF, XT, 1, 2>(A, W, C, M, N, K, s);
-    return skinny_launch<QF, XT, 2, 1>(A, W, C, M, N, K, s);
+    if (M <= 16) return small ? skinny_launch<QF, XT, 1, 1>(A, W, C, M, N, K, ws, s)
+                              : skinny_launch<QF, XT, 1, 2>(A, W, C, M, N, K, ws, s);
+    return skinny_launch<QF, XT, 2, 1>(A, W, C, M, N, K, ws, s);
   } else {
-    if (M <= 16) return skinny_launch<QF, XT, 1, kQ4 ? 4 : 2>(A, W, C, M, N, K, s);
-    return skinny_launch<QF, XT, 2, kQ4 ? 2 : 1>(A, W, C, M, N, K, s);
+    if (M <= 16) return small ? skinny_launch<QF, XT, 1, 1>(A, W, C, M, N, K, ws, s)
+                              : skinny_launch<QF, XT, 1, kQ4 ? 4 : 2>(A, W, C, M, N, K, ws, s);
+    if (small) return skinny_launch<QF, XT, 2, 1>(A, W, C, M, N, K, ws, s);
+    return skinny_launch<QF, XT, 2, kQ4 ? 2 : 1>(A, W, C, M, N, K, ws, s);
   }
 }
 
@@ -465,12 +516,12 @@ bool skinny_fits(uint32_t M, uint32_t N, uint32_t K, const void* A, const void* 
 uint32_t skinny_max_rows(EType) { return 32u; }
 
 hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M, uint32_t N,
-                         uint32_t K, hipStream_t s) {
+                         uint32_t K, const Workspace& ws, hipStream_t s) {
   if (q == QFmt::Q4_0)
-    return t == EType::F32 ? nfk::skinny_dispatch<nfk::Q4_0, float>(A, W, C, M, N, K, s)
-                           : nfk::skinny_dispatch<nfk::Q4_0, nfk::half_t>(A, W, C, M, N, K, s);
-  return t == EType::F32 ? nfk::skinny_dispatch<nfk::Q8_0, float>(A, W, C, M, N, K, s)
-                         : nfk::skinny_dispatch<nfk::Q8_0, nfk::half_t>(A, W, C, M, N, K, s);
+    return t == EType::F32 ? nfk::skinny_dispatch<nfk::Q4_0, float>(A, W, C, M, N, K, ws, s)
+                           : nfk::skinny_dispatch<nfk::Q4_0, nfk::half_t>(A, W, C, M, N, K, ws, s);
+  return t == EType::F32 ? nfk::skinny_dispatch<nfk::Q8_0, float>(A, W, C, M, N, K, ws, s)
+                         : nfk::skinny_dispatch<nfk::Q8_0, nfk::half_t>(A, W, C, M, N, K, ws, s);
 }
 
 }  // namespace nfhip

@@ -11,6 +11,19 @@
 
 namespace nfhip {
 
+// Device workspace owned by the provider (allocated at init): fp32 partial
+// tiles of split-K launches and one counter per output tile.  Counters start
+// at zero and every split-K launch leaves them at zero again (the last
+// workgroup of a tile resets its counter), so no per-launch clearing is
+// needed.  Launches on the provider's single stream never overlap, so they
+// share it.
+struct Workspace {
+  float* part = nullptr;
+  uint32_t* cnt = nullptr;
+  size_t part_floats = 0;
+  uint32_t cnt_len = 0;
+};
+
 hipError_t launch_dequant(QFmt q, EType out_t, const void* w, void* out, uint64_t count,
                           hipStream_t s);
 
@@ -22,7 +35,7 @@ hipError_t launch_gemv(QFmt q, EType t, const void* A, const void* W, void* C, u
 bool skinny_fits(uint32_t M, uint32_t N, uint32_t K, const void* A, const void* W);
 uint32_t skinny_max_rows(EType t);  // activation rows per launch
 hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M, uint32_t N,
-                         uint32_t K, hipStream_t s);
+                         uint32_t K, const Workspace& ws, hipStream_t s);
 
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                             uint32_t N, uint32_t K, hipStream_t s);

@@ -133,7 +133,13 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
     } else {
       const bool f16 = p.c == EType::F16;
       const uint32_t gemv_max = f16 ? tuning.gemv_max_m_f16 : tuning.gemv_max_m_f32;
-      if (p.M <= gemv_max) {
+      // The GEMV stages M' x K activations per workgroup (M' = M rounded up
+      // to 1, 2 or 4) plus f32 Q4_0 block sums; beyond 120 KB of LDS it would
+      // fall back to its slow block kernel, so the MFMA kernel takes over.
+      const uint64_t mm = p.M <= 2 ? p.M : 4;
+      const uint64_t stage = mm * K * elt_bytes(p.a) + ((!f16 && p.q == QFmt::Q4_0) ? mm * (K / 64) * 8 : 0);
+      const bool gemv_fits = K % 64 != 0 || stage <= 120 * 1024;
+      if (p.M <= gemv_max && (gemv_fits || K % 256 != 0)) {
         p.path = Path::Gemv;
         p.kernel = "gemv_" + tag;
       } else if (K % 256 == 0 && (!f16 || p.M <= tuning.skinny_max_m_f16)) {

@@ -26,12 +26,15 @@ enum class Path {
 };
 
 // Switch points between the kernel families of the fused op: the VALU GEMV
-// while M <= gemv_max_m, the small-batch MFMA kernel while M <= skinny_max_m
-// (the f32 path stays there for every larger M, 64 rows per launch), the
-// tiled MFMA GEMM above (f16).  Defaults from the measured sweep.
+// while M <= gemv_max_m (and its activation stage fits in LDS), the
+// small-batch MFMA kernel while M <= skinny_max_m (the f32 path stays there
+// for every larger M, 32 rows per launch), the tiled MFMA GEMM above (f16).
+// Defaults from the measured sweep on MI355X: the GEMV wins or ties up to
+// M = 4, the small-batch kernel from M = 8, and for f16 it still beats the
+// tiled GEMM at M = 64.
 struct Tuning {
-  uint32_t gemv_max_m_f32 = 2;
-  uint32_t gemv_max_m_f16 = 2;
+  uint32_t gemv_max_m_f32 = 4;
+  uint32_t gemv_max_m_f16 = 4;
   uint32_t skinny_max_m_f16 = 64;
 };
 

@@ -97,6 +97,7 @@ struct Provider {
   uint64_t issued_seq = 0;            // guarded by mu
   std::atomic<uint64_t> done_seq{0};  // all dispatches <= done_seq finished
   Tuning tuning;
+  Workspace ws;  // split-K partials and tile counters
   // timing ring
   std::atomic<bool> timing{false};
   std::atomic<uint32_t> timing_head{0};
@@ -303,6 +304,21 @@ nf_status hip_init(nf_provider self) {
                                                p->props.gcnArchName);
   e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
   if (e != hipSuccess) return map_hip(e, "hipStreamCreateWithFlags");
+  // split-K workspace: 32 MB of partial tiles, 64 Ki tile counters (zeroed once)
+  p->ws.part_floats = (size_t)8 << 20;
+  p->ws.cnt_len = 1u << 16;
+  e = hipMalloc(reinterpret_cast<void**>(&p->ws.part), p->ws.part_floats * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->ws.cnt), p->ws.cnt_len * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemsetAsync(p->ws.cnt, 0, p->ws.cnt_len * sizeof(uint32_t), p->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p->ws.part);
+    (void)hipFree(p->ws.cnt);
+    p->ws = Workspace{};
+    (void)hipStreamDestroy(p->stream);
+    p->stream = nullptr;
+    return map_hip(e, "init: workspace");
+  }
   p->initialized = true;
   return NF_OK;
 }
@@ -322,6 +338,9 @@ void hip_shutdown(nf_provider self) {
     }
     p->ring_ready = false;
   }
+  (void)hipFree(p->ws.part);
+  (void)hipFree(p->ws.cnt);
+  p->ws = Workspace{};
   (void)hipStreamDestroy(p->stream);
   p->stream = nullptr;
   p->initialized = false;
@@ -394,7 +413,7 @@ const nf_task_desc* enclosing_task(const nf_buffer* inputs) {
   return reinterpret_cast<const nf_task_desc*>(base);
 }
 
-hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, hipStream_t s) {
+hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, const Workspace& ws, hipStream_t s) {
   switch (pl.path) {
     case Path::Dequant:
       return launch_dequant(pl.q, pl.c, in[0]->dev, out[0]->dev, pl.count, s);
@@ -412,7 +431,7 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, hipSt
         const uint32_t mc = pl.M - m0 < rows ? pl.M - m0 : rows;
         const hipError_t e = launch_skinny(pl.q, pl.c, static_cast<const char*>(in[0]->dev) + (size_t)m0 * pl.K * ea,
                                            in[1]->dev, static_cast<char*>(out[0]->dev) + (size_t)m0 * pl.N * ec, mc,
-                                           pl.N, pl.K, s);
+                                           pl.N, pl.K, ws, s);
         if (e != hipSuccess) return e;
       }
       return hipSuccess;
@@ -486,7 +505,7 @@ nf_status hip_dispatch(nf_provider self, const char* op_name, const nf_buffer* i
       rec->elems = (uint32_t)(pl.path == Path::Dequant ? pl.count : (uint64_t)pl.M * pl.N);
       (void)hipEventRecord(rec->start, p->stream);
     }
-    e = run_plan(pl, in, out, p->stream);
+    e = run_plan(pl, in, out, p->ws, p->stream);
     if (rec) (void)hipEventRecord(rec->stop, p->stream);
     for (uint32_t i = 0; i < n_out; ++i) out[i]->last_write_seq.store(seq);
   }

@@ -150,6 +150,22 @@ def test_skinny_mfma_shapes(provider, oracle_mod, fmt, f16, shape):
         provider.set_skinny_max_m(old[1])
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("shape", [(4, 300, 4096), (3, 130, 5632), (4, 64, 7168)], ids=lambda s: "x".join(map(str, s)))
+def test_gemv_large_activation_staging(provider, oracle_mod, fmt, f16, shape):
+    """GEMV with the activations' LDS stage above 64 KB (opt-in dynamic LDS):
+    M = 3..4 rows of long K."""
+    M, N, K = shape
+    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    try:
+        _force_path(provider, "gemv", f16)
+        check_fused(provider, oracle_mod, fmt, M, N, K, f16=f16, seed=M + N + K)
+    finally:
+        provider.set_gemv_max_m(*old[0])
+        provider.set_skinny_max_m(old[1])
+
+
 def test_skinny_f32_large_activations(provider, oracle_mod):
     """The exact three-way bf16 split keeps f32 activations far outside the
     fp16 range (|x| ~ 1e6 and 1e-6) exact before accumulation."""

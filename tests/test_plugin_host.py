@@ -120,8 +120,8 @@ def test_plan_path_follows_output_dtype(lib):
 
 
 def test_plan_q8_0_and_ragged_k(lib):
-    p = plan(lib, "dequant_q8_0_linear", [D(abi.NF_DTYPE_F32, 4 * 256 * 4), D(abi.NF_DTYPE_Q8_0, 7 * 8 * 34)],
-             [D(abi.NF_DTYPE_F32, 4 * 7 * 4)], 4, 7, 256)
+    p = plan(lib, "dequant_q8_0_linear", [D(abi.NF_DTYPE_F32, 5 * 256 * 4), D(abi.NF_DTYPE_Q8_0, 7 * 8 * 34)],
+             [D(abi.NF_DTYPE_F32, 5 * 7 * 4)], 5, 7, 256)
     assert p["kernel"] == "skinny_mfma_q8_0_f32" and p["weight_bytes"] == 7 * 8 * 34
     # K % 256 != 0: the small-batch MFMA kernel stages four block pairs at a time
     p = plan(lib, "dequant_q8_0_linear", [D(abi.NF_DTYPE_F32, 4 * 64 * 4), D(abi.NF_DTYPE_Q8_0, 7 * 2 * 34)],
@@ -215,12 +215,15 @@ def test_crossover_setter_roundtrip():
 
 
 def test_default_switch_points(lib):
-    """Defaults from the configs[4] sweep: GEMV for M <= 2, the small-batch
-    MFMA kernel up to 64 rows, the tiled GEMM beyond (f16)."""
+    """Defaults from the measured sweep: GEMV for M <= 4 while its activation
+    stage fits in 120 KB of LDS, the small-batch MFMA kernel up to 64 rows,
+    the tiled GEMM beyond (f16)."""
     f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
-    assert _fused(lib, 2, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"
-    assert _fused(lib, 3, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
+    assert _fused(lib, 4, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"   # 4 x 8192 x 2 B = 64 KB
+    assert _fused(lib, 5, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
     assert _fused(lib, 64, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
     assert _fused(lib, 65, 28672, 8192, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
-    assert _fused(lib, 2, 4096, 4096)["kernel"] == "gemv_q4_0_f32"
+    assert _fused(lib, 4, 4096, 4096)["kernel"] == "gemv_q4_0_f32"
+    assert _fused(lib, 2, 28672, 8192)["kernel"] == "gemv_q4_0_f32"           # 2 x 8192 x 4 B + sums
+    assert _fused(lib, 3, 28672, 8192)["kernel"] == "skinny_mfma_q4_0_f32"    # 4 x 8192 x 4 B > 120 KB
     assert _fused(lib, 16, 4096, 4096)["kernel"] == "skinny_mfma_q4_0_f32"
