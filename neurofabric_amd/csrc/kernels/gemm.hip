@@ -30,6 +30,7 @@
 // built from v_mfma_f32_16x16x32_f16, one block per K step.
 #include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "../launch.hpp"
 #include "common.hpp"
@@ -334,11 +335,13 @@ __device__ __forceinline__ void xcd_tile(int bid, int mt, int nt, int& tm, int& 
 //   * W of step s+1 (fetched one step earlier) is dequantized to fp16 and
 //     written into the other stage;
 //   * one barrier.
-template <class QF, int BM, int BN, int WGM, int WGN, int NS>
+template <class QF, int BM, int BN, int WGM, int WGN, int NS, bool SPLIT>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half_t* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
                                                                     half_t* __restrict__ C, int M,
-                                                                    int N, int K) {
+                                                                    int N, int K,
+                                                                    float* __restrict__ ws_part,
+                                                                    uint32_t* __restrict__ ws_cnt) {
   constexpr int NWAVE = WGM * WGN;
   constexpr int NT = 64 * NWAVE;
   constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;
@@ -356,7 +359,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
   int tm, tn;
   xcd_tile(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int nk = K / kBK;
+  // Split K: the KG = gridDim.y workgroups of a tile take contiguous ranges
+  // of K steps.
+  const int KG = SPLIT ? (int)gridDim.y : 1, kg = SPLIT ? (int)blockIdx.y : 0;
+  const int nk_all = K / kBK;
+  const int k_first = (int)((long)nk_all * kg / KG);
+  const int nk = (int)((long)nk_all * (kg + 1) / KG) - k_first;
 
   // A: lane -> (row within its 8-row group, chunk slot); the global chunk is
   // the one the swizzle places in that slot.  Rows past M read row M-1
@@ -367,7 +375,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
     const int r = (wave * A_DMA + i) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     const int gr = m0 + r < M ? m0 + r : M - 1;
-    asrc[i] = A + (size_t)gr * K + c * 8;
+    asrc[i] = A + (size_t)gr * K + (size_t)k_first * kBK + c * 8;
   }
   // Dense fp16 B: rows stream into LDS with the same mapping as A; rows past
   // N read row N-1 (their outputs are never stored).
@@ -382,7 +390,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
       const int r = (wave * B_DMA + i) * 8 + (lane >> 3);
       const int c = (lane & 7) ^ ((r >> 1) & 7);
       const int gr = n0 + r < N ? n0 + r : N - 1;
-      bsrc[i] = Bh + (size_t)gr * K + c * 8;
+      bsrc[i] = Bh + (size_t)gr * K + (size_t)k_first * kBK + c * 8;
     }
   }
   // W: thread -> (row, block); extra threads duplicate a row (identical
@@ -394,7 +402,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
   const uint8_t* wsrc = nullptr;
   if constexpr (!kDenseB) {
     const size_t row_bytes = (size_t)(K / 64) * GPair<QF>::kBytes;
-    wsrc = W + (size_t)(w_valid ? n0 + w_row : 0) * row_bytes + w_half * 4 * WBlk<QF>::kStride;
+    wsrc = W + (size_t)(w_valid ? n0 + w_row : 0) * row_bytes + (size_t)k_first * GPair<QF>::kBytes +
+           w_half * 4 * WBlk<QF>::kStride;
   }
 
   auto dma_a = [&](int ks, int buf) {
@@ -520,18 +529,62 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
 
   // epilogue: round to fp16 and store
   const int col = lane & 31, rq = (lane >> 5) * 4;
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int gn = n0 + wn + 32 * j + col;
+        if (gn >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int gm = m0 + wm + 32 * i + (r >> 2) * 8 + rq + (r & 3);
+          if (gm < M) C[(size_t)gm * N + gn] = (half_t)acc[i][j][r];
+        }
+      }
+  };
+  if constexpr (!SPLIT) {
+    store();
+    return;
+  }
+  // Split K across workgroups: each parks its fp32 accumulators in the
+  // workspace (value (i, j, r) of thread tid at ((i*TN + j)*16 + r)*NT + tid);
+  // the last workgroup of the tile to arrive (per-tile counter, agent-scope
+  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1, its own
+  // from registers, stores C and resets the counter.
+  const int tile = blockIdx.x;
+  float* tile_ws = ws_part + (size_t)tile * KG * (BM * BN);
+  {
+    float* mine = tile_ws + (size_t)kg * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mine[((i * TN + j) * 16 + r) * NT + tid] = acc[i][j][r];
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ uint32_t is_last;
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == (uint32_t)(KG - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int gn = n0 + wn + 32 * j + col;
-      if (gn >= N) continue;
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + wm + 32 * i + (r >> 2) * 8 + rq + (r & 3);
-        if (gm < M) C[(size_t)gm * N + gn] = (half_t)acc[i][j][r];
+        float sum = 0.f;
+        for (int g = 0; g < KG; ++g)
+          sum += g == kg ? acc[i][j][r] : tile_ws[(size_t)g * (BM * BN) + ((i * TN + j) * 16 + r) * NT + tid];
+        acc[i][j][r] = sum;
       }
-    }
+  store();
+  if (tid == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -648,17 +701,41 @@ inline int pick_tile(uint32_t M, uint32_t N) {
 
 template <class QF, int BM, int BN, int WGM, int WGN, int NS = 2>
 hipError_t gemm_tile_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_t M, uint32_t N,
-                            uint32_t K, hipStream_t s) {
+                            uint32_t K, const nfhip::Workspace& ws, hipStream_t s) {
   const long tiles = (long)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
   if (tiles > (1L << 31) - 1) return hipErrorInvalidConfiguration;
-  const dim3 grid((unsigned)tiles);
+  // Split K over 2, 4, ... workgroups per tile while the grid is below one
+  // workgroup per CU and every part keeps at least 64 K steps (measured on
+  // MI355X: shorter parts lose more to the fix-up than the wider grid gains);
+  // bounded by the workspace.
+  const int nk = (int)(K / kBK);
+  static const int kg_max = [] {
+    const char* e = std::getenv("NF_HIP_GEMM_SPLITK_MAX");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 ? v : 8;
+  }();
+  int kg = 1;
+  while (kg < kg_max && tiles * kg < 256 && nk >= 128 * kg && tiles <= (long)ws.cnt_len &&
+         (size_t)tiles * 2 * kg * BM * BN <= ws.part_floats)
+    kg *= 2;
   const size_t lds = (size_t)NS * (BM + BN) * 64 * sizeof(half_t);
   // More than 64 KB of dynamic LDS must be allowed explicitly, once per kernel.
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (attr != hipSuccess) return attr;
-  gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS><<<grid, dim3(64 * WGM * WGN), lds, s>>>(a, w, c, M, N, K);
+  if (kg == 1) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, false>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, false><<<dim3((unsigned)tiles), dim3(64 * WGM * WGN), lds, s>>>(
+        a, w, c, M, N, K, ws.part, ws.cnt);
+  } else {
+    if constexpr (std::is_same<QF, F16B>::value) return hipErrorInvalidValue;  // dense path never splits
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, true>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, true><<<dim3((unsigned)tiles, (unsigned)kg), dim3(64 * WGM * WGN), lds, s>>>(
+        a, w, c, M, N, K, ws.part, ws.cnt);
+  }
   return hipGetLastError();
 }
 
@@ -674,18 +751,18 @@ hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t
   nfk::half_t* c = static_cast<nfk::half_t*>(C);
   if (K % 64 != 0 || (uintptr_t)A % 16 != 0 || (uintptr_t)B % 16 != 0) return hipErrorInvalidValue;
   switch (nfk::pick_tile(M, N)) {
-    case 0: return nfk::gemm_tile_launch<nfk::F16B, 256, 256, 2, 4>(a, b, c, M, N, K, s);
-    case 1: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 4, 2>(a, b, c, M, N, K, s);
-    case 3: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2>(a, b, c, M, N, K, s);
-    case 4: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2, 3>(a, b, c, M, N, K, s);
-    case 5: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2, 3>(a, b, c, M, N, K, s);
-    case 6: return nfk::gemm_tile_launch<nfk::F16B, 128, 256, 2, 4>(a, b, c, M, N, K, s);
-    default: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2>(a, b, c, M, N, K, s);
+    case 0: return nfk::gemm_tile_launch<nfk::F16B, 256, 256, 2, 4>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 1: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 4, 2>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 3: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 4: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2, 3>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 5: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2, 3>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 6: return nfk::gemm_tile_launch<nfk::F16B, 128, 256, 2, 4>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    default: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2>(a, b, c, M, N, K, nfhip::Workspace{}, s);
   }
 }
 
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
-                            uint32_t N, uint32_t K, hipStream_t s) {
+                            uint32_t N, uint32_t K, const Workspace& ws, hipStream_t s) {
   if (t != EType::F16) return hipErrorInvalidValue;  // f32 path uses the skinny kernels
   const nfk::half_t* a = static_cast<const nfk::half_t*>(A);
   const uint8_t* w = static_cast<const uint8_t*>(W);
@@ -694,26 +771,26 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
   if (K % 64 == 0 && aligned) {
     switch (nfk::pick_tile(M, N)) {
       case 0:
-        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 256, 2, 4>(a, w, c, M, N, K, s)
-                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 256, 2, 4>(a, w, c, M, N, K, s);
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 256, 2, 4>(a, w, c, M, N, K, ws, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 256, 2, 4>(a, w, c, M, N, K, ws, s);
       case 1:
-        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 4, 2>(a, w, c, M, N, K, s)
-                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 4, 2>(a, w, c, M, N, K, s);
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 4, 2>(a, w, c, M, N, K, ws, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 4, 2>(a, w, c, M, N, K, ws, s);
       case 3:
-        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 2, 2>(a, w, c, M, N, K, s)
-                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 2, 2>(a, w, c, M, N, K, s);
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 2, 2>(a, w, c, M, N, K, ws, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 2, 2>(a, w, c, M, N, K, ws, s);
       case 4:
-        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 2, 2, 3>(a, w, c, M, N, K, s)
-                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 2, 2, 3>(a, w, c, M, N, K, s);
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 128, 2, 2, 3>(a, w, c, M, N, K, ws, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 256, 128, 2, 2, 3>(a, w, c, M, N, K, ws, s);
       case 5:
-        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2, 3>(a, w, c, M, N, K, s)
-                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2, 3>(a, w, c, M, N, K, s);
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2, 3>(a, w, c, M, N, K, ws, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2, 3>(a, w, c, M, N, K, ws, s);
       case 6:
-        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 256, 2, 4>(a, w, c, M, N, K, s)
-                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 256, 2, 4>(a, w, c, M, N, K, s);
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 256, 2, 4>(a, w, c, M, N, K, ws, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 256, 2, 4>(a, w, c, M, N, K, ws, s);
       default:
-        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2>(a, w, c, M, N, K, s)
-                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2>(a, w, c, M, N, K, s);
+        return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 128, 128, 2, 2>(a, w, c, M, N, K, ws, s)
+                                 : nfk::gemm_tile_launch<nfk::Q8_0, 128, 128, 2, 2>(a, w, c, M, N, K, ws, s);
     }
   }
   const dim3 grid((N + nfk::kTile - 1) / nfk::kTile, (M + nfk::kTile - 1) / nfk::kTile);

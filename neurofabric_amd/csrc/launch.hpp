@@ -38,7 +38,7 @@ hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C,
                          uint32_t K, const Workspace& ws, hipStream_t s);
 
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
-                            uint32_t N, uint32_t K, hipStream_t s);
+                            uint32_t N, uint32_t K, const Workspace& ws, hipStream_t s);
 
 hipError_t launch_generic(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                           uint32_t N, uint32_t K, hipStream_t s);

@@ -422,7 +422,7 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, const
     case Path::Skinny: {
       if (!skinny_fits(1, pl.N, pl.K, in[0]->dev, in[1]->dev))  // odd alignment (imported buffers)
         return pl.c == EType::F16
-                   ? launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s)
+                   ? launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, ws, s)
                    : launch_gemv(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
       // at most skinny_max_rows activation rows per launch
       const size_t ea = pl.a == EType::F16 ? 2 : 4, ec = pl.c == EType::F16 ? 2 : 4;
@@ -437,7 +437,7 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, const
       return hipSuccess;
     }
     case Path::GemmMfma:
-      return launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
+      return launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, ws, s);
     case Path::Generic:
       return launch_generic(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
     case Path::Dense:

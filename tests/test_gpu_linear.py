@@ -166,6 +166,30 @@ def test_gemv_large_activation_staging(provider, oracle_mod, fmt, f16, shape):
         provider.set_skinny_max_m(old[1])
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("shape", [(200, 520, 8192), (130, 300, 16384), (512, 4096, 11008)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_tiled_gemm_split_k(provider, oracle_mod, fmt, shape):
+    """Tiled MFMA GEMM with fewer tiles than CUs and long K: K is split over
+    2-4 workgroups per tile and the last one adds the partial tiles.  Two
+    calls in a row: the per-tile counters must be back at zero after each."""
+    M, N, K = shape
+    W = syn.weights(fmt, N, K, seed=N + 1)
+    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    try:
+        _force_path(provider, "tiled", True)
+        for rep in range(2):
+            A = syn.activations(M, K, seed=K + rep, dtype=np.float16)
+            cols = (0, N) if N <= 520 else (N - 256, N)
+            ref = oracle_mod.fused(A, W, fmt, M, N, K, f16=True, cols=cols, threads=8).view(np.float16)
+            got = run_fused(provider, fmt, A, W, M, N, K, True)
+            assert_close(got[:, cols[0]:cols[1]].astype(np.float32), ref[:, cols[0]:cols[1]].astype(np.float32),
+                         what=f"{fmt} {M}x{N}x{K} call {rep}")
+    finally:
+        provider.set_gemv_max_m(*old[0])
+        provider.set_skinny_max_m(old[1])
+
+
 def test_skinny_f32_large_activations(provider, oracle_mod):
     """The exact three-way bf16 split keeps f32 activations far outside the
     fp16 range (|x| ~ 1e6 and 1e-6) exact before accumulation."""
