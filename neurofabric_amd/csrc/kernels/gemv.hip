@@ -125,19 +125,24 @@ __device__ __forceinline__ void pair_f32_q4(const uint32_t (&w)[R2][9], const fl
                                             float inv_unit, float (&acc)[R2][MM]) {
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
-    float s[R2][MM];
+    // four independent FMA chains per block (one per code dword), added at
+    // the end, so consecutive FMAs do not wait on each other
+    float s[4][R2][MM];
+    // all of the block's activation chunks are requested from LDS before
+    // any arithmetic, so their latencies overlap
+    float4v xa[4][MM], xb[4][MM];
 #pragma unroll
-    for (int j = 0; j < R2; ++j)
-#pragma unroll
-      for (int m = 0; m < MM; ++m) s[j][m] = 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      float4v xl[MM], xh[MM];
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
-        xl[m] = xs[xslot<float>(m, P, pair, blk * 8 + t)];
-        xh[m] = xs[xslot<float>(m, P, pair, blk * 8 + 4 + t)];
+        xa[t][m] = xs[xslot<float>(m, P, pair, blk * 8 + t)];
+        xb[t][m] = xs[xslot<float>(m, P, pair, blk * 8 + 4 + t)];
       }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float4v* xl = xa[t];
+      const float4v* xh = xb[t];
 #pragma unroll
       for (int j = 0; j < R2; ++j) {
         const uint32_t q = code_dword<Q4_0>(w[j], blk, t);
@@ -149,8 +154,7 @@ __device__ __forceinline__ void pair_f32_q4(const uint32_t (&w)[R2][9], const fl
         const float2v e = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
-          float v = s[j][m];
-          v = __builtin_fmaf(a.x, xl[m].x, v);
+          float v = a.x * xl[m].x;
           v = __builtin_fmaf(a.y, xl[m].y, v);
           v = __builtin_fmaf(b.x, xl[m].z, v);
           v = __builtin_fmaf(b.y, xl[m].w, v);
@@ -158,7 +162,7 @@ __device__ __forceinline__ void pair_f32_q4(const uint32_t (&w)[R2][9], const fl
           v = __builtin_fmaf(c.y, xh[m].y, v);
           v = __builtin_fmaf(e.x, xh[m].z, v);
           v = __builtin_fmaf(e.y, xh[m].w, v);
-          s[j][m] = v;
+          s[t][j][m] = v;
         }
       }
     }
@@ -166,8 +170,10 @@ __device__ __forceinline__ void pair_f32_q4(const uint32_t (&w)[R2][9], const fl
     for (int j = 0; j < R2; ++j) {
       const float d = h2f_bits((uint16_t)scale_bits<Q4_0>(w[j], blk)) * inv_unit;
 #pragma unroll
-      for (int m = 0; m < MM; ++m)
-        acc[j][m] = __builtin_fmaf(d, s[j][m] - sxs[(m * P + pair) * 2 + blk], acc[j][m]);
+      for (int m = 0; m < MM; ++m) {
+        const float sum = (s[0][j][m] + s[1][j][m]) + (s[2][j][m] + s[3][j][m]);
+        acc[j][m] = __builtin_fmaf(d, sum - sxs[(m * P + pair) * 2 + blk], acc[j][m]);
+      }
     }
   }
 }
@@ -178,16 +184,17 @@ __device__ __forceinline__ void pair_f32_q8(const uint32_t (&w)[R2][17], const f
                                             int P, int pair, float (&acc)[R2][MM]) {
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
-    float s[R2][MM];
+    // four independent FMA chains per block (code dwords t and t+4 share one)
+    float s[4][R2][MM];
+    float4v xall[8][MM];
 #pragma unroll
-    for (int j = 0; j < R2; ++j)
+    for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int m = 0; m < MM; ++m) s[j][m] = 0.f;
+      for (int m = 0; m < MM; ++m) xall[t][m] = xs[xslot<float>(m, P, pair, blk * 8 + t)];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      float4v xv[MM];
-#pragma unroll
-      for (int m = 0; m < MM; ++m) xv[m] = xs[xslot<float>(m, P, pair, blk * 8 + t)];
+      const float4v* xv = xall[t];
 #pragma unroll
       for (int j = 0; j < R2; ++j) {
         const uint32_t q = code_dword<Q8_0>(w[j], blk, t);
@@ -197,12 +204,11 @@ __device__ __forceinline__ void pair_f32_q8(const uint32_t (&w)[R2][17], const f
         const float f3 = (float)((int32_t)q >> 24);
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
-          float v = s[j][m];
-          v = __builtin_fmaf(f0, xv[m].x, v);
+          float v = t < 4 ? f0 * xv[m].x : __builtin_fmaf(f0, xv[m].x, s[t & 3][j][m]);
           v = __builtin_fmaf(f1, xv[m].y, v);
           v = __builtin_fmaf(f2, xv[m].z, v);
           v = __builtin_fmaf(f3, xv[m].w, v);
-          s[j][m] = v;
+          s[t & 3][j][m] = v;
         }
       }
     }
@@ -210,7 +216,8 @@ __device__ __forceinline__ void pair_f32_q8(const uint32_t (&w)[R2][17], const f
     for (int j = 0; j < R2; ++j) {
       const float d = h2f_bits((uint16_t)scale_bits<Q8_0>(w[j], blk));
 #pragma unroll
-      for (int m = 0; m < MM; ++m) acc[j][m] = __builtin_fmaf(d, s[j][m], acc[j][m]);
+      for (int m = 0; m < MM; ++m)
+        acc[j][m] = __builtin_fmaf(d, (s[0][j][m] + s[1][j][m]) + (s[2][j][m] + s[3][j][m]), acc[j][m]);
     }
   }
 }
@@ -225,6 +232,15 @@ __device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kD
                                          float (&acc)[R2][MM]) {
   constexpr bool kQ4 = PairFmt<QF>::kQd == 4;
   constexpr int qd = PairFmt<QF>::kQd;
+  // four independent accumulation chains (code dword t feeds chain t & 3),
+  // folded into acc at the end of the pair
+  float part[4][R2][MM];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int j = 0; j < R2; ++j)
+#pragma unroll
+      for (int m = 0; m < MM; ++m) part[c][j][m] = 0.f;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     half8 xv[MM][4];
@@ -232,6 +248,7 @@ __device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kD
     for (int m = 0; m < MM; ++m)
 #pragma unroll
       for (int c = 0; c < 4; ++c) xv[m][c] = xs[xslot<half_t>(m, P, pair, blk * 4 + c)];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < R2; ++j) {
       const uint32_t db = scale_bits<QF>(w[j], blk);
@@ -254,12 +271,12 @@ __device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kD
             const half8 xl = xv[m][t >> 1];
             const half8 xh = xv[m][2 + (t >> 1)];
             const int o = (t & 1) * 4;
-            float v = acc[j][m];
+            float v = part[t & 3][j][m];
             v = __builtin_amdgcn_fdot2(w0, half2v{xl[o + 0], xl[o + 1]}, v, false);
             v = __builtin_amdgcn_fdot2(w1, half2v{xl[o + 2], xl[o + 3]}, v, false);
             v = __builtin_amdgcn_fdot2(w2, half2v{xh[o + 0], xh[o + 1]}, v, false);
             v = __builtin_amdgcn_fdot2(w3, half2v{xh[o + 2], xh[o + 3]}, v, false);
-            acc[j][m] = v;
+            part[t & 3][j][m] = v;
           }
         } else {
           // Q8_0: 4 signed codes -> elements 4t..4t+3 (chunk t/2, halves 4*(t&1)..)
@@ -271,15 +288,20 @@ __device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kD
           for (int m = 0; m < MM; ++m) {
             const half8 xc = xv[m][t >> 1];
             const int o = (t & 1) * 4;
-            float v = acc[j][m];
+            float v = part[t & 3][j][m];
             v = __builtin_amdgcn_fdot2(w0, half2v{xc[o + 0], xc[o + 1]}, v, false);
             v = __builtin_amdgcn_fdot2(w1, half2v{xc[o + 2], xc[o + 3]}, v, false);
-            acc[j][m] = v;
+            part[t & 3][j][m] = v;
           }
         }
       }
     }
   }
+#pragma unroll
+  for (int j = 0; j < R2; ++j)
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+      acc[j][m] += (part[0][j][m] + part[1][j][m]) + (part[2][j][m] + part[3][j][m]);
 }
 
 // ---- cross-lane sums --------------------------------------------------------
