@@ -111,6 +111,18 @@ NF_API void nf_hip_get_gemv_max_m(uint32_t *f32_path, uint32_t *f16_path);
 NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path);
 NF_API uint32_t nf_hip_get_skinny_max_m(void);
 
+/* Kernel of the fused f16 GEMM path (M above the small-batch range): -1
+ * (default) = the kernel that dequantizes weights in registers, measured
+ * fastest on MI355X; 0..6 = the kernel that dequantizes weight tiles into
+ * LDS, tile shape 256x256, 256x128, 128x128, 256x128 with 4 waves,
+ * 256x128 with 4 waves and 3 stages, 128x128 with 3 stages, 128x256.
+ * Other values mean -1.  Environment override NF_HIP_GEMM_TILE (the shape
+ * name or number) is read at nf_plugin_register.  No counterpart in the
+ * reference (its Metal provider has one fused GEMM kernel); this is
+ * process-wide tuning like the switch points above. */
+NF_API void nf_hip_set_gemm_tile(int32_t tile);
+NF_API int32_t nf_hip_get_gemm_tile(void);
+
 /* Dispatch `n_tasks` prepared task descriptors in order, `repeat` times —
  * a compiled step submitted with one call, the way Session::step walks its
  * plan (PipelineEngine.hpp:518-561) but without a thread hop per node.  Each

@@ -5,21 +5,21 @@
 // dequant_*_f16 produces — and multiplied with fp32 accumulation; C is
 // rounded to fp16.
 //
-// Big-tile kernel (K % 64 == 0), the MFMA-bound prefill path:
-//   * CTA tile 256(M) x 256(N), K step 64 (two 32-element blocks = one
-//     Q4_0/Q8_0 pair per weight row), 4 waves in a 2x2 arrangement, each
-//     owning a 128x128 sub-tile = 4x4 v_mfma_f32_32x32x16_f16 tiles with
-//     fp32 accumulators (256 per lane, held in AGPRs).
-//   * A tile and dequantized W tile live in LDS as fp16, double buffered,
-//     rows padded to 144 B so the 16 lanes of a ds_read_b128 phase (16
-//     consecutive rows, same 16-B column) land in 16 distinct bank groups.
-//   * Each of the 256 threads fetches the next step's A chunks (8 x 16 B)
-//     and one weight pair (36 B Q4_0 / 68 B Q8_0, dword-aligned loads)
-//     before the current step's MFMAs are issued, then dequantizes the pair
-//     (exact packed-f16 arithmetic) into the other LDS buffer; one barrier
-//     per K step.
-//   * Dequantization happens once per CTA per weight element; its VALU cost
-//     relative to the MFMA work shrinks with the 256-row M tile.
+// Three kernels:
+//   * register-dequantizing tiled kernel (gemm_wq_kernel, K % 64 == 0): the
+//     default prefill path.  Workgroup tile 128(M) x 256(N), 4 waves side by
+//     side along N, each owning 128x64 = 4x2 v_mfma_f32_32x32x16_f16 tiles.
+//     A goes through a two-stage LDS buffer; each wave loads its own weight
+//     blocks straight into registers four K steps ahead and dequantizes them
+//     there (weights never touch LDS, and no weight is dequantized twice).
+//     The issue order of each K step is fixed slot by slot so that loads,
+//     LDS writes and dequantization VALU sit in the shadow of the MFMAs.
+//   * LDS-staged tiled kernel (gemm_tile_kernel, K % 64 == 0): A streams into
+//     LDS with direct-to-LDS loads, the workgroup dequantizes each weight
+//     tile once into LDS as fp16, and the waves read both operands from LDS;
+//     tile shapes 256x256 .. 128x128 (selectable; also the dense fp16 path).
+//   * small-tile kernel (any K % 32 == 0): fallback for shapes the two above
+//     do not take.
 //
 // MFMA 32x32x16 f16 operand layout (lane l of a wave64):
 //   A: row l%32, k = 8*(l/32) .. +7     (8 halves, one ds_read_b128)
@@ -588,6 +588,376 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
 }
 
 // ---------------------------------------------------------------------------
+// quantized-W tiled kernel: weights dequantized in registers, A through LDS
+//
+// Each wave owns a 32*TM (M) x 32*TN (N) output tile; the NW waves of a
+// workgroup sit side by side along N and share one BM = 32*TM row block of
+// A in LDS.  The weights never touch LDS: lane (n = l%32, kb = l/32) loads,
+// for each of its TN weight rows, block kb of the step's Q4_0/Q8_0 pair
+// (5 / 9 dwords, dword-aligned window) PF steps ahead and dequantizes it to
+// 32 fp16 values one step ahead.
+//
+// K order inside a step: the MFMA sums over its 16 k slots, so any
+// permutation of the step's 64 k values that A and W share gives the same
+// sum.  Slice kk (0..3) pairs slot group kb with elements 8kk..8kk+7 of
+// block kb, i.e. step offset 32*kb + 8*kk: the weight operand is then dwords
+// 4kk..4kk+3 of the lane's own dequantized block, and the A operand is the
+// 16-B chunk 4*kb + kk of the row.
+//
+// The weight block is MFMA operand "A" and the activation operand "B", so
+// accumulator r of lane l is C[m = l%32][n = (r/4)*8 + (l/32)*4 + r%4]: four
+// consecutive columns of one row per r/4, stored as one 8-byte write.
+//
+// A is prefetched PF steps ahead into registers (16 B per lane per 8 rows)
+// and written to a two-stage LDS buffer one step ahead.  Every load has a
+// register destination, so the compiler's wait insertion tracks each one
+// exactly and waits only for the oldest (direct-to-LDS loads would make it
+// drain the whole queue before each use of a weight register).
+//
+// Per step s (LDS stage s & 1):
+//   * slices 0-2: operand reads of the next slice, then this slice's MFMAs;
+//     in their shadow: W(s+1) dequantized, A(s+1) written to stage
+//     (s+1) & 1, and W(s+PF), A(s+PF) loaded;
+//   * one barrier (every wave's A(s+1) writes are done and every wave has
+//     read its last operands from stage s & 1);
+//   * slice 0 of step s+1 is read, and the slice-3 MFMAs of step s
+//     (operands already in registers) run.
+template <class QF, int TM, int TN, int NW, int PF, bool SPLIT>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_wq_kernel(const half_t* __restrict__ A,
+                                                             const uint8_t* __restrict__ W,
+                                                             half_t* __restrict__ C, int M, int N, int K,
+                                                             float* __restrict__ ws_part,
+                                                             uint32_t* __restrict__ ws_cnt) {
+  constexpr int BM = 32 * TM, BN = 32 * TN * NW, NT = 64 * NW;
+  constexpr int STAGE = BM * 64;      // halves per LDS stage
+  constexpr int A_LD = BM / 8 / NW;   // 16-B A loads per lane per step
+  constexpr int WD = WBlk<QF>::kDwords;
+  static_assert(PF == 2 || PF == 4, "even prefetch depth (register sets alternate by step parity)");
+  static_assert(BM % (8 * NW) == 0, "A rows per wave");
+  extern __shared__ __attribute__((aligned(16))) half_t lds[];  // [2][BM][64]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r32 = lane & 31, kb = lane >> 5;
+  int tm, tn;
+  xcd_tile(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN, wn = wave * 32 * TN;
+  const int KG = SPLIT ? (int)gridDim.y : 1, kg = SPLIT ? (int)blockIdx.y : 0;
+  const int nk_all = K / kBK;
+  const int k_first = (int)((long)nk_all * kg / KG);
+  const int nk = (int)((long)nk_all * (kg + 1) / KG) - k_first;
+
+  // A: load i of a lane covers row (wave*A_LD + i)*8 + l/8, chunk l%8 (eight
+  // lanes read one row's 128 B).  Rows past M read row M-1 (their outputs
+  // are never stored).
+  const half_t* asrc[A_LD];
+  int adst[A_LD];
+#pragma unroll
+  for (int i = 0; i < A_LD; ++i) {
+    const int r = (wave * A_LD + i) * 8 + (lane >> 3);
+    const int gr = m0 + r < M ? m0 + r : M - 1;
+    asrc[i] = A + (size_t)gr * K + (size_t)k_first * kBK + (lane & 7) * 8;
+    adst[i] = tile_off(r, lane & 7);
+  }
+  // W: frag j of this lane is row n0 + wn + 32j + r32, block kb of each pair.
+  // Rows past N read row 0 with the scale forced to zero.
+  const size_t row_bytes = (size_t)(K / 64) * GPair<QF>::kBytes;
+  const uint32_t w_sel = kb ? 0x07060504u : 0x05040302u, w_sh = kb ? 16u : 0u;
+  const uint8_t* wsrc[TN];
+  bool w_valid[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn + 32 * j + r32;
+    w_valid[j] = n < N;
+    wsrc[j] = W + (size_t)(w_valid[j] ? n : 0) * row_bytes + (size_t)k_first * GPair<QF>::kBytes +
+              kb * 4 * WBlk<QF>::kStride;
+  }
+
+  u32x4 ra[PF][A_LD];
+  auto load_a = [&](int ks, int set) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) ra[set][i] = *reinterpret_cast<const u32x4*>(asrc[i] + (size_t)ks * kBK);
+  };
+  auto write_a = [&](int set, int stage) {
+    half_t* dst = lds + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) *reinterpret_cast<u32x4*>(dst + adst[i]) = ra[set][i];
+  };
+  uint32_t wr[PF][TN][WD];
+  auto load_w = [&](int ks, int set) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) load_wblk<QF>(wsrc[j] + (size_t)ks * GPair<QF>::kBytes, wr[set][j]);
+  };
+  uint32_t bq[2][TN][16];
+  auto dequant = [&](int set, int buf) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) dequant_wblk<QF>(wr[set][j], w_sel, w_sh, w_valid[j], bq[buf][j]);
+  };
+  half8 af[2][TM];
+  auto read_a = [&](int stage, int kk, int buf) {
+    const half_t* As = lds + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      af[buf][i] = *reinterpret_cast<const half8*>(As + tile_off(32 * i + r32, 4 * kb + kk));
+  };
+  float16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
+  auto mfma = [&](int kk, int abuf, int wbuf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const u32x4 wv = {bq[wbuf][j][4 * kk + 0], bq[wbuf][j][4 * kk + 1], bq[wbuf][j][4 * kk + 2],
+                          bq[wbuf][j][4 * kk + 3]};
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, wv), af[abuf][i], acc[i][j],
+                                                           0, 0, 0);
+      }
+  };
+  // LDS operations of this wave done, then barrier.  The s_waitcnt builtin
+  // (lgkmcnt(0), vmcnt and expcnt untouched) is visible to the compiler's
+  // wait insertion; the empty asm statements keep memory accesses in place.
+  auto lds_barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: loads of steps 0..PF-1 (clamped: loads past the last step
+  // re-read it and are never used).
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    load_w(i < nk ? i : nk - 1, i);
+    load_a(i < nk ? i : nk - 1, i);
+  }
+  write_a(0, 0);
+  dequant(0, 0);
+  lds_barrier();
+  read_a(0, 0, 0);
+
+  // Issue order of a step, fixed slot by slot (sched_barrier between
+  // slots).  A wave stalls at issue when the vector-memory queue is full,
+  // and with one wave per SIMD nothing else feeds the MFMA pipe meanwhile;
+  // left alone the compiler bunches the loads and the dequantization VALU.
+  // So each MFMA is followed by at most one small piece of other work, about
+  // as much VALU as fits in the issue shadow of one 32-cycle MFMA (six):
+  //   slices 0-2 (MFMA idx 0..23): idx % 3 == 1: one global load of step
+  //     s+PF; idx 14, 17, 20, 23: one LDS write of A(s+1); otherwise one
+  //     dequantization piece of W(s+1);
+  //   slice 3 (after the barrier, MFMA m 0..7): m < 4: dequantization
+  //     pieces; m = 4, 5: the remaining loads (Q8_0 has ten).
+  // A piece is half of one Q4_0 code dword (four weights) or one Q8_0 code
+  // dword (four weights): 16 per step.
+  static_assert(TM == 4 && TN == 2, "slot plan below is laid out for 4x2 tiles per wave");
+  static_assert(A_LD == 4 && TN * WBlk<QF>::kLoads + A_LD <= 10, "slot plan: at most 10 loads, 4 LDS writes");
+  constexpr bool kQ4 = std::is_same<QF, Q4_0>::value;
+  half2v dscale[TN];
+  uint32_t qword[TN];
+  auto dequant_piece = [&](int set, int buf, int piece) {
+    const int j = piece / 8;
+    const int t = kQ4 ? (piece / 2) % 4 : piece % 8;  // code dword within the block
+    if (piece % 8 == 0) {
+      uint32_t db = (wr[set][j][0] >> w_sh) & 0xFFFFu;
+      db = w_valid[j] ? db : 0u;
+      dscale[j] = h2_of(db | (db << 16));
+    }
+    if constexpr (kQ4) {
+      const half2v off = {(half_t)-1032.f, (half_t)-1032.f};
+      if (piece % 2 == 0) {
+        qword[j] = __builtin_amdgcn_perm(wr[set][j][t + 1], wr[set][j][t], w_sel);
+        const uint32_t l = qword[j] & 0x0F0F0F0Fu;
+        bq[buf][j][2 * t + 0] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, l, 0x04010400u)) + off) * dscale[j]);
+        bq[buf][j][2 * t + 1] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, l, 0x04030402u)) + off) * dscale[j]);
+      } else {
+        const uint32_t h = (qword[j] >> 4) & 0x0F0F0F0Fu;
+        bq[buf][j][8 + 2 * t + 0] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, h, 0x04010400u)) + off) * dscale[j]);
+        bq[buf][j][8 + 2 * t + 1] = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, h, 0x04030402u)) + off) * dscale[j]);
+      }
+    } else {
+      const uint32_t q = __builtin_amdgcn_perm(wr[set][j][t + 1], wr[set][j][t], w_sel);
+      uint32_t v[2];
+      q8_word_f16(q, dscale[j], v);
+      bq[buf][j][2 * t + 0] = v[0];
+      bq[buf][j][2 * t + 1] = v[1];
+    }
+  };
+  auto load_piece = [&](int ks, int set, int piece) {
+    constexpr int kWl = TN * WBlk<QF>::kLoads;
+    if (piece < kWl) {
+      const int j = piece / WBlk<QF>::kLoads, part = piece % WBlk<QF>::kLoads;
+      const uint8_t* p = wsrc[j] + (size_t)ks * GPair<QF>::kBytes;
+      if (part < WBlk<QF>::kDwords / 4) {
+        const u32x4 t = reinterpret_cast<const u32x4a4_g*>(p)[part];
+        wr[set][j][4 * part + 0] = t.x;
+        wr[set][j][4 * part + 1] = t.y;
+        wr[set][j][4 * part + 2] = t.z;
+        wr[set][j][4 * part + 3] = t.w;
+      } else {
+        wr[set][j][WD - 1] = reinterpret_cast<const uint32_t*>(p)[WD - 1];
+      }
+    } else if (piece < kWl + A_LD) {
+      const int i = piece - kWl;
+      ra[set][i] = *reinterpret_cast<const u32x4*>(asrc[i] + (size_t)ks * kBK);
+    }
+  };
+  auto mfma_one = [&](int kk, int i, int j, int abuf, int wbuf) {
+    const u32x4 wv = {bq[wbuf][j][4 * kk + 0], bq[wbuf][j][4 * kk + 1], bq[wbuf][j][4 * kk + 2],
+                      bq[wbuf][j][4 * kk + 3]};
+    acc[i][j] =
+        __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, wv), af[abuf][i], acc[i][j], 0, 0, 0);
+  };
+
+  // One K step; u = s % PF (compile time: the loop advances PF steps).
+  auto step = [&](auto uc, int s) {
+    constexpr int u = decltype(uc)::value;
+    constexpr int wb = u & 1;
+    const int ks = s + PF < nk ? s + PF : nk - 1;
+    int dq = 0;
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+      read_a(wb, kk + 1, (kk + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < TM * TN; ++m) {
+        const int idx = kk * TM * TN + m;
+        mfma_one(kk, m / TN, m % TN, kk & 1, wb);
+        if (idx % 3 == 1) {
+          load_piece(ks, u, idx / 3);
+        } else if (idx >= 14 && idx % 3 == 2) {
+          half_t* dst = lds + (wb ^ 1) * STAGE;
+          *reinterpret_cast<u32x4*>(dst + adst[(idx - 14) / 3]) = ra[(u + 1) % PF][(idx - 14) / 3];
+        } else {
+          dequant_piece((u + 1) % PF, wb ^ 1, dq++);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // PROBE_PRE_BARRIER
+    lds_barrier();
+    // PROBE_POST_BARRIER
+    read_a(wb ^ 1, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < TM * TN; ++m) {
+      mfma_one(3, m / TN, m % TN, 1, wb);
+      if (m < 4) dequant_piece((u + 1) % PF, wb ^ 1, dq++);
+      if (m == 4 || m == 5) load_piece(ks, u, 8 + (m - 4));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // PROBE_STEP_END
+  };
+  // PROBE_LOOP_BEGIN
+  int s = 0;
+  for (; s + PF <= nk; s += PF) {
+    step(std::integral_constant<int, 0>{}, s);
+    step(std::integral_constant<int, 1>{}, s + 1);
+    if constexpr (PF == 4) {
+      step(std::integral_constant<int, 2>{}, s + 2);
+      step(std::integral_constant<int, 3>{}, s + 3);
+    }
+  }
+  if (s < nk) step(std::integral_constant<int, 0>{}, s);
+  if (s + 1 < nk) step(std::integral_constant<int, 1>{}, s + 1);
+  if constexpr (PF == 4) {
+    if (s + 2 < nk) step(std::integral_constant<int, 2>{}, s + 2);
+  }
+
+  auto store = [&]() {
+    const bool vec = (N & 3) == 0 && ((uintptr_t)C & 7) == 0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int gm = m0 + 32 * i + r32;
+      if (gm >= M) continue;
+      half_t* crow = C + (size_t)gm * N;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int gn = n0 + wn + 32 * j + 8 * q + 4 * kb;
+          const half_t h0 = (half_t)acc[i][j][4 * q + 0], h1 = (half_t)acc[i][j][4 * q + 1];
+          const half_t h2 = (half_t)acc[i][j][4 * q + 2], h3 = (half_t)acc[i][j][4 * q + 3];
+          if (vec && gn + 3 < N) {
+            typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<half4v*>(crow + gn) = half4v{h0, h1, h2, h3};
+          } else {
+            if (gn + 0 < N) crow[gn + 0] = h0;
+            if (gn + 1 < N) crow[gn + 1] = h1;
+            if (gn + 2 < N) crow[gn + 2] = h2;
+            if (gn + 3 < N) crow[gn + 3] = h3;
+          }
+        }
+    }
+  };
+  if constexpr (!SPLIT) {
+    store();
+    return;
+  }
+  // Split K across workgroups: each parks its fp32 accumulators in the
+  // workspace as 16-byte groups (values 4q..4q+3 of tile (i, j) of thread tid
+  // at float4 index ((i*TN + j)*4 + q)*NT + tid, coalesced per wave); the
+  // last workgroup of the tile to arrive (per-tile counter, agent-scope
+  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1, its own
+  // from registers, stores C and resets the counter.  The partials of one
+  // (i, j) tile are loaded for every g before any is added, so a thread has
+  // 4*(KG-1) loads in flight rather than one.
+  const int tile = blockIdx.x;
+  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
+  {
+    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          mine[((i * TN + j) * 4 + q) * NT + tid] =
+              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ uint32_t is_last;
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == (uint32_t)(KG - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  constexpr int kMaxKG = 8;  // the launcher splits K at most 8 ways
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      float4v part[kMaxKG][4];
+#pragma unroll
+      for (int g = 0; g < kMaxKG; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (g < KG && g != kg) part[g][q] = tile_ws[(size_t)g * (BM * BN / 4) + ((i * TN + j) * 4 + q) * NT + tid];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float4v sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < kMaxKG; ++g) {
+          if (g >= KG) break;
+          sum += g == kg ? float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]}
+                         : part[g][q];
+        }
+        acc[i][j][4 * q + 0] = sum[0];
+        acc[i][j][4 * q + 1] = sum[1];
+        acc[i][j][4 * q + 2] = sum[2];
+        acc[i][j][4 * q + 3] = sum[3];
+      }
+    }
+  store();
+  if (tid == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // small-tile kernel (any K % 32 == 0)
 
 constexpr int kTile = 64;
@@ -663,27 +1033,21 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const half_t* __restric
       }
 }
 
-// Tile shape for the tiled MFMA kernel: 0 = 256x256 (8 waves, one CTA per
-// CU), 1 = 256x128 (8 waves, one CTA per CU), 2 = 128x128 (4 waves, two CTAs
-// per CU).  Score = fraction of CTA slots busy over the whole run (the last
-// round is usually partial) x the tile's relative per-CU efficiency, which
-// measured on MI355X at about 0.8 for the two smaller tiles against 256x256;
-// ties go to 128x128, whose two CTAs per CU hide each other's barriers.
-// NF_HIP_GEMM_TILE overrides the choice.
-inline int pick_tile(uint32_t M, uint32_t N) {
-  static const int forced = [] {
-    const char* e = std::getenv("NF_HIP_GEMM_TILE");  // "256x256", "256x128", "128x128" (or 0, 1, 2)
-    if (!e) return -1;
-    const std::string v(e);
-    if (v == "256x256") return 0;
-    if (v == "256x128") return 1;
-    if (v == "128x128") return 2;
-    if (v == "256x128w4") return 3;
-    if (v == "256x128w4s3") return 4;
-    if (v == "128x128s3") return 5;
-    if (v == "128x256") return 6;
-    return std::atoi(e);
-  }();
+// NF_HIP_GEMM_TILE for the dense fp16 path: an LDS-staged tile shape 0..6,
+// or -1 (automatic choice).
+inline int forced_tile() {
+  static const int forced = nfhip::gemm_tile_from_name(std::getenv("NF_HIP_GEMM_TILE"));
+  return forced;
+}
+
+// Tile shape for the LDS-staged tiled MFMA kernel: 0 = 256x256 (8 waves, one
+// CTA per CU), 1 = 256x128 (8 waves, one CTA per CU), 2 = 128x128 (4 waves,
+// two CTAs per CU).  Score = fraction of CTA slots busy over the whole run
+// (the last round is usually partial) x the tile's relative per-CU
+// efficiency, which measured on MI355X at about 0.8 for the two smaller
+// tiles against 256x256; ties go to 128x128, whose two CTAs per CU hide each
+// other's barriers.  NF_HIP_GEMM_TILE overrides the choice.
+inline int pick_tile(uint32_t M, uint32_t N, int forced) {
   if (forced >= 0 && forced <= 6) return forced;
   constexpr long kCUs = 256;
   auto fill = [](long tiles, long slots) {
@@ -739,6 +1103,50 @@ hipError_t gemm_tile_launch(const half_t* a, const uint8_t* w, half_t* c, uint32
   return hipGetLastError();
 }
 
+template <class QF, int TM, int TN, int NW, int PF>
+hipError_t gemm_wq_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_t M, uint32_t N, uint32_t K,
+                          const nfhip::Workspace& ws, hipStream_t s) {
+  constexpr int BM = 32 * TM, BN = 32 * TN * NW;
+  const long tiles = (long)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
+  if (tiles > (1L << 31) - 1) return hipErrorInvalidConfiguration;
+  // Split K over kg = 1, 2, 4, ... workgroups per tile: one workgroup per CU
+  // (256 CUs), so the run time goes as (rounds of 256 workgroups) x (K steps
+  // per workgroup); take the smallest kg that minimizes it, with at least 16
+  // K steps per part, bounded by the workspace.
+  const int nk = (int)(K / kBK);
+  static const int kg_max = [] {
+    const char* e = std::getenv("NF_HIP_GEMM_SPLITK_MAX");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 ? v : 8;
+  }();
+  constexpr long kCUs = 256;
+  int kg = 1;
+  long best = ((tiles + kCUs - 1) / kCUs) * nk;
+  for (int g = 2; g <= kg_max && g <= 8 && nk / g >= 16 && tiles <= (long)ws.cnt_len &&
+                  (size_t)tiles * g * BM * BN <= ws.part_floats;
+       g *= 2) {
+    const long cost = ((tiles * g + kCUs - 1) / kCUs) * ((nk + g - 1) / g);
+    if (cost < best) best = cost, kg = g;
+  }
+  const size_t lds = (size_t)2 * BM * 64 * sizeof(half_t);
+  if (kg == 1) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_wq_kernel<QF, TM, TN, NW, PF, false>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    gemm_wq_kernel<QF, TM, TN, NW, PF, false><<<dim3((unsigned)tiles), dim3(64 * NW), lds, s>>>(
+        a, w, c, M, N, K, ws.part, ws.cnt);
+  } else {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_wq_kernel<QF, TM, TN, NW, PF, true>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    gemm_wq_kernel<QF, TM, TN, NW, PF, true><<<dim3((unsigned)tiles, (unsigned)kg), dim3(64 * NW), lds, s>>>(
+        a, w, c, M, N, K, ws.part, ws.cnt);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace nfk
 
 namespace nfhip {
@@ -750,7 +1158,7 @@ hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t
   const uint8_t* b = static_cast<const uint8_t*>(B);
   nfk::half_t* c = static_cast<nfk::half_t*>(C);
   if (K % 64 != 0 || (uintptr_t)A % 16 != 0 || (uintptr_t)B % 16 != 0) return hipErrorInvalidValue;
-  switch (nfk::pick_tile(M, N)) {
+  switch (nfk::pick_tile(M, N, nfk::forced_tile())) {
     case 0: return nfk::gemm_tile_launch<nfk::F16B, 256, 256, 2, 4>(a, b, c, M, N, K, nfhip::Workspace{}, s);
     case 1: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 4, 2>(a, b, c, M, N, K, nfhip::Workspace{}, s);
     case 3: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2>(a, b, c, M, N, K, nfhip::Workspace{}, s);
@@ -762,14 +1170,20 @@ hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t
 }
 
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
-                            uint32_t N, uint32_t K, const Workspace& ws, hipStream_t s) {
+                            uint32_t N, uint32_t K, int tile, const Workspace& ws, hipStream_t s) {
   if (t != EType::F16) return hipErrorInvalidValue;  // f32 path uses the skinny kernels
   const nfk::half_t* a = static_cast<const nfk::half_t*>(A);
   const uint8_t* w = static_cast<const uint8_t*>(W);
   nfk::half_t* c = static_cast<nfk::half_t*>(C);
   const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
   if (K % 64 == 0 && aligned) {
-    switch (nfk::pick_tile(M, N)) {
+    // Default: the register-dequantizing kernel (measured faster than the
+    // LDS-staged tiles at every prefill shape with M > 64); tile 0..6 selects
+    // one of the LDS-staged tile shapes instead.
+    if (tile < 0 || tile > 6)
+      return (q == QFmt::Q4_0) ? nfk::gemm_wq_launch<nfk::Q4_0, 4, 2, 4, 4>(a, w, c, M, N, K, ws, s)
+                               : nfk::gemm_wq_launch<nfk::Q8_0, 4, 2, 4, 4>(a, w, c, M, N, K, ws, s);
+    switch (tile) {
       case 0:
         return (q == QFmt::Q4_0) ? nfk::gemm_tile_launch<nfk::Q4_0, 256, 256, 2, 4>(a, w, c, M, N, K, ws, s)
                                  : nfk::gemm_tile_launch<nfk::Q8_0, 256, 256, 2, 4>(a, w, c, M, N, K, ws, s);

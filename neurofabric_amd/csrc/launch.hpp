@@ -37,8 +37,10 @@ uint32_t skinny_max_rows(EType t);  // activation rows per launch
 hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M, uint32_t N,
                          uint32_t K, const Workspace& ws, hipStream_t s);
 
+// tile: Tuning::gemm_tile (-1 = register-dequantizing kernel, 0..6 = an
+// LDS-staged tile shape).
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
-                            uint32_t N, uint32_t K, const Workspace& ws, hipStream_t s);
+                            uint32_t N, uint32_t K, int tile, const Workspace& ws, hipStream_t s);
 
 hipError_t launch_generic(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                           uint32_t N, uint32_t K, hipStream_t s);

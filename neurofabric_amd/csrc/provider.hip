@@ -413,7 +413,8 @@ const nf_task_desc* enclosing_task(const nf_buffer* inputs) {
   return reinterpret_cast<const nf_task_desc*>(base);
 }
 
-hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, const Workspace& ws, hipStream_t s) {
+hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, int gemm_tile, const Workspace& ws,
+                    hipStream_t s) {
   switch (pl.path) {
     case Path::Dequant:
       return launch_dequant(pl.q, pl.c, in[0]->dev, out[0]->dev, pl.count, s);
@@ -422,7 +423,7 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, const
     case Path::Skinny: {
       if (!skinny_fits(1, pl.N, pl.K, in[0]->dev, in[1]->dev))  // odd alignment (imported buffers)
         return pl.c == EType::F16
-                   ? launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, ws, s)
+                   ? launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, gemm_tile, ws, s)
                    : launch_gemv(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
       // at most skinny_max_rows activation rows per launch
       const size_t ea = pl.a == EType::F16 ? 2 : 4, ec = pl.c == EType::F16 ? 2 : 4;
@@ -437,7 +438,7 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, const
       return hipSuccess;
     }
     case Path::GemmMfma:
-      return launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, ws, s);
+      return launch_gemm_mfma(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, gemm_tile, ws, s);
     case Path::Generic:
       return launch_generic(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
     case Path::Dense:
@@ -505,7 +506,7 @@ nf_status hip_dispatch(nf_provider self, const char* op_name, const nf_buffer* i
       rec->elems = (uint32_t)(pl.path == Path::Dequant ? pl.count : (uint64_t)pl.M * pl.N);
       (void)hipEventRecord(rec->start, p->stream);
     }
-    e = run_plan(pl, in, out, p->ws, p->stream);
+    e = run_plan(pl, in, out, p->tuning.gemm_tile, p->ws, p->stream);
     if (rec) (void)hipEventRecord(rec->stop, p->stream);
     for (uint32_t i = 0; i < n_out; ++i) out[i]->last_write_seq.store(seq);
   }
@@ -650,6 +651,7 @@ NF_API nf_status nf_plugin_register(nf_provider_vtable* vt, nf_provider* out) {
   g_prov.tuning.gemv_max_m_f32 = env_u32("NF_HIP_GEMV_MAX_M_F32", g_prov.tuning.gemv_max_m_f32);
   g_prov.tuning.gemv_max_m_f16 = env_u32("NF_HIP_GEMV_MAX_M_F16", g_prov.tuning.gemv_max_m_f16);
   g_prov.tuning.skinny_max_m_f16 = env_u32("NF_HIP_SKINNY_MAX_M_F16", g_prov.tuning.skinny_max_m_f16);
+  g_prov.tuning.gemm_tile = gemm_tile_from_name(std::getenv("NF_HIP_GEMM_TILE"));
   *out = reinterpret_cast<nf_provider>(&g_prov);
   return NF_OK;
 }
@@ -745,6 +747,13 @@ NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path) {
 }
 
 NF_API uint32_t nf_hip_get_skinny_max_m(void) { return g_prov.tuning.skinny_max_m_f16; }
+
+NF_API void nf_hip_set_gemm_tile(int32_t tile) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  g_prov.tuning.gemm_tile = (tile >= 0 && tile <= 6) ? tile : -1;
+}
+
+NF_API int32_t nf_hip_get_gemm_tile(void) { return g_prov.tuning.gemm_tile; }
 
 NF_API void nf_hip_get_gemv_max_m(uint32_t* f32_path, uint32_t* f16_path) {
   if (f32_path) *f32_path = g_prov.tuning.gemv_max_m_f32;

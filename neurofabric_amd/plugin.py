@@ -65,6 +65,10 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     lib.nf_hip_get_gemv_max_m.restype = None
     lib.nf_hip_set_skinny_max_m.argtypes = [C.c_uint32]
     lib.nf_hip_set_skinny_max_m.restype = None
+    lib.nf_hip_set_gemm_tile.argtypes = [C.c_int32]
+    lib.nf_hip_set_gemm_tile.restype = None
+    lib.nf_hip_get_gemm_tile.argtypes = []
+    lib.nf_hip_get_gemm_tile.restype = C.c_int32
     lib.nf_hip_get_skinny_max_m.argtypes = []
     lib.nf_hip_get_skinny_max_m.restype = C.c_uint32
     lib.nf_hip_get_stream.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
@@ -305,6 +309,13 @@ class Provider:
 
     def set_skinny_max_m(self, f16: int) -> None:
         self.lib.nf_hip_set_skinny_max_m(f16)
+
+    def set_gemm_tile(self, tile: int) -> None:
+        """-1: register-dequantizing GEMM kernel (default); 0..6: LDS-staged tile shapes."""
+        self.lib.nf_hip_set_gemm_tile(tile)
+
+    def get_gemm_tile(self) -> int:
+        return int(self.lib.nf_hip_get_gemm_tile())
 
     def get_skinny_max_m(self) -> int:
         return self.lib.nf_hip_get_skinny_max_m()

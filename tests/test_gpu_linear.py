@@ -190,6 +190,31 @@ def test_tiled_gemm_split_k(provider, oracle_mod, fmt, shape):
         provider.set_skinny_max_m(old[1])
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 5], ids=lambda t: "regdq" if t < 0 else f"lds{t}")
+@pytest.mark.parametrize("shape", [(129, 260, 64), (257, 514, 192), (130, 302, 320), (200, 777, 448)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemm_kernels_edges(provider, oracle_mod, fmt, tile, shape):
+    """Both f16 GEMM kernels (weights dequantized in registers: tile -1; into
+    LDS: tiles 0..6) against the oracle on ragged shapes: M and N past a tile
+    edge, N % 4 != 0 (element-wise stores), and 1, 3, 5 and 7 K steps, i.e.
+    fewer steps than the prefetch depth and every loop remainder."""
+    M, N, K = shape
+    W = syn.weights(fmt, N, K, seed=N + K)
+    A = syn.activations(M, K, seed=M + K, dtype=np.float16)
+    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m(), provider.get_gemm_tile())
+    try:
+        _force_path(provider, "tiled", True)
+        provider.set_gemm_tile(tile)
+        got = run_fused(provider, fmt, A, W, M, N, K, True)
+    finally:
+        provider.set_gemv_max_m(*old[0])
+        provider.set_skinny_max_m(old[1])
+        provider.set_gemm_tile(old[2])
+    ref = oracle_mod.fused(A, W, fmt, M, N, K, f16=True, threads=8).view(np.float16)
+    assert_close(got.astype(np.float32), ref.astype(np.float32), what=f"{fmt} tile {tile} {M}x{N}x{K}")
+
+
 def test_skinny_f32_large_activations(provider, oracle_mod):
     """The exact three-way bf16 split keeps f32 activations far outside the
     fp16 range (|x| ~ 1e6 and 1e-6) exact before accumulation."""
