@@ -126,10 +126,24 @@ NF_API int32_t nf_hip_get_gemm_tile(void);
 /* Dispatch `n_tasks` prepared task descriptors in order, `repeat` times —
  * a compiled step submitted with one call, the way Session::step walks its
  * plan (PipelineEngine.hpp:518-561) but without a thread hop per node.  Each
- * element goes through the same path as vtable.dispatch (same validation,
- * same stream); returns the first non-NF_OK status. */
+ * element goes through the same validation as vtable.dispatch, on the same
+ * stream; returns the first non-NF_OK status.  Because the whole batch is
+ * known, adjacent decode GEMVs that read the same activation buffer (same
+ * fused op, M and K; no output overlapping another member's inputs or
+ * output) are launched as one grouped kernel, up to four at a time: the
+ * results are bit-identical to dispatching them one by one, in order.  Not
+ * done while per-dispatch timing is enabled.  vtable.dispatch itself never
+ * defers or merges anything. */
 NF_API nf_status nf_hip_run_tasks(nf_provider self, const nf_task_desc *tasks, uint32_t n_tasks,
                                   uint32_t repeat);
+
+/* Launches enqueued since nf_plugin_register: one per dispatch, and one per
+ * group of decode GEMVs that nf_hip_run_tasks merged into a single launch
+ * (adjacent tasks of the same fused op reading the same activation buffer
+ * with the same M and K, with no buffer hazard between them: q/k/v,
+ * gate/up).  No counterpart in the reference; lets a caller relate a step's
+ * time to its kernel launches. */
+NF_API uint64_t nf_hip_launch_count(nf_provider self);
 
 /* The in-order hipStream_t (as void*) every dispatch is launched on, so a
  * caller can time or capture (hipStreamBeginCapture) a run of dispatches.

@@ -328,11 +328,40 @@ __device__ __forceinline__ float group_sum(float v, int log2L) {
 
 // ---- the pair kernel ------------------------------------------------------
 
+// Up to kGroupMax GEMVs over the same activations in one launch: job j owns
+// workgroups begin[j] .. begin[j+1]-1 and runs on its own weights, output and
+// N exactly as a launch of its own would (same geometry, same results).
+constexpr int kGroupMax = nfhip::kGemvGroupMax;
+struct GemvGroup {
+  const uint8_t* W[kGroupMax];
+  void* C[kGroupMax];
+  int N[kGroupMax];
+  int begin[kGroupMax + 1];
+  int count;
+};
+
 template <class QF, typename XT, int R2, int MM>
-__global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A,
-                                                        const uint8_t* __restrict__ W,
-                                                        XT* __restrict__ C, int M, int N, int K,
-                                                        int log2L) {
+__global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A, const GemvGroup grp, int M,
+                                                        int K, int log2L) {
+  // This workgroup's job (uniform; selects rather than an indexed load of
+  // the argument block).
+  int job = 0;
+#pragma unroll
+  for (int q = 1; q < kGroupMax; ++q) job = (q < grp.count && (int)blockIdx.x >= grp.begin[q]) ? q : job;
+  const uint8_t* __restrict__ W = grp.W[0];
+  void* Cv = grp.C[0];
+  int N = grp.N[0], wg0 = grp.begin[0], wg1 = grp.begin[1];
+#pragma unroll
+  for (int q = 1; q < kGroupMax; ++q)
+    if (job == q) {
+      W = grp.W[q];
+      Cv = grp.C[q];
+      N = grp.N[q];
+      wg0 = grp.begin[q];
+      wg1 = grp.begin[q + 1];
+    }
+  XT* __restrict__ C = static_cast<XT*>(Cv);
+  const int bid = (int)blockIdx.x - wg0, nwg = wg1 - wg0;
   constexpr bool kF32 = sizeof(XT) == 4;
   constexpr bool kQ4 = PairFmt<QF>::kQd == 4;
   constexpr bool kSx = kF32 && kQ4;  // block sums of x needed for the nibble offset
@@ -355,14 +384,14 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   const int R = 64 >> log2L;
   const int g = lane >> log2L, li = lane & (L - 1);
   const int rows_per_pass = 4 * R * R2;
-  const int pass_stride = gridDim.x * rows_per_pass;
+  const int pass_stride = nwg * rows_per_pass;
   const size_t row_bytes = (size_t)P * PairFmt<QF>::kBytes;
 
   // Iteration space of a lane group: npass passes over the grid's rows, IP
   // pair steps per pass (pair = li + L * step).  Both are uniform across the
   // workgroup, so every lane runs the same straight-line loop; loads past
   // the end are clamped to the last row / pair and never stored.
-  const int base0 = blockIdx.x * rows_per_pass;
+  const int base0 = bid * rows_per_pass;
   const int grp_row = base0 + (wave * R + g) * R2;
   const int IP = (P + L - 1) >> log2L;
   const int npass = base0 < N ? (N - 1 - base0) / pass_stride + 1 : 0;
@@ -607,17 +636,29 @@ inline int pick_log2L(int P) {
 constexpr size_t kPairMaxLds = 120 * 1024;
 
 template <class QF, typename XT, int R2, int MM>
-hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const void* W, void* C, uint32_t M,
-                            uint32_t N, uint32_t K, hipStream_t s) {
+hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const GemvGroup& grp, uint32_t M, uint32_t K,
+                            hipStream_t s) {
   if (g.lds > 64 * 1024) {
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_pair_kernel<QF, XT, R2, MM>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPairMaxLds);
     if (attr != hipSuccess) return attr;
   }
-  gemv_pair_kernel<QF, XT, R2, MM><<<dim3(g.grid), dim3(256), g.lds, s>>>(
-      static_cast<const XT*>(A), static_cast<const uint8_t*>(W), static_cast<XT*>(C), (int)M, (int)N,
-      (int)K, g.log2L);
+  gemv_pair_kernel<QF, XT, R2, MM><<<dim3(g.grid), dim3(256), g.lds, s>>>(static_cast<const XT*>(A), grp, (int)M,
+                                                                          (int)K, g.log2L);
   return hipGetLastError();
+}
+
+template <class QF, typename XT, int R2, int MM>
+hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const void* W, void* C, uint32_t M,
+                            uint32_t N, uint32_t K, hipStream_t s) {
+  GemvGroup grp{};
+  grp.W[0] = static_cast<const uint8_t*>(W);
+  grp.C[0] = C;
+  grp.N[0] = (int)N;
+  grp.begin[0] = 0;
+  for (int q = 1; q <= kGroupMax; ++q) grp.begin[q] = (int)g.grid;
+  grp.count = 1;
+  return gemv_pair_launch<QF, XT, R2, MM>(g, A, grp, M, K, s);
 }
 
 template <class QF, typename XT>
@@ -663,9 +704,56 @@ hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint
   }
 }
 
+// Geometry shared by the jobs of a group (same M, K): the single-launch
+// rules with one row per lane group; each job gets its own one-pass grid.
+template <class QF, typename XT>
+hipError_t gemv_group_dispatch(const void* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
+                               hipStream_t s) {
+  constexpr bool kF32 = sizeof(XT) == 4;
+  if (n < 1 || n > (uint32_t)kGroupMax || K % 64 != 0 || M < 1 || M > 4 || (uintptr_t)A % 16 != 0)
+    return hipErrorNotSupported;
+  PairGeom g;
+  const int P = (int)(K / 64);
+  g.MM = M == 1 ? 1 : (M == 2 ? 2 : 4);
+  g.lds = (size_t)g.MM * P * 64 * (kF32 ? 4 : 2) + ((kF32 && PairFmt<QF>::kQd == 4) ? (size_t)g.MM * P * 2 * 4 : 0);
+  if (g.lds > kPairMaxLds) return hipErrorNotSupported;
+  g.log2L = pick_log2L(P);
+  const int R = 64 >> g.log2L;
+  GemvGroup grp{};
+  long total = 0;
+  for (uint32_t j = 0; j < n; ++j) {
+    if ((uintptr_t)jobs[j].W % 4 != 0 || jobs[j].N == 0) return hipErrorNotSupported;
+    const long wgs1 = ((long)jobs[j].N + 4L * R - 1) / (4L * R);
+    if (wgs1 > 256L * 4) return hipErrorNotSupported;  // a single launch would loop over rows instead
+    grp.W[j] = static_cast<const uint8_t*>(jobs[j].W);
+    grp.C[j] = jobs[j].C;
+    grp.N[j] = (int)jobs[j].N;
+    grp.begin[j] = (int)total;
+    total += wgs1;
+  }
+  for (int q = (int)n; q <= kGroupMax; ++q) grp.begin[q] = (int)total;
+  grp.count = (int)n;
+  g.R2 = 1;
+  g.grid = (unsigned)total;
+  switch (g.MM) {
+    case 1: return gemv_pair_launch<QF, XT, 1, 1>(g, A, grp, M, K, s);
+    case 2: return gemv_pair_launch<QF, XT, 1, 2>(g, A, grp, M, K, s);
+    default: return gemv_pair_launch<QF, XT, 1, 4>(g, A, grp, M, K, s);
+  }
+}
+
 }  // namespace nfk
 
 namespace nfhip {
+
+hipError_t launch_gemv_group(QFmt q, EType t, const void* A, const GemvJob* jobs, uint32_t n, uint32_t M,
+                             uint32_t K, hipStream_t s) {
+  if (q == QFmt::Q4_0)
+    return t == EType::F32 ? nfk::gemv_group_dispatch<nfk::Q4_0, float>(A, jobs, n, M, K, s)
+                           : nfk::gemv_group_dispatch<nfk::Q4_0, nfk::half_t>(A, jobs, n, M, K, s);
+  return t == EType::F32 ? nfk::gemv_group_dispatch<nfk::Q8_0, float>(A, jobs, n, M, K, s)
+                         : nfk::gemv_group_dispatch<nfk::Q8_0, nfk::half_t>(A, jobs, n, M, K, s);
+}
 
 hipError_t launch_gemv(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                        uint32_t N, uint32_t K, hipStream_t s) {

@@ -30,6 +30,19 @@ hipError_t launch_dequant(QFmt q, EType out_t, const void* w, void* out, uint64_
 hipError_t launch_gemv(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                        uint32_t N, uint32_t K, hipStream_t s);
 
+// Several decode GEMVs over the same activations A (same format, dtype, M
+// and K; each with its own weights, output and N) in one launch, each job
+// computed exactly as launch_gemv would.  hipErrorNotSupported when the
+// jobs do not suit one launch (the caller then launches them one by one).
+constexpr int kGemvGroupMax = 4;
+struct GemvJob {
+  const void* W;
+  void* C;
+  uint32_t N;
+};
+hipError_t launch_gemv_group(QFmt q, EType t, const void* A, const GemvJob* jobs, uint32_t n, uint32_t M,
+                             uint32_t K, hipStream_t s);
+
 // Small-batch (M <= 64) MFMA kernel; skinny_fits() says whether a shape and
 // operand alignment suit it.
 bool skinny_fits(uint32_t M, uint32_t N, uint32_t K, const void* A, const void* W);

@@ -96,6 +96,7 @@ struct Provider {
   hipDeviceProp_t props{};
   uint64_t issued_seq = 0;            // guarded by mu
   std::atomic<uint64_t> done_seq{0};  // all dispatches <= done_seq finished
+  std::atomic<uint64_t> launch_groups{0};  // launches enqueued (a merged group counts once)
   Tuning tuning;
   Workspace ws;  // split-K partials and tile counters
   // timing ring
@@ -456,27 +457,36 @@ void ensure_ring(Provider* p) {
   p->ring_ready = true;
 }
 
-nf_status hip_dispatch(nf_provider self, const char* op_name, const nf_buffer* inputs,
-                       uint32_t n_in, nf_buffer* outputs, uint32_t n_out) {
-  Provider* p = as_prov(self);
+// A validated dispatch: its plan and buffers.
+struct Prepared {
+  const char* op = nullptr;
+  Plan pl;
+  Buffer* in[NF_MAX_TASK_INPUTS] = {};
+  Buffer* out[NF_MAX_TASK_OUTPUTS] = {};
+  uint32_t n_in = 0, n_out = 0;
+};
+
+nf_status prepare(Provider* p, const char* op_name, const nf_buffer* inputs, uint32_t n_in, nf_buffer* outputs,
+                  uint32_t n_out, Prepared* pr) {
   if (!p || !op_name) return set_error(NF_ERROR_INVALID_ARG, "dispatch: null provider or op name");
   if (!op_known(op_name))
     return set_error(NF_ERROR_UNSUPPORTED_OP, std::string("dispatch: unsupported op '") + op_name + "'");
   if (n_in > NF_MAX_TASK_INPUTS || n_out > NF_MAX_TASK_OUTPUTS || (n_in && !inputs) || (n_out && !outputs))
     return set_error(NF_ERROR_INVALID_ARG, "dispatch: bad input/output arrays");
-  Buffer* in[NF_MAX_TASK_INPUTS] = {};
-  Buffer* out[NF_MAX_TASK_OUTPUTS] = {};
   const nf_tensor_desc* in_d[NF_MAX_TASK_INPUTS] = {};
   const nf_tensor_desc* out_d[NF_MAX_TASK_OUTPUTS] = {};
+  pr->op = op_name;
+  pr->n_in = n_in;
+  pr->n_out = n_out;
   for (uint32_t i = 0; i < n_in; ++i) {
-    in[i] = as_buf(inputs[i]);
-    if (!in[i]) return set_error(NF_ERROR_INVALID_ARG, "dispatch: null input buffer");
-    in_d[i] = &in[i]->desc;
+    pr->in[i] = as_buf(inputs[i]);
+    if (!pr->in[i]) return set_error(NF_ERROR_INVALID_ARG, "dispatch: null input buffer");
+    in_d[i] = &pr->in[i]->desc;
   }
   for (uint32_t i = 0; i < n_out; ++i) {
-    out[i] = as_buf(outputs[i]);
-    if (!out[i]) return set_error(NF_ERROR_INVALID_ARG, "dispatch: null output buffer");
-    out_d[i] = &out[i]->desc;
+    pr->out[i] = as_buf(outputs[i]);
+    if (!pr->out[i]) return set_error(NF_ERROR_INVALID_ARG, "dispatch: null output buffer");
+    out_d[i] = &pr->out[i]->desc;
   }
   const uint8_t* pc = nullptr;
   uint32_t pc_size = 0;
@@ -485,39 +495,69 @@ nf_status hip_dispatch(nf_provider self, const char* op_name, const nf_buffer* i
     pc_size = td->push_constants_size;
     pc = td->push_constants;
   }
-  Plan pl;
   std::string why;
-  nf_status st = make_plan(op_name, in_d, n_in, out_d, n_out, pc, pc_size, p->tuning, &pl, &why);
+  nf_status st = make_plan(op_name, in_d, n_in, out_d, n_out, pc, pc_size, p->tuning, &pr->pl, &why);
   if (st != NF_OK) return set_error(st, std::string("dispatch ") + op_name + ": " + why);
+  return NF_OK;
+}
 
-  hipError_t e;
-  uint64_t seq;
+// Enqueue prepared dispatches in order.  n > 1 only for a group that
+// groupable() accepted: one grouped GEMV launch (or, if the kernel declines
+// the group, one launch each).
+nf_status launch(Provider* p, const Prepared* prs, uint32_t n) {
+  hipError_t e = hipSuccess;
   {
     std::lock_guard<std::mutex> lk(p->mu);
     if (!p->initialized) return set_error(NF_ERROR_INVALID_ARG, "dispatch: provider not initialised");
-    seq = ++p->issued_seq;
     TimingRec* rec = nullptr;
-    if (p->timing.load(std::memory_order_relaxed)) {
+    if (n == 1 && p->timing.load(std::memory_order_relaxed)) {
       ensure_ring(p);
       rec = &p->ring[p->timing_head.fetch_add(1, std::memory_order_relaxed) % kTimingRing];
-      std::strncpy(rec->op, op_name, 63);
+      std::strncpy(rec->op, prs[0].op, 63);
       rec->op[63] = '\0';
-      rec->dtype = (uint8_t)out_d[0]->dtype;
-      rec->elems = (uint32_t)(pl.path == Path::Dequant ? pl.count : (uint64_t)pl.M * pl.N);
+      rec->dtype = (uint8_t)prs[0].out[0]->desc.dtype;
+      rec->elems = (uint32_t)(prs[0].pl.path == Path::Dequant ? prs[0].pl.count : (uint64_t)prs[0].pl.M * prs[0].pl.N);
       (void)hipEventRecord(rec->start, p->stream);
     }
-    e = run_plan(pl, in, out, p->tuning.gemm_tile, p->ws, p->stream);
+    p->launch_groups.fetch_add(1, std::memory_order_relaxed);
+    if (n == 1) {
+      e = run_plan(prs[0].pl, prs[0].in, prs[0].out, p->tuning.gemm_tile, p->ws, p->stream);
+    } else {
+      GemvJob jobs[kGemvGroupMax];
+      for (uint32_t j = 0; j < n; ++j) jobs[j] = GemvJob{prs[j].in[1]->dev, prs[j].out[0]->dev, prs[j].pl.N};
+      const Plan& pl = prs[0].pl;
+      e = launch_gemv_group(pl.q, pl.c, prs[0].in[0]->dev, jobs, n, pl.M, pl.K, p->stream);
+      if (e == hipErrorNotSupported) {
+        p->launch_groups.fetch_add(n - 1, std::memory_order_relaxed);
+        e = hipSuccess;
+        for (uint32_t j = 0; j < n && e == hipSuccess; ++j)
+          e = run_plan(prs[j].pl, prs[j].in, prs[j].out, p->tuning.gemm_tile, p->ws, p->stream);
+      }
+    }
     if (rec) (void)hipEventRecord(rec->stop, p->stream);
-    for (uint32_t i = 0; i < n_out; ++i) out[i]->last_write_seq.store(seq);
+    for (uint32_t j = 0; j < n; ++j) {
+      const uint64_t seq = ++p->issued_seq;
+      for (uint32_t i = 0; i < prs[j].n_out; ++i) prs[j].out[i]->last_write_seq.store(seq);
+    }
   }
   // Buffer flags are updated outside the provider lock (map takes the
   // buffer lock first, then the provider lock).
-  for (uint32_t i = 0; i < n_out; ++i) {
-    std::lock_guard<std::mutex> bl(out[i]->mu);
-    out[i]->host_valid = false;
-  }
-  if (e != hipSuccess) return map_hip(e, (std::string("launch ") + pl.kernel).c_str());
+  for (uint32_t j = 0; j < n; ++j)
+    for (uint32_t i = 0; i < prs[j].n_out; ++i) {
+      std::lock_guard<std::mutex> bl(prs[j].out[i]->mu);
+      prs[j].out[i]->host_valid = false;
+    }
+  if (e != hipSuccess) return map_hip(e, (std::string("launch ") + prs[0].pl.kernel).c_str());
   return NF_OK;
+}
+
+nf_status hip_dispatch(nf_provider self, const char* op_name, const nf_buffer* inputs,
+                       uint32_t n_in, nf_buffer* outputs, uint32_t n_out) {
+  Provider* p = as_prov(self);
+  Prepared pr;
+  nf_status st = prepare(p, op_name, inputs, n_in, outputs, n_out, &pr);
+  if (st != NF_OK) return st;
+  return launch(p, &pr, 1);
 }
 
 nf_status hip_synchronize(nf_provider self) {
@@ -760,18 +800,62 @@ NF_API void nf_hip_get_gemv_max_m(uint32_t* f32_path, uint32_t* f16_path) {
   if (f16_path) *f16_path = g_prov.tuning.gemv_max_m_f16;
 }
 
+bool overlaps(const Buffer* a, const Buffer* b) {
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a->dev), b0 = reinterpret_cast<uintptr_t>(b->dev);
+  return a0 < b0 + b->alloc_bytes && b0 < a0 + a->alloc_bytes;
+}
+
+// May `next` join the GEMV group g[0..n)?  Same kernel family, same
+// activation buffer, M and K, and no hazard between the members: no output
+// overlaps another member's activations, weights or output, so running them
+// in one launch is the same as running them in order.
+bool groupable(const Prepared* g, uint32_t n, const Prepared& next) {
+  if (n >= (uint32_t)kGemvGroupMax) return false;
+  const Plan& a = g[0].pl;
+  const Plan& b = next.pl;
+  if (a.path != Path::Gemv || b.path != Path::Gemv || a.op != b.op || a.q != b.q || a.a != b.a || a.c != b.c ||
+      a.M != b.M || a.K != b.K || next.n_in < 2 || next.n_out < 1 || next.in[0] != g[0].in[0])
+    return false;
+  for (uint32_t j = 0; j < n; ++j) {
+    if (overlaps(next.out[0], g[j].in[0]) || overlaps(next.out[0], g[j].in[1]) || overlaps(next.out[0], g[j].out[0]) ||
+        overlaps(g[j].out[0], next.in[1]))
+      return false;
+  }
+  return !overlaps(next.out[0], next.in[0]) && !overlaps(next.out[0], next.in[1]);
+}
+
 NF_API nf_status nf_hip_run_tasks(nf_provider self, const nf_task_desc* tasks, uint32_t n_tasks,
                                   uint32_t repeat) {
-  if (!self || (n_tasks && !tasks)) return NF_ERROR_INVALID_ARG;
+  Provider* p = as_prov(self);
+  if (!p || (n_tasks && !tasks)) return NF_ERROR_INVALID_ARG;
+  const bool group = !p->timing.load(std::memory_order_relaxed);
+  Prepared prs[kGemvGroupMax + 1];
   for (uint32_t r = 0; r < repeat; ++r) {
-    for (uint32_t i = 0; i < n_tasks; ++i) {
+    uint32_t i = 0;
+    while (i < n_tasks) {
       const nf_task_desc& t = tasks[i];
-      nf_status st = hip_dispatch(self, t.op_name, t.inputs, t.n_inputs,
-                                  const_cast<nf_buffer*>(t.outputs), t.n_outputs);
+      nf_status st = prepare(p, t.op_name, t.inputs, t.n_inputs, const_cast<nf_buffer*>(t.outputs), t.n_outputs, &prs[0]);
       if (st != NF_OK) return st;
+      uint32_t n = 1;
+      while (group && prs[0].pl.path == Path::Gemv && i + n < n_tasks && n < (uint32_t)kGemvGroupMax) {
+        const nf_task_desc& u = tasks[i + n];
+        if (prepare(p, u.op_name, u.inputs, u.n_inputs, const_cast<nf_buffer*>(u.outputs), u.n_outputs, &prs[n]) !=
+                NF_OK ||
+            !groupable(prs, n, prs[n]))
+          break;
+        ++n;
+      }
+      st = launch(p, prs, n);
+      if (st != NF_OK) return st;
+      i += n;
     }
   }
   return NF_OK;
+}
+
+NF_API uint64_t nf_hip_launch_count(nf_provider self) {
+  Provider* p = as_prov(self);
+  return p ? p->launch_groups.load(std::memory_order_relaxed) : 0;
 }
 
 NF_API nf_status nf_hip_get_stream(nf_provider self, void** stream) {

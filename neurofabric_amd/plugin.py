@@ -65,6 +65,8 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     lib.nf_hip_get_gemv_max_m.restype = None
     lib.nf_hip_set_skinny_max_m.argtypes = [C.c_uint32]
     lib.nf_hip_set_skinny_max_m.restype = None
+    lib.nf_hip_launch_count.argtypes = [C.c_void_p]
+    lib.nf_hip_launch_count.restype = C.c_uint64
     lib.nf_hip_set_gemm_tile.argtypes = [C.c_int32]
     lib.nf_hip_set_gemm_tile.restype = None
     lib.nf_hip_get_gemm_tile.argtypes = []
@@ -309,6 +311,10 @@ class Provider:
 
     def set_skinny_max_m(self, f16: int) -> None:
         self.lib.nf_hip_set_skinny_max_m(f16)
+
+    def launch_count(self) -> int:
+        """Launches enqueued so far (a merged GEMV group counts once)."""
+        return int(self.lib.nf_hip_launch_count(self.handle))
 
     def set_gemm_tile(self, tile: int) -> None:
         """-1: register-dequantizing GEMM kernel (default); 0..6: LDS-staged tile shapes."""

@@ -1,0 +1,103 @@
+"""nf_hip_run_tasks merges adjacent decode GEMVs that read the same
+activation buffer (q/k/v, gate/up) into one launch.  Each merged result must
+be bit-identical to dispatching the tasks one by one, the launch count must
+show the merge, and a hazard between two tasks (here: both write the same
+output) must keep them in separate launches."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from helpers import assert_close
+from neurofabric_amd import abi
+from neurofabric_amd import synthetic as syn
+from neurofabric_amd.abi import nf_task_desc
+
+pytestmark = pytest.mark.gpu
+
+QDT = {"q4_0": abi.NF_DTYPE_Q4_0, "q8_0": abi.NF_DTYPE_Q8_0}
+
+
+def _array(tasks):
+    arr = (nf_task_desc * len(tasks))()
+    for i, td in enumerate(tasks):
+        C.memmove(C.addressof(arr[i]), C.addressof(td), C.sizeof(nf_task_desc))
+        arr[i].user_data = C.addressof(arr[i])
+    return arr
+
+
+def _block(provider, fmt, f16, M, hidden, kv, ffn, seed):
+    """One Llama block's projections with the model's dataflow."""
+    adt = abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32
+    npdt = np.float16 if f16 else np.float32
+    elt = 2 if f16 else 4
+    acts = {r: provider.alloc_array(syn.activations(M, k, seed=seed + i, dtype=npdt), adt)
+            for i, (r, k) in enumerate((("attn_norm", hidden), ("attn_out", hidden), ("ffn_norm", hidden),
+                                       ("ffn_act", ffn)))}
+    projs = [("q", "attn_norm", hidden, hidden), ("k", "attn_norm", kv, hidden), ("v", "attn_norm", kv, hidden),
+             ("o", "attn_out", hidden, hidden), ("gate", "ffn_norm", ffn, hidden), ("up", "ffn_norm", ffn, hidden),
+             ("down", "ffn_act", hidden, ffn)]
+    host_w, bufs, outs, specs = {}, [], {}, []
+    op = f"dequant_{fmt}_linear" + ("_f16" if f16 else "")
+    for j, (name, role, N, K) in enumerate(projs):
+        host_w[name] = syn.weights(fmt, N, K, seed=seed + 10 + j)
+        w = provider.alloc_array(host_w[name], QDT[fmt])
+        outs[name] = provider.alloc(adt, M * N * elt)
+        bufs.append(w)
+        specs.append((name, role, w, N, K))
+    tasks = [provider.task(op, [acts[role], w], [outs[name]], M, N, K) for (name, role, w, N, K) in specs]
+    return op, acts, outs, specs, tasks, bufs + list(acts.values()) + list(outs.values()), host_w
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("M", [1, 3])
+def test_run_tasks_merges_same_input_gemvs(provider, oracle_mod, fmt, f16, M):
+    hidden, kv, ffn = 1024, 128, 2816
+    op, acts, outs, specs, tasks, bufs, host_w = _block(provider, fmt, f16, M, hidden, kv, ffn, seed=M * 7)
+    npdt = np.float16 if f16 else np.float32
+    try:
+        arr = _array(tasks)
+        before = provider.launch_count()
+        provider.run_tasks(arr, 1)
+        provider.synchronize()
+        assert provider.launch_count() - before == 4  # q+k+v, o, gate+up, down
+        grouped = {name: outs[name].download(npdt).copy() for (name, *_r) in specs}
+        # the same tasks one dispatch each
+        for (name, role, w, N, K) in specs:
+            provider.dispatch(op, [acts[role], w], [outs[name]], M, N, K)
+        provider.synchronize()
+        for (name, *_r) in specs:
+            single = outs[name].download(npdt)
+            assert np.array_equal(grouped[name].view(np.uint8), single.view(np.uint8)), name
+        # and one merged member against the oracle
+        A = acts["attn_norm"].download(npdt).reshape(M, hidden)
+        ref = oracle_mod.fused(A, host_w["k"], fmt, M, kv, hidden, f16=f16, threads=8)
+        if f16:
+            ref = ref.view(np.float16)
+        assert_close(grouped["k"].reshape(M, kv).astype(np.float32), ref.astype(np.float32), what=f"{fmt} k")
+    finally:
+        for b in bufs:
+            b.release()
+
+
+def test_run_tasks_keeps_hazards_apart(provider, oracle_mod):
+    """Two GEMVs over the same activations that write the same output are
+    not merged; the output is the second one's, as in dispatch order."""
+    M, N, K = 1, 300, 512
+    A = syn.activations(M, K, seed=1)
+    W1, W2 = syn.q4_0_weights(N, K, seed=2), syn.q4_0_weights(N, K, seed=3)
+    a = provider.alloc_array(A, abi.NF_DTYPE_F32)
+    w1 = provider.alloc_array(W1, abi.NF_DTYPE_Q4_0)
+    w2 = provider.alloc_array(W2, abi.NF_DTYPE_Q4_0)
+    c = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    try:
+        arr = _array([provider.task("dequant_q4_0_linear", [a, w], [c], M, N, K) for w in (w1, w2)])
+        before = provider.launch_count()
+        provider.run_tasks(arr, 1)
+        provider.synchronize()
+        assert provider.launch_count() - before == 2
+        assert_close(c.download(np.float32).reshape(M, N), oracle_mod.fused(A, W2, "q4_0", M, N, K))
+    finally:
+        for b in (a, w1, w2, c):
+            b.release()
