@@ -29,13 +29,14 @@ enum class Path {
 // while M <= gemv_max_m (and its activation stage fits in LDS), the
 // small-batch MFMA kernel while M <= skinny_max_m (the f32 path stays there
 // for every larger M, 32 rows per launch), the tiled MFMA GEMM above (f16).
-// Defaults from the measured sweep on MI355X: the GEMV wins or ties up to
-// M = 4, the small-batch kernel from M = 8, and for f16 it still beats the
-// tiled GEMM at M = 64.
+// Defaults from the measured sweep on MI355X (28672x8192 Q4_0): the GEMV
+// wins or ties up to M = 4, the small-batch kernel from M = 8; for f16 it
+// still beats the tiled GEMM at M = 32 (91 vs 95 us) and loses at M = 64
+// (177 vs 96 us).
 struct Tuning {
   uint32_t gemv_max_m_f32 = 4;
   uint32_t gemv_max_m_f16 = 4;
-  uint32_t skinny_max_m_f16 = 64;
+  uint32_t skinny_max_m_f16 = 32;
   // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernel
   // (default, measured fastest), 0..6 = one of the LDS-staged tile shapes.
   int32_t gemm_tile = -1;
