@@ -36,6 +36,7 @@ HIP_SOURCES = [
     CSRC / "kernels" / "gemm.hip",
     CSRC / "kernels" / "skinny.hip",
     CSRC / "kernels" / "generic.hip",
+    CSRC / "kernels" / "dense.hip",
 ]
 CXX_SOURCES = [CSRC / "plan.cpp"]
 

@@ -335,10 +335,10 @@ __device__ __forceinline__ void xcd_tile(int bid, int mt, int nt, int& tm, int& 
 //   * W of step s+1 (fetched one step earlier) is dequantized to fp16 and
 //     written into the other stage;
 //   * one barrier.
-template <class QF, int BM, int BN, int WGM, int WGN, int NS, bool SPLIT>
+template <class QF, int BM, int BN, int WGM, int WGN, int NS, bool SPLIT, typename CT = half_t>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half_t* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
-                                                                    half_t* __restrict__ C, int M,
+                                                                    CT* __restrict__ C, int M,
                                                                     int N, int K,
                                                                     float* __restrict__ ws_part,
                                                                     uint32_t* __restrict__ ws_cnt) {
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int gm = m0 + wm + 32 * i + (r >> 2) * 8 + rq + (r & 3);
-          if (gm < M) C[(size_t)gm * N + gn] = (half_t)acc[i][j][r];
+          if (gm < M) C[(size_t)gm * N + gn] = (CT)acc[i][j][r];
         }
       }
   };
@@ -1063,8 +1063,8 @@ inline int pick_tile(uint32_t M, uint32_t N, int forced) {
   return s1 > s2 ? 1 : 2;
 }
 
-template <class QF, int BM, int BN, int WGM, int WGN, int NS = 2>
-hipError_t gemm_tile_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_t M, uint32_t N,
+template <class QF, int BM, int BN, int WGM, int WGN, int NS = 2, typename CT = half_t>
+hipError_t gemm_tile_launch(const half_t* a, const uint8_t* w, CT* c, uint32_t M, uint32_t N,
                             uint32_t K, const nfhip::Workspace& ws, hipStream_t s) {
   const long tiles = (long)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
   if (tiles > (1L << 31) - 1) return hipErrorInvalidConfiguration;
@@ -1086,18 +1086,18 @@ hipError_t gemm_tile_launch(const half_t* a, const uint8_t* w, half_t* c, uint32
   // More than 64 KB of dynamic LDS must be allowed explicitly, once per kernel.
   if (kg == 1) {
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, false>),
+        reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, false, CT>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, false><<<dim3((unsigned)tiles), dim3(64 * WGM * WGN), lds, s>>>(
+    gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, false, CT><<<dim3((unsigned)tiles), dim3(64 * WGM * WGN), lds, s>>>(
         a, w, c, M, N, K, ws.part, ws.cnt);
   } else {
     if constexpr (std::is_same<QF, F16B>::value) return hipErrorInvalidValue;  // dense path never splits
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, true>),
+        reinterpret_cast<const void*>(&gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, true, CT>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, true><<<dim3((unsigned)tiles, (unsigned)kg), dim3(64 * WGM * WGN), lds, s>>>(
+    gemm_tile_kernel<QF, BM, BN, WGM, WGN, NS, true, CT><<<dim3((unsigned)tiles, (unsigned)kg), dim3(64 * WGM * WGN), lds, s>>>(
         a, w, c, M, N, K, ws.part, ws.cnt);
   }
   return hipGetLastError();
@@ -1151,22 +1151,29 @@ hipError_t gemm_wq_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_t
 
 namespace nfhip {
 
-// Dense fp16 x fp16 -> fp16 linear on the tiled MFMA kernel (B stored [N,K]).
+// Dense fp16 x fp16 linear on the tiled MFMA kernel (B stored [N,K]), fp16
+// or fp32 output.
+template <typename CT>
+hipError_t dense_mfma_f16(const nfk::half_t* a, const uint8_t* b, CT* c, uint32_t M, uint32_t N, uint32_t K,
+                          hipStream_t s) {
+  switch (nfk::pick_tile(M, N, nfk::forced_tile())) {
+    case 0: return nfk::gemm_tile_launch<nfk::F16B, 256, 256, 2, 4, 2, CT>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 1: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 4, 2, 2, CT>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 3: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2, 2, CT>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 4: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2, 3, CT>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 5: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2, 3, CT>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    case 6: return nfk::gemm_tile_launch<nfk::F16B, 128, 256, 2, 4, 2, CT>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+    default: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2, 2, CT>(a, b, c, M, N, K, nfhip::Workspace{}, s);
+  }
+}
+
 hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t M, uint32_t N, uint32_t K,
-                                 hipStream_t s) {
+                                 bool out_f32, hipStream_t s) {
   const nfk::half_t* a = static_cast<const nfk::half_t*>(A);
   const uint8_t* b = static_cast<const uint8_t*>(B);
-  nfk::half_t* c = static_cast<nfk::half_t*>(C);
   if (K % 64 != 0 || (uintptr_t)A % 16 != 0 || (uintptr_t)B % 16 != 0) return hipErrorInvalidValue;
-  switch (nfk::pick_tile(M, N, nfk::forced_tile())) {
-    case 0: return nfk::gemm_tile_launch<nfk::F16B, 256, 256, 2, 4>(a, b, c, M, N, K, nfhip::Workspace{}, s);
-    case 1: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 4, 2>(a, b, c, M, N, K, nfhip::Workspace{}, s);
-    case 3: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2>(a, b, c, M, N, K, nfhip::Workspace{}, s);
-    case 4: return nfk::gemm_tile_launch<nfk::F16B, 256, 128, 2, 2, 3>(a, b, c, M, N, K, nfhip::Workspace{}, s);
-    case 5: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2, 3>(a, b, c, M, N, K, nfhip::Workspace{}, s);
-    case 6: return nfk::gemm_tile_launch<nfk::F16B, 128, 256, 2, 4>(a, b, c, M, N, K, nfhip::Workspace{}, s);
-    default: return nfk::gemm_tile_launch<nfk::F16B, 128, 128, 2, 2>(a, b, c, M, N, K, nfhip::Workspace{}, s);
-  }
+  return out_f32 ? dense_mfma_f16<float>(a, b, static_cast<float*>(C), M, N, K, s)
+                 : dense_mfma_f16<nfk::half_t>(a, b, static_cast<nfk::half_t*>(C), M, N, K, s);
 }
 
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,

@@ -253,10 +253,18 @@ hipError_t launch_dense(EType a, EType b, EType c, const void* A, const void* B,
     return b == EType::F32 ? nfk::dense_gemv_c<nfk::half_t, float>(c, A, B, C, M, N, K, s)
                            : nfk::dense_gemv_c<nfk::half_t, nfk::half_t>(c, A, B, C, M, N, K, s);
   }
-  // fp16 x fp16 -> fp16 with enough rows for MFMA tiles: the tiled MFMA kernel.
-  if (a == EType::F16 && b == EType::F16 && c == EType::F16 && M >= 32 && K % 64 == 0 &&
-      (uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0)
-    return launch_dense_mfma_f16(A, B, C, M, N, K, s);
+  // fp16 x fp16 with enough rows for MFMA tiles: the tiled fp16 MFMA kernel
+  // (fp32 accumulation; fp16 or fp32 output).
+  if (a == EType::F16 && b == EType::F16 && M >= 32 && K % 64 == 0 && (uintptr_t)A % 16 == 0 &&
+      (uintptr_t)B % 16 == 0)
+    return launch_dense_mfma_f16(A, B, C, M, N, K, c == EType::F32, s);
+  // Every other dtype mix (fp32 operands, or an fp32 output) on the fp32
+  // MFMA, fp16 operands widened exactly; the VALU tile kernel below takes
+  // K % 32 != 0 and misaligned buffers.
+  {
+    const hipError_t e = launch_dense_mfma_f32(a, b, c, A, B, C, M, N, K, s);
+    if (e != hipErrorNotSupported) return e;
+  }
   if (a == EType::F32) {
     return b == EType::F32 ? nfk::dense_c<float, float>(c, A, B, C, M, N, K, s)
                            : nfk::dense_c<float, nfk::half_t>(c, A, B, C, M, N, K, s);

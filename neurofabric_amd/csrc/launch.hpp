@@ -58,10 +58,17 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
 hipError_t launch_generic(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                           uint32_t N, uint32_t K, hipStream_t s);
 
-// Dense fp16 linear on the tiled MFMA kernel; hipErrorInvalidValue when the
-// shape/alignment does not fit it (K % 64, 16-B aligned operands).
+// Dense fp16 x fp16 linear on the tiled MFMA kernel, fp16 or fp32 output;
+// hipErrorInvalidValue when the shape/alignment does not fit it (K % 64,
+// 16-B aligned operands).
 hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t M, uint32_t N, uint32_t K,
-                                 hipStream_t s);
+                                 bool out_f32, hipStream_t s);
+
+// Dense linear with at least one fp32 operand (fp16 operands widened
+// exactly) on the fp32 MFMA; hipErrorNotSupported when K % 32 != 0 or an
+// operand is not 16-B aligned.
+hipError_t launch_dense_mfma_f32(EType a, EType b, EType c, const void* A, const void* B, void* C, uint32_t M,
+                                 uint32_t N, uint32_t K, hipStream_t s);
 
 hipError_t launch_dense(EType a, EType b, EType c, const void* A, const void* B, void* C,
                         uint32_t M, uint32_t N, uint32_t K, hipStream_t s);

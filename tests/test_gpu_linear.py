@@ -360,6 +360,32 @@ def test_dense_linear_dtype_mixes(provider, oracle_mod, adt, bdt, cdt):
         x.release()
 
 
+@pytest.mark.parametrize("adt,bdt,cdt", [("f32", "f32", "f32"), ("f32", "f16", "f32"), ("f16", "f32", "f16"),
+                                         ("f16", "f16", "f32")])
+@pytest.mark.parametrize("shape", [(300, 1000, 1024), (129, 257, 96), (1024, 256, 640), (9, 130, 32), (40, 50, 100)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_dense_linear_f32_mfma(provider, oracle_mod, adt, bdt, cdt, shape):
+    """`linear` with an fp32 operand or output above decode batch sizes: the
+    fp32 MFMA kernel (fp16 operands widened exactly), ragged M/N, a single K
+    step; K % 32 != 0 (the last shape) falls back to the VALU tile kernel."""
+    M, N, K = shape
+    rng = np.random.default_rng(M + N + K)
+    np_t = {"f16": np.float16, "f32": np.float32}
+    nf_t = {"f16": abi.NF_DTYPE_F16, "f32": abi.NF_DTYPE_F32}
+    A = rng.standard_normal((M, K)).astype(np_t[adt])
+    B = rng.standard_normal((N, K)).astype(np_t[bdt])
+    a, b = provider.alloc_array(A, nf_t[adt]), provider.alloc_array(B, nf_t[bdt])
+    c = provider.alloc(nf_t[cdt], M * N * (2 if cdt == "f16" else 4))
+    provider.dispatch("linear", [a, b], [c], M, N, K)
+    got = c.download(np_t[cdt]).reshape(M, N).astype(np.float32)
+    ref = oracle_mod.linear_f32(A.astype(np.float32), B.astype(np.float32), M, N, K)
+    if cdt == "f16":
+        ref = ref.astype(np.float16).astype(np.float32)
+    assert_close(got, ref, what=f"{adt}{bdt}->{cdt} {M}x{N}x{K}")
+    for x in (a, b, c):
+        x.release()
+
+
 @pytest.mark.parametrize("adt,bdt,cdt,M,N,K", [
     ("f32", "f32", "f32", 1, 1000, 4096), ("f32", "f32", "f32", 2, 64, 100), ("f16", "f16", "f16", 3, 333, 2048),
     ("f32", "f16", "f32", 8, 130, 1024), ("f16", "f16", "f32", 4, 257, 512), ("f16", "f32", "f16", 5, 96, 256),
