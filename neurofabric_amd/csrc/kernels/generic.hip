@@ -243,7 +243,7 @@ hipError_t launch_generic(QFmt q, EType t, const void* A, const void* W, void* C
 }
 
 hipError_t launch_dense(EType a, EType b, EType c, const void* A, const void* B, void* C,
-                        uint32_t M, uint32_t N, uint32_t K, hipStream_t s) {
+                        uint32_t M, uint32_t N, uint32_t K, const Workspace& ws, hipStream_t s) {
   // Decode-sized batches: the HBM-bound dense GEMV (16-byte aligned rows).
   const size_t ea = a == EType::F16 ? 2 : 4, eb = b == EType::F16 ? 2 : 4;
   if (M <= 8 && (uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0 && (K * ea) % 16 == 0 && (K * eb) % 16 == 0) {
@@ -262,7 +262,7 @@ hipError_t launch_dense(EType a, EType b, EType c, const void* A, const void* B,
   // MFMA, fp16 operands widened exactly; the VALU tile kernel below takes
   // K % 32 != 0 and misaligned buffers.
   {
-    const hipError_t e = launch_dense_mfma_f32(a, b, c, A, B, C, M, N, K, s);
+    const hipError_t e = launch_dense_mfma_f32(a, b, c, A, B, C, M, N, K, ws, s);
     if (e != hipErrorNotSupported) return e;
   }
   if (a == EType::F32) {

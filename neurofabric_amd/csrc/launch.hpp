@@ -68,9 +68,9 @@ hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t
 // exactly) on the fp32 MFMA; hipErrorNotSupported when K % 32 != 0 or an
 // operand is not 16-B aligned.
 hipError_t launch_dense_mfma_f32(EType a, EType b, EType c, const void* A, const void* B, void* C, uint32_t M,
-                                 uint32_t N, uint32_t K, hipStream_t s);
+                                 uint32_t N, uint32_t K, const Workspace& ws, hipStream_t s);
 
 hipError_t launch_dense(EType a, EType b, EType c, const void* A, const void* B, void* C,
-                        uint32_t M, uint32_t N, uint32_t K, hipStream_t s);
+                        uint32_t M, uint32_t N, uint32_t K, const Workspace& ws, hipStream_t s);
 
 }  // namespace nfhip

@@ -443,7 +443,7 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, int g
     case Path::Generic:
       return launch_generic(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
     case Path::Dense:
-      return launch_dense(pl.a, pl.b, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
+      return launch_dense(pl.a, pl.b, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, ws, s);
   }
   return hipErrorInvalidValue;
 }

@@ -386,6 +386,34 @@ def test_dense_linear_f32_mfma(provider, oracle_mod, adt, bdt, cdt, shape):
         x.release()
 
 
+@pytest.mark.parametrize("adt,bdt", [("f32", "f32"), ("f16", "f32")])
+@pytest.mark.parametrize("shape", [(16, 4096, 4096), (64, 1000, 2048), (33, 300, 8192)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_dense_linear_f32_split_k(provider, oracle_mod, adt, bdt, shape):
+    """fp32 dense linear at small batches: 32-row tiles with K split over
+    workgroups (partial tiles added by the last arrival).  Two calls in a row
+    with different activations: the per-tile counters must be back at zero."""
+    M, N, K = shape
+    rng = np.random.default_rng(M * 3 + N)
+    np_t = {"f16": np.float16, "f32": np.float32}
+    nf_t = {"f16": abi.NF_DTYPE_F16, "f32": abi.NF_DTYPE_F32}
+    B = rng.standard_normal((N, K)).astype(np_t[bdt])
+    b = provider.alloc_array(B, nf_t[bdt])
+    c = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    try:
+        for rep in range(2):
+            A = rng.standard_normal((M, K)).astype(np_t[adt])
+            a = provider.alloc_array(A, nf_t[adt])
+            provider.dispatch("linear", [a, b], [c], M, N, K)
+            got = c.download(np.float32).reshape(M, N)
+            a.release()
+            ref = oracle_mod.linear_f32(A.astype(np.float32), B.astype(np.float32), M, N, K)
+            assert_close(got, ref, what=f"{adt}{bdt} {M}x{N}x{K} call {rep}")
+    finally:
+        b.release()
+        c.release()
+
+
 @pytest.mark.parametrize("adt,bdt,cdt,M,N,K", [
     ("f32", "f32", "f32", 1, 1000, 4096), ("f32", "f32", "f32", 2, 64, 100), ("f16", "f16", "f16", 3, 333, 2048),
     ("f32", "f16", "f32", 8, 130, 1024), ("f16", "f16", "f32", 4, 257, 512), ("f16", "f32", "f16", 5, 96, 256),
