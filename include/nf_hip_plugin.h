@@ -128,12 +128,12 @@ NF_API int32_t nf_hip_get_gemm_tile(void);
  * plan (PipelineEngine.hpp:518-561) but without a thread hop per node.  Each
  * element goes through the same validation as vtable.dispatch, on the same
  * stream; returns the first non-NF_OK status.  Because the whole batch is
- * known, adjacent decode GEMVs that read the same activation buffer (same
- * fused op, M and K; no output overlapping another member's inputs or
- * output) are launched as one grouped kernel, up to four at a time: the
- * results are bit-identical to dispatching them one by one, in order.  Not
- * done while per-dispatch timing is enabled.  vtable.dispatch itself never
- * defers or merges anything. */
+ * known, adjacent decode GEMVs and small-batch (M <= 32) linears that read
+ * the same activation buffer (same fused op, M and K; no output overlapping
+ * another member's inputs or output) are launched as one grouped kernel, up
+ * to four at a time: the results are bit-identical to dispatching them one
+ * by one, in order.  Not done while per-dispatch timing is enabled.
+ * vtable.dispatch itself never defers or merges anything. */
 NF_API nf_status nf_hip_run_tasks(nf_provider self, const nf_task_desc *tasks, uint32_t n_tasks,
                                   uint32_t repeat);
 

@@ -40,6 +40,8 @@
 // and the accumulators in registers; more rows take more launches.
 #include <type_traits>
 
+#include <cstdlib>
+
 #include "../launch.hpp"
 #include "common.hpp"
 
@@ -184,10 +186,40 @@ template <> struct Piece<16> { typedef u32x4 T; };
 template <> struct Piece<8> { typedef uint2 T; };
 template <> struct Piece<4> { typedef uint32_t T; };
 
+// Up to kGroupMax small-batch linears over the same activations in one
+// launch: job j owns row tiles (grid x) begin[j] .. begin[j+1]-1 and runs on
+// its own weights, output and N with the launch's shared K split, exactly as
+// a launch of its own with that split would.
+constexpr int kSkGroupMax = nfhip::kGemvGroupMax;
+struct SkinnyGroup {
+  const uint8_t* W[kSkGroupMax];
+  void* C[kSkGroupMax];
+  int N[kSkGroupMax];
+  int begin[kSkGroupMax + 1];
+  int count;
+};
+
 template <class QF, typename XT, int MT, int CHP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) void skinny_kernel(
-    const XT* __restrict__ A, const uint8_t* __restrict__ W, XT* __restrict__ C, int M, int N, int K,
-    float* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt) {
+    const XT* __restrict__ A, const SkinnyGroup grp, int M, int K, float* __restrict__ ws_part,
+    uint32_t* __restrict__ ws_cnt) {
+  // This workgroup's job (uniform; selects rather than an indexed load of
+  // the argument block).
+  int job = 0;
+#pragma unroll
+  for (int q = 1; q < kSkGroupMax; ++q) job = (q < grp.count && (int)blockIdx.x >= grp.begin[q]) ? q : job;
+  const uint8_t* __restrict__ W = grp.W[0];
+  void* Cv = grp.C[0];
+  int N = grp.N[0], tile0 = grp.begin[0];
+#pragma unroll
+  for (int q = 1; q < kSkGroupMax; ++q)
+    if (job == q) {
+      W = grp.W[q];
+      Cv = grp.C[q];
+      N = grp.N[q];
+      tile0 = grp.begin[q];
+    }
+  XT* __restrict__ C = static_cast<XT*>(Cv);
   constexpr bool kF32 = sizeof(XT) == 4;
   constexpr bool kQ4 = SkW<QF>::kLoads == 5;
   constexpr int WL = SkW<QF>::kLoads;
@@ -212,7 +244,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const int r16 = lane & 15, s = lane >> 4;
   const int P = K >> 6;
   const int NC = P / CHP;  // chunks along K
-  const int n0 = blockIdx.x * RW;
+  const int n0 = ((int)blockIdx.x - tile0) * RW;
   uint32_t* wst = smem + (size_t)wave * AREA;
 
   // K range of this wave (whole chunks): the KG = gridDim.y workgroups of a
@@ -455,30 +487,92 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   if (tid == 0) __hip_atomic_store(&ws_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <class QF, typename XT, int MT, int CHP>
-hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
-                         const nfhip::Workspace& ws, hipStream_t s) {
-  constexpr int RW = 64, PITCH = CHP * SkW<QF>::kPairBytes / 4, NV = MT * 4 * 4;
-  constexpr int AREA = RW * PITCH > NV * 64 ? RW * PITCH : NV * 64;  // dwords per wave
-  const long wgs = ((long)N + RW - 1) / RW;
+// Waves per workgroup (ks) and workgroups per row tile (kg) for a launch of
+// `wgs` row tiles: up to 8 waves per workgroup (the kernel's launch bound of
+// 512 threads); for launches with very few row tiles (under 512 waves), also
+// kg workgroups per row tile, while every wave keeps at least one chunk; kg
+// is bounded by the workspace.
+template <int MT, int CHP>
+void skinny_split(long wgs, uint32_t K, const nfhip::Workspace& ws, int& ks, int& kg) {
+  constexpr int NV = MT * 4 * 4;
   const int NC = (int)(K / (64 * CHP));
-  // K split: up to 8 waves per workgroup; for launches with very few row
-  // tiles (under 512 waves), also KG workgroups per row tile, while every
-  // wave keeps at least one chunk; KG is bounded by the workspace.
-  int ks = 1;
-  while (ks < 8 && wgs * ks < 2048 && NC >= 2 * ks) ks *= 2;
-  int kg = 1;
-  while (wgs * ks * kg < 512 && NC >= 2 * ks * kg && kg < 64 && wgs <= (long)ws.cnt_len &&
+  static const int ks_max = [] {
+    const char* e = std::getenv("NF_HIP_SKINNY_KS_MAX");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 && v <= 8 ? v : 8;
+  }();
+  static const int kg_max = [] {
+    const char* e = std::getenv("NF_HIP_SKINNY_KG_MAX");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 && v <= 64 ? v : 64;
+  }();
+  ks = 1;
+  while (ks < ks_max && wgs * ks < 2048 && NC >= 2 * ks) ks *= 2;
+  kg = 1;
+  while (wgs * ks * kg < 512 && NC >= 2 * ks * kg && kg < kg_max && wgs <= (long)ws.cnt_len &&
          (size_t)wgs * 2 * kg * NV * 64 <= ws.part_floats)
     kg *= 2;
+}
+
+template <class QF, typename XT, int MT, int CHP>
+hipError_t skinny_launch_group(const void* A, const SkinnyGroup& grp, long tiles, uint32_t M, uint32_t K, int ks,
+                               int kg, const nfhip::Workspace& ws, hipStream_t s) {
+  constexpr int RW = 64, PITCH = CHP * SkW<QF>::kPairBytes / 4, NV = MT * 4 * 4;
+  constexpr int AREA = RW * PITCH > NV * 64 ? RW * PITCH : NV * 64;  // dwords per wave
+  if (kg > 1 && (tiles > (long)ws.cnt_len || (size_t)tiles * kg * NV * 64 > ws.part_floats))
+    return hipErrorNotSupported;
   const size_t lds = (size_t)ks * AREA * 4;
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_kernel<QF, XT, MT, CHP>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
   if (attr != hipSuccess) return attr;
-  skinny_kernel<QF, XT, MT, CHP><<<dim3((unsigned)wgs, (unsigned)kg), dim3(64 * ks), lds, s>>>(
-      static_cast<const XT*>(A), static_cast<const uint8_t*>(W), static_cast<XT*>(C), (int)M, (int)N, (int)K,
-      ws.part, ws.cnt);
+  skinny_kernel<QF, XT, MT, CHP><<<dim3((unsigned)tiles, (unsigned)kg), dim3(64 * ks), lds, s>>>(
+      static_cast<const XT*>(A), grp, (int)M, (int)K, ws.part, ws.cnt);
   return hipGetLastError();
+}
+
+template <class QF, typename XT, int MT, int CHP>
+hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
+                         const nfhip::Workspace& ws, hipStream_t s) {
+  const long wgs = ((long)N + 63) / 64;
+  int ks, kg;
+  skinny_split<MT, CHP>(wgs, K, ws, ks, kg);
+  SkinnyGroup grp{};
+  grp.W[0] = static_cast<const uint8_t*>(W);
+  grp.C[0] = C;
+  grp.N[0] = (int)N;
+  for (int q = 1; q <= kSkGroupMax; ++q) grp.begin[q] = (int)wgs;
+  grp.count = 1;
+  return skinny_launch_group<QF, XT, MT, CHP>(A, grp, wgs, M, K, ks, kg, ws, s);
+}
+
+// A group of jobs goes out as one launch when every job would get the same
+// kernel variant and K split on its own (so each output is bit-identical to
+// its own launch); otherwise hipErrorNotSupported.
+template <class QF, typename XT, int MT, int CHP>
+hipError_t skinny_group_same_split(const void* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
+                                   const nfhip::Workspace& ws, hipStream_t s) {
+  SkinnyGroup grp{};
+  long tiles = 0;
+  int ks0 = 0, kg0 = 0;
+  for (uint32_t j = 0; j < n; ++j) {
+    const long wgs = ((long)jobs[j].N + 63) / 64;
+    int ks, kg;
+    skinny_split<MT, CHP>(wgs, K, ws, ks, kg);
+    if (j == 0) {
+      ks0 = ks;
+      kg0 = kg;
+    } else if (ks != ks0 || kg != kg0) {
+      return hipErrorNotSupported;
+    }
+    grp.W[j] = static_cast<const uint8_t*>(jobs[j].W);
+    grp.C[j] = jobs[j].C;
+    grp.N[j] = (int)jobs[j].N;
+    grp.begin[j] = (int)tiles;
+    tiles += wgs;
+  }
+  for (int q = (int)n; q <= kSkGroupMax; ++q) grp.begin[q] = (int)tiles;
+  grp.count = (int)n;
+  return skinny_launch_group<QF, XT, MT, CHP>(A, grp, tiles, M, K, ks0, kg0, ws, s);
 }
 
 // Activation tiles per launch (16 rows each) and pairs per staged chunk,
@@ -502,9 +596,49 @@ hipError_t skinny_dispatch(const void* A, const void* W, void* C, uint32_t M, ui
   }
 }
 
+// The variant a job gets on its own (skinny_dispatch's choice); a group
+// launch needs the same for every job.
+template <class QF, typename XT>
+int skinny_variant(uint32_t M, uint32_t N) {
+  const bool small = N < 64u * 128u;
+  if constexpr (sizeof(XT) == 4) return M <= 16 ? (small ? 0 : 1) : 2;
+  return M <= 16 ? (small ? 0 : 3) : (small ? 2 : 4);
+}
+
+template <class QF, typename XT>
+hipError_t skinny_group_dispatch(const void* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
+                                 const nfhip::Workspace& ws, hipStream_t s) {
+  constexpr bool kQ4 = SkW<QF>::kLoads == 5;
+  if (n < 1 || n > (uint32_t)kSkGroupMax || M < 1 || M > 32) return hipErrorNotSupported;
+  const int v = skinny_variant<QF, XT>(M, jobs[0].N);
+  for (uint32_t j = 1; j < n; ++j)
+    if (skinny_variant<QF, XT>(M, jobs[j].N) != v) return hipErrorNotSupported;
+  if constexpr (sizeof(XT) == 4) {
+    if (v == 0) return skinny_group_same_split<QF, XT, 1, 1>(A, jobs, n, M, K, ws, s);
+    if (v == 1) return skinny_group_same_split<QF, XT, 1, 2>(A, jobs, n, M, K, ws, s);
+    return skinny_group_same_split<QF, XT, 2, 1>(A, jobs, n, M, K, ws, s);
+  } else {
+    if (v == 0) return skinny_group_same_split<QF, XT, 1, 1>(A, jobs, n, M, K, ws, s);
+    if (v == 3) return skinny_group_same_split<QF, XT, 1, kQ4 ? 4 : 2>(A, jobs, n, M, K, ws, s);
+    if (v == 2) return skinny_group_same_split<QF, XT, 2, 1>(A, jobs, n, M, K, ws, s);
+    return skinny_group_same_split<QF, XT, 2, kQ4 ? 2 : 1>(A, jobs, n, M, K, ws, s);
+  }
+}
+
 }  // namespace nfk
 
 namespace nfhip {
+
+hipError_t launch_skinny_group(QFmt q, EType t, const void* A, const GemvJob* jobs, uint32_t n, uint32_t M,
+                               uint32_t K, const Workspace& ws, hipStream_t s) {
+  for (uint32_t j = 0; j < n; ++j)
+    if (!skinny_fits(M, jobs[j].N, K, A, jobs[j].W)) return hipErrorNotSupported;
+  if (q == QFmt::Q4_0)
+    return t == EType::F32 ? nfk::skinny_group_dispatch<nfk::Q4_0, float>(A, jobs, n, M, K, ws, s)
+                           : nfk::skinny_group_dispatch<nfk::Q4_0, nfk::half_t>(A, jobs, n, M, K, ws, s);
+  return t == EType::F32 ? nfk::skinny_group_dispatch<nfk::Q8_0, float>(A, jobs, n, M, K, ws, s)
+                         : nfk::skinny_group_dispatch<nfk::Q8_0, nfk::half_t>(A, jobs, n, M, K, ws, s);
+}
 
 bool skinny_fits(uint32_t M, uint32_t N, uint32_t K, const void* A, const void* W) {
   // 32-bit in-kernel offsets: weight matrix and activation tile below 4 GB

@@ -42,6 +42,8 @@ struct GemvJob {
 };
 hipError_t launch_gemv_group(QFmt q, EType t, const void* A, const GemvJob* jobs, uint32_t n, uint32_t M,
                              uint32_t K, hipStream_t s);
+hipError_t launch_skinny_group(QFmt q, EType t, const void* A, const GemvJob* jobs, uint32_t n, uint32_t M,
+                               uint32_t K, const Workspace& ws, hipStream_t s);
 
 // Small-batch (M <= 64) MFMA kernel; skinny_fits() says whether a shape and
 // operand alignment suit it.
@@ -49,6 +51,10 @@ bool skinny_fits(uint32_t M, uint32_t N, uint32_t K, const void* A, const void* 
 uint32_t skinny_max_rows(EType t);  // activation rows per launch
 hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M, uint32_t N,
                          uint32_t K, const Workspace& ws, hipStream_t s);
+// Several small-batch linears over the same activations (M <= 32, same
+// format, dtype and K) in one launch, each computed exactly as launch_skinny
+// would; hipErrorNotSupported when they would not get the same kernel
+// variant and K split on their own (the caller launches them one by one).
 
 // tile: Tuning::gemm_tile (-1 = register-dequantizing kernel, 0..6 = an
 // LDS-staged tile shape).

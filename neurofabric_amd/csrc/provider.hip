@@ -502,8 +502,8 @@ nf_status prepare(Provider* p, const char* op_name, const nf_buffer* inputs, uin
 }
 
 // Enqueue prepared dispatches in order.  n > 1 only for a group that
-// groupable() accepted: one grouped GEMV launch (or, if the kernel declines
-// the group, one launch each).
+// groupable() accepted: one grouped launch of the GEMV or small-batch kernel
+// (or, if the kernel declines the group, one launch each).
 nf_status launch(Provider* p, const Prepared* prs, uint32_t n) {
   hipError_t e = hipSuccess;
   {
@@ -526,7 +526,9 @@ nf_status launch(Provider* p, const Prepared* prs, uint32_t n) {
       GemvJob jobs[kGemvGroupMax];
       for (uint32_t j = 0; j < n; ++j) jobs[j] = GemvJob{prs[j].in[1]->dev, prs[j].out[0]->dev, prs[j].pl.N};
       const Plan& pl = prs[0].pl;
-      e = launch_gemv_group(pl.q, pl.c, prs[0].in[0]->dev, jobs, n, pl.M, pl.K, p->stream);
+      e = pl.path == Path::Gemv ? launch_gemv_group(pl.q, pl.c, prs[0].in[0]->dev, jobs, n, pl.M, pl.K, p->stream)
+                                : launch_skinny_group(pl.q, pl.c, prs[0].in[0]->dev, jobs, n, pl.M, pl.K, p->ws,
+                                                      p->stream);
       if (e == hipErrorNotSupported) {
         p->launch_groups.fetch_add(n - 1, std::memory_order_relaxed);
         e = hipSuccess;
@@ -805,15 +807,21 @@ bool overlaps(const Buffer* a, const Buffer* b) {
   return a0 < b0 + b->alloc_bytes && b0 < a0 + a->alloc_bytes;
 }
 
-// May `next` join the GEMV group g[0..n)?  Same kernel family, same
-// activation buffer, M and K, and no hazard between the members: no output
-// overlaps another member's activations, weights or output, so running them
-// in one launch is the same as running them in order.
+// Paths whose kernels take a group of same-input jobs in one launch: the
+// decode GEMV, and the small-batch MFMA kernel while the rows fit one launch.
+bool group_path(const Plan& p) {
+  return p.path == Path::Gemv || (p.path == Path::Skinny && p.M <= skinny_max_rows(p.c));
+}
+
+// May `next` join the group g[0..n)?  Same kernel family, same activation
+// buffer, M and K, and no hazard between the members: no output overlaps
+// another member's activations, weights or output, so running them in one
+// launch is the same as running them in order.
 bool groupable(const Prepared* g, uint32_t n, const Prepared& next) {
   if (n >= (uint32_t)kGemvGroupMax) return false;
   const Plan& a = g[0].pl;
   const Plan& b = next.pl;
-  if (a.path != Path::Gemv || b.path != Path::Gemv || a.op != b.op || a.q != b.q || a.a != b.a || a.c != b.c ||
+  if (!group_path(a) || a.path != b.path || a.op != b.op || a.q != b.q || a.a != b.a || a.c != b.c ||
       a.M != b.M || a.K != b.K || next.n_in < 2 || next.n_out < 1 || next.in[0] != g[0].in[0])
     return false;
   for (uint32_t j = 0; j < n; ++j) {
@@ -837,7 +845,7 @@ NF_API nf_status nf_hip_run_tasks(nf_provider self, const nf_task_desc* tasks, u
       nf_status st = prepare(p, t.op_name, t.inputs, t.n_inputs, const_cast<nf_buffer*>(t.outputs), t.n_outputs, &prs[0]);
       if (st != NF_OK) return st;
       uint32_t n = 1;
-      while (group && prs[0].pl.path == Path::Gemv && i + n < n_tasks && n < (uint32_t)kGemvGroupMax) {
+      while (group && group_path(prs[0].pl) && i + n < n_tasks && n < (uint32_t)kGemvGroupMax) {
         const nf_task_desc& u = tasks[i + n];
         if (prepare(p, u.op_name, u.inputs, u.n_inputs, const_cast<nf_buffer*>(u.outputs), u.n_outputs, &prs[n]) !=
                 NF_OK ||

@@ -1,5 +1,5 @@
-"""nf_hip_run_tasks merges adjacent decode GEMVs that read the same
-activation buffer (q/k/v, gate/up) into one launch.  Each merged result must
+"""nf_hip_run_tasks merges adjacent decode GEMVs and small-batch linears
+that read the same activation buffer (q/k/v, gate/up) into one launch.  Each merged result must
 be bit-identical to dispatching the tasks one by one, the launch count must
 show the merge, and a hazard between two tasks (here: both write the same
 output) must keep them in separate launches."""
@@ -51,8 +51,9 @@ def _block(provider, fmt, f16, M, hidden, kv, ffn, seed):
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
-@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("M", [1, 3, 8, 16])
 def test_run_tasks_merges_same_input_gemvs(provider, oracle_mod, fmt, f16, M):
+    """M <= 4: decode GEMV groups; M = 8, 16: small-batch MFMA groups."""
     hidden, kv, ffn = 1024, 128, 2816
     op, acts, outs, specs, tasks, bufs, host_w = _block(provider, fmt, f16, M, hidden, kv, ffn, seed=M * 7)
     npdt = np.float16 if f16 else np.float32
