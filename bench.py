@@ -71,7 +71,7 @@ def parse(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--sweep", action="store_true", help="configs[4] GEMV/MFMA crossover sweep")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
-    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4"], default=None,
+    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "dq"], default=None,
                     help="run one configs[i] section alone and print its JSON (profiling aid)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 4 device-to-device copies of BYTES (reference for HBM byte counters)")
@@ -395,6 +395,42 @@ def run_c2(prov) -> dict:
     return pre
 
 
+DQ_FORMATS = ["q4_0", "q8_0", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q4_k", "q5_k", "q6_k"]
+
+
+def run_dq(prov, n_elems: int = 11008 * 4096, copies: int = 2) -> dict:
+    """Standalone dequantization (the weight-upload warm-up path) of one
+    Llama-2-7B FFN weight (11008 x 4096 elements) in every block format, to
+    f16 and f32, over `copies` distinct input/output buffer pairs per format
+    (each pair 115..205 MB, so consecutive launches do not hit in cache).
+    Achieved bandwidth counts the algorithmic bytes: blocks read + output
+    written."""
+    from neurofabric_amd import abi, synthetic as syn
+    res = {}
+    for fmt in DQ_FORMATS:
+        _, be = syn.KQ_GEOM[fmt]
+        blocks = syn.kquant_blocks(fmt, n_elems // be, seed=len(res))
+        qdt = getattr(abi, f"NF_DTYPE_{fmt.upper()}")
+        for f16 in (True, False):
+            st = Step(prov)
+            odt = abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32
+            for _ in range(copies):
+                w = prov.alloc_array(blocks, qdt)
+                o = prov.alloc(odt, n_elems * (2 if f16 else 4))
+                st.buffers += [w, o]
+                st.add(f"dequant_{fmt}" + ("_f16" if f16 else ""), [w], [o], 0, 0, 0)
+            st.finish()
+            r = time_step(prov, st, 10, 2, "eager")
+            gbs = st.bytes / (r["ms_per_step"] * 1e-3) / 1e9
+            res[f"{fmt}_{'f16' if f16 else 'f32'}"] = {"GB_s": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
+                                                       "us_per_launch": r["us_per_launch"],
+                                                       "bytes_per_launch": st.bytes / copies,
+                                                       "kernel": sorted(st.kernels)[0]}
+            log(f"[bench] dequant {fmt} {'f16' if f16 else 'f32'}: {gbs:.0f} GB/s, {r['us_per_launch']:.1f} us")
+            st.release()
+    return res
+
+
 def load_pmc_summary():
     if PMC_SUMMARY.exists():
         try:
@@ -421,7 +457,8 @@ def main(argv=None) -> int:
     prov.init()
     if args.only:
         sections = {"c0": lambda: run_c0(prov, args.mode), "c2": lambda: run_c2(prov),
-                    "c3": lambda: run_c3(prov, args.mode), "c4": lambda: crossover_sweep(prov)}
+                    "c3": lambda: run_c3(prov, args.mode), "c4": lambda: crossover_sweep(prov),
+                    "dq": lambda: run_dq(prov)}
         print(json.dumps({args.only: sections[args.only]()}), flush=True)
         return 0
 
@@ -472,6 +509,7 @@ def main(argv=None) -> int:
         extra["c0_gemv_5632x2048"] = run_c0(prov, args.mode)
         extra["c3_llama3_8b_q8_0_decode"] = run_c3(prov, args.mode)
         extra["c2_prefill_f16"] = run_c2(prov)
+        extra["dequant_7b_ffn_weight"] = run_dq(prov)
     if args.sweep:
         extra["c4_crossover"] = crossover_sweep(prov)
 

@@ -37,6 +37,14 @@ NF_DTYPE_I32 = 4
 NF_DTYPE_U8 = 5
 NF_DTYPE_Q4_0 = 6
 NF_DTYPE_Q8_0 = 7
+NF_DTYPE_Q4_1 = 8
+NF_DTYPE_Q5_0 = 9
+NF_DTYPE_Q5_1 = 10
+NF_DTYPE_Q2_K = 11
+NF_DTYPE_Q3_K = 12
+NF_DTYPE_Q4_K = 13
+NF_DTYPE_Q5_K = 14
+NF_DTYPE_Q6_K = 15
 
 NF_MEM_DOMAIN_CPU = 0
 NF_MEM_DOMAIN_UNIFIED = 1

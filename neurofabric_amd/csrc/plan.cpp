@@ -30,6 +30,23 @@ const std::unordered_map<std::string, OpInfo>& op_table() {
       {"dequant_q4_0_f16", {OpKind::Dequant, QFmt::Q4_0, true}},
       {"dequant_q8_0", {OpKind::Dequant, QFmt::Q8_0, false}},
       {"dequant_q8_0_f16", {OpKind::Dequant, QFmt::Q8_0, true}},
+      // metal_provider.mm:3159-3176
+      {"dequant_q4_1", {OpKind::Dequant, QFmt::Q4_1, false}},
+      {"dequant_q4_1_f16", {OpKind::Dequant, QFmt::Q4_1, true}},
+      {"dequant_q5_0", {OpKind::Dequant, QFmt::Q5_0, false}},
+      {"dequant_q5_0_f16", {OpKind::Dequant, QFmt::Q5_0, true}},
+      {"dequant_q5_1", {OpKind::Dequant, QFmt::Q5_1, false}},
+      {"dequant_q5_1_f16", {OpKind::Dequant, QFmt::Q5_1, true}},
+      {"dequant_q2_k", {OpKind::Dequant, QFmt::Q2_K, false}},
+      {"dequant_q2_k_f16", {OpKind::Dequant, QFmt::Q2_K, true}},
+      {"dequant_q3_k", {OpKind::Dequant, QFmt::Q3_K, false}},
+      {"dequant_q3_k_f16", {OpKind::Dequant, QFmt::Q3_K, true}},
+      {"dequant_q4_k", {OpKind::Dequant, QFmt::Q4_K, false}},
+      {"dequant_q4_k_f16", {OpKind::Dequant, QFmt::Q4_K, true}},
+      {"dequant_q5_k", {OpKind::Dequant, QFmt::Q5_K, false}},
+      {"dequant_q5_k_f16", {OpKind::Dequant, QFmt::Q5_K, true}},
+      {"dequant_q6_k", {OpKind::Dequant, QFmt::Q6_K, false}},
+      {"dequant_q6_k_f16", {OpKind::Dequant, QFmt::Q6_K, true}},
       {"dequant_q4_0_linear", {OpKind::FusedLinear, QFmt::Q4_0, false}},
       {"dequant_q4_0_linear_f16", {OpKind::FusedLinear, QFmt::Q4_0, false}},
       {"dequant_q8_0_linear", {OpKind::FusedLinear, QFmt::Q8_0, false}},
@@ -40,7 +57,21 @@ const std::unordered_map<std::string, OpInfo>& op_table() {
   return t;
 }
 
-const char* qname(QFmt q) { return q == QFmt::Q4_0 ? "q4_0" : "q8_0"; }
+const char* qname(QFmt q) {
+  switch (q) {
+    case QFmt::Q4_0: return "q4_0";
+    case QFmt::Q8_0: return "q8_0";
+    case QFmt::Q4_1: return "q4_1";
+    case QFmt::Q5_0: return "q5_0";
+    case QFmt::Q5_1: return "q5_1";
+    case QFmt::Q2_K: return "q2_k";
+    case QFmt::Q3_K: return "q3_k";
+    case QFmt::Q4_K: return "q4_k";
+    case QFmt::Q5_K: return "q5_k";
+    case QFmt::Q6_K: return "q6_k";
+    default: return "none";
+  }
+}
 const char* ename(EType e) { return e == EType::F16 ? "f16" : "f32"; }
 
 nf_status fail(std::string* why, const std::string& msg) {
@@ -88,8 +119,10 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
     p.c = info.f16_out ? EType::F16 : EType::F32;
     p.path = Path::Dequant;
     p.count = outs[0]->size_bytes / elt_bytes(p.c);
-    const uint64_t blocks = (p.count + 31) / 32;
+    const uint64_t be = block_elems(p.q);
+    const uint64_t blocks = (p.count + be - 1) / be;
     p.weight_bytes = blocks * block_bytes(p.q);
+    p.in_bytes = ins[0]->size_bytes;
     p.out_bytes = p.count * elt_bytes(p.c);
     if (ins[0]->size_bytes < p.weight_bytes)
       return fail(why, "quantized input holds fewer blocks than the output needs");

@@ -14,7 +14,9 @@
 namespace nfhip {
 
 enum class OpKind { Dequant, FusedLinear, DenseLinear };
-enum class QFmt { None, Q4_0, Q8_0 };
+// Q4_0 and Q8_0 serve the fused linear kernels; every format serves the
+// standalone dequant ops.
+enum class QFmt { None, Q4_0, Q8_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K };
 enum class EType { F32, F16 };
 enum class Path {
   Dequant,   // standalone dequantization
@@ -53,14 +55,35 @@ struct Plan {
   EType a = EType::F32, b = EType::F32, c = EType::F32;
   Path path = Path::Dequant;
   uint32_t M = 0, N = 0, K = 0;
-  uint64_t count = 0;  // dequant: output elements
+  uint64_t count = 0;     // dequant: output elements
+  uint64_t in_bytes = 0;  // dequant: size of the quantized input buffer
   uint64_t weight_bytes = 0, act_bytes = 0, out_bytes = 0, flops = 0;
   std::string kernel;
 };
 
-// Bytes of one 32-element block: Q4_0 = 2 (fp16 scale) + 16, Q8_0 = 2 + 32
-// (gguf_loader.hpp:64,68).
-inline uint32_t block_bytes(QFmt q) { return q == QFmt::Q4_0 ? 18u : (q == QFmt::Q8_0 ? 34u : 0u); }
+// Bytes and elements of one block (gguf_loader.hpp:64-74): Q4_0 = 2 (fp16
+// scale) + 16, Q8_0 = 2 + 32, Q4_1 20, Q5_0 22, Q5_1 24 (32 elements);
+// Q2_K 84, Q3_K 110, Q4_K 144, Q5_K 176, Q6_K 210 (256 elements).
+inline uint32_t block_bytes(QFmt q) {
+  switch (q) {
+    case QFmt::Q4_0: return 18u;
+    case QFmt::Q8_0: return 34u;
+    case QFmt::Q4_1: return 20u;
+    case QFmt::Q5_0: return 22u;
+    case QFmt::Q5_1: return 24u;
+    case QFmt::Q2_K: return 84u;
+    case QFmt::Q3_K: return 110u;
+    case QFmt::Q4_K: return 144u;
+    case QFmt::Q5_K: return 176u;
+    case QFmt::Q6_K: return 210u;
+    default: return 0u;
+  }
+}
+inline uint32_t block_elems(QFmt q) {
+  return (q == QFmt::Q2_K || q == QFmt::Q3_K || q == QFmt::Q4_K || q == QFmt::Q5_K || q == QFmt::Q6_K)
+             ? 256u
+             : 32u;
+}
 inline uint32_t elt_bytes(EType t) { return t == EType::F16 ? 2u : 4u; }
 
 // Validates and plans one dispatch.  `ins`/`outs` are descriptor pointers

@@ -418,7 +418,9 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, int g
                     hipStream_t s) {
   switch (pl.path) {
     case Path::Dequant:
-      return launch_dequant(pl.q, pl.c, in[0]->dev, out[0]->dev, pl.count, s);
+      if (pl.q == QFmt::Q4_0 || pl.q == QFmt::Q8_0)
+        return launch_dequant(pl.q, pl.c, in[0]->dev, out[0]->dev, pl.count, s);
+      return launch_kquant_dequant(pl.q, pl.c, in[0]->dev, pl.in_bytes, out[0]->dev, pl.count, s);
     case Path::Gemv:
       return launch_gemv(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
     case Path::Skinny: {

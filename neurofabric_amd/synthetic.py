@@ -88,6 +88,30 @@ def weights(fmt: str, n: int, k: int, seed: int) -> np.ndarray:
     return q4_0_weights(n, k, seed) if fmt == "q4_0" else q8_0_weights(n, k, seed)
 
 
+# Geometry (block bytes, elements per block) and the byte offsets of the fp16
+# fields (scale d, min m / dmin) of every block format the dequant ops take
+# (gguf_loader.hpp:64-74, metal_provider.mm:500-736).
+KQ_GEOM = {"q4_0": (18, 32), "q8_0": (34, 32), "q4_1": (20, 32), "q5_0": (22, 32),
+           "q5_1": (24, 32), "q2_k": (84, 256), "q3_k": (110, 256), "q4_k": (144, 256),
+           "q5_k": (176, 256), "q6_k": (210, 256)}
+KQ_F16_FIELDS = {"q4_0": (0,), "q8_0": (0,), "q4_1": (0, 2), "q5_0": (0,), "q5_1": (0, 2),
+                 "q2_k": (80, 82), "q3_k": (108,), "q4_k": (0, 2), "q5_k": (0, 2), "q6_k": (208,)}
+
+
+def kquant_blocks(fmt: str, n_blocks: int, seed: int, scale: float = 0.01) -> np.ndarray:
+    """n_blocks random blocks of `fmt` as uint8 [n_blocks, block_bytes]: every
+    code / scale byte uniform, every fp16 field |N(0,1)| * scale rounded to
+    nearest even (finite, so no NaN reaches the outputs)."""
+    bs, _ = KQ_GEOM[fmt]
+    r = rng_for(seed)
+    raw = r.integers(0, 256, (n_blocks, bs), dtype=np.uint8)
+    for off in KQ_F16_FIELDS[fmt]:
+        h = (np.abs(r.standard_normal(n_blocks)) * scale).astype(np.float16).view(np.uint16)
+        raw[:, off] = (h & 0xFF).astype(np.uint8)
+        raw[:, off + 1] = (h >> 8).astype(np.uint8)
+    return raw
+
+
 def activations(m: int, k: int, seed: int, dtype=np.float32) -> np.ndarray:
     """A[m, k] ~ N(0, 1); f16 activations are rounded to nearest even."""
     x = rng_for(seed).standard_normal((m, k)).astype(np.float32)

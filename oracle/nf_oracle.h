@@ -17,6 +17,14 @@
  *                             (plugins/metal/src/metal_provider.mm:749,758,1457,1467)
  *   nf_oracle_dequant_*_f32   ref_dequant_q4_0/q8_0, dequant_test.cpp:112-128
  *   nf_oracle_dequant_*_f16   dequant_q4_0_f16/q8_0_f16, metal_provider.mm:741-759
+ *   nf_oracle_dequant         every dequant_<fmt>[_f16] op:
+ *                             q4_1/q5_0/q5_1/q2_k/q3_k/q4_k/q5_k f32 follow
+ *                             the CPU refs of tests/driver/kquant_dequant_test.cpp:118-224;
+ *                             q6_k follows metal_provider.mm:534-573 (no CPU
+ *                             ref exists); the _f16 ops are the RNE half of
+ *                             the same f32 value (metal_provider.mm:761-900),
+ *                             except q3_k_f16, whose kernel reads raw bytes
+ *                             as scales (metal_provider.mm:833-848)
  *   nf_oracle_linear_*        naive sequential-k loop, dequant_test.cpp:313-319,
  *                             with B stored [N,K] (dequant_test.cpp:321-325)
  *   nf_oracle_fused_*         dequant_q4_0_linear_tiled[_f16] semantics,
@@ -34,7 +42,11 @@
 extern "C" {
 #endif
 
-enum { NF_ORACLE_Q4_0 = 0, NF_ORACLE_Q8_0 = 1 };
+enum {
+    NF_ORACLE_Q4_0 = 0, NF_ORACLE_Q8_0 = 1, NF_ORACLE_Q4_1 = 2, NF_ORACLE_Q5_0 = 3,
+    NF_ORACLE_Q5_1 = 4, NF_ORACLE_Q2_K = 5, NF_ORACLE_Q3_K = 6, NF_ORACLE_Q4_K = 7,
+    NF_ORACLE_Q5_K = 8, NF_ORACLE_Q6_K = 9, NF_ORACLE_NFMT = 10
+};
 
 float nf_oracle_f16_to_f32(uint16_t h);
 uint16_t nf_oracle_f32_to_f16_rne(float f);
@@ -49,6 +61,16 @@ void nf_oracle_dequant_q4_0_f32(const uint8_t *blocks, uint64_t count, float *ou
 void nf_oracle_dequant_q8_0_f32(const uint8_t *blocks, uint64_t count, float *out);
 void nf_oracle_dequant_q4_0_f16(const uint8_t *blocks, uint64_t count, uint16_t *out);
 void nf_oracle_dequant_q8_0_f16(const uint8_t *blocks, uint64_t count, uint16_t *out);
+
+/* Any of the ten block formats: `count` elements to f32 (f16_out = 0) or
+ * fp16 bits (f16_out = 1) with the semantics of dequant_<fmt>[_f16].
+ * `in_bytes` is the size of the input buffer: dequant_q3_k_f16 reads two
+ * bytes past its last block, taken as 0 beyond `in_bytes`.  Returns -1 for an
+ * unknown format or an input shorter than ceil(count / elems) blocks. */
+int nf_oracle_dequant(int fmt, const uint8_t *blocks, uint64_t in_bytes, uint64_t count, int f16_out,
+                      void *out);
+uint32_t nf_oracle_block_bytes(int fmt);
+uint32_t nf_oracle_block_elems(int fmt);
 
 /* C[M,N] = A[M,K] * B[N,K]^T, fp32 accumulation in k order. */
 void nf_oracle_linear_f32(const float *A, const float *B, float *C,

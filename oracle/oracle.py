@@ -18,7 +18,13 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "lib" / "libnf_oracle.so"
 Q4_0, Q8_0 = 0, 1
-FMT = {"q4_0": Q4_0, "q8_0": Q8_0}
+FMT = {"q4_0": 0, "q8_0": 1, "q4_1": 2, "q5_0": 3, "q5_1": 4,
+       "q2_k": 5, "q3_k": 6, "q4_k": 7, "q5_k": 8, "q6_k": 9}
+# (block bytes, elements per block) of each format (gguf_loader.hpp:64-74).
+GEOM = {"q4_0": (18, 32), "q8_0": (34, 32), "q4_1": (20, 32), "q5_0": (22, 32),
+        "q5_1": (24, 32), "q2_k": (84, 256), "q3_k": (110, 256), "q4_k": (144, 256),
+        "q5_k": (176, 256), "q6_k": (210, 256)}
+REF_KQUANT = HERE / "_ref" / "libnfref_kquant.so"
 
 _lib = None
 
@@ -48,6 +54,12 @@ def lib() -> C.CDLL:
         for name in ("q4_0", "q8_0"):
             getattr(L, f"nf_oracle_dequant_{name}_f32").argtypes = [u8p, C.c_uint64, f32p]
             getattr(L, f"nf_oracle_dequant_{name}_f16").argtypes = [u8p, C.c_uint64, u16p]
+        L.nf_oracle_dequant.argtypes = [C.c_int, u8p, C.c_uint64, C.c_uint64, C.c_int, C.c_void_p]
+        L.nf_oracle_dequant.restype = C.c_int
+        L.nf_oracle_block_bytes.argtypes = [C.c_int]
+        L.nf_oracle_block_bytes.restype = C.c_uint32
+        L.nf_oracle_block_elems.argtypes = [C.c_int]
+        L.nf_oracle_block_elems.restype = C.c_uint32
         L.nf_oracle_linear_f32.argtypes = [f32p, f32p, f32p, C.c_uint32, C.c_uint32, C.c_uint32]
         L.nf_oracle_linear_f16.argtypes = [u16p, u16p, u16p, C.c_uint32, C.c_uint32, C.c_uint32]
         L.nf_oracle_fused_f32.argtypes = [f32p, u8p, C.c_int, f32p] + [C.c_uint32] * 6
@@ -75,17 +87,43 @@ def f32_to_f16_trunc(x: float) -> int:
 
 
 def dequant(blocks: np.ndarray, fmt: str, count: int, f16: bool = False) -> np.ndarray:
-    """f32 values, or fp16 BITS (uint16) when f16=True."""
+    """f32 values, or fp16 BITS (uint16) when f16=True.  `blocks` is the whole
+    input buffer (dequant_q3_k_f16 reads two bytes past its last block)."""
     b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
-    bs = 18 if fmt == "q4_0" else 34
-    if b.size < (count + 31) // 32 * bs:
+    bs, be = GEOM[fmt]
+    if b.size < (count + be - 1) // be * bs:
         raise ValueError("not enough blocks")
+    if fmt not in ("q4_0", "q8_0"):
+        out = np.empty(count, np.uint16 if f16 else np.float32)
+        if lib().nf_oracle_dequant(FMT[fmt], b, b.size, count, int(f16), out.ctypes.data) != 0:
+            raise ValueError("nf_oracle_dequant rejected the input")
+        return out
     if f16:
         out = np.empty(count, np.uint16)
         getattr(lib(), f"nf_oracle_dequant_{fmt}_f16")(b, count, out)
     else:
         out = np.empty(count, np.float32)
         getattr(lib(), f"nf_oracle_dequant_{fmt}_f32")(b, count, out)
+    return out
+
+
+def ref_kquant_available() -> bool:
+    return REF_KQUANT.exists()
+
+
+def ref_kquant_dequant(blocks: np.ndarray, fmt: str, n_blocks: int) -> np.ndarray:
+    """The reference's own CPU dequantizer for `fmt` (q4_1, q5_0, q5_1, q2_k,
+    q3_k, q4_k, q5_k), compiled from kquant_dequant_test.cpp by
+    `make -C oracle ref` into oracle/_ref/libnfref_kquant.so."""
+    L = C.CDLL(str(REF_KQUANT))
+    L.nfref_kquant_dequant.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p]
+    L.nfref_kquant_dequant.restype = C.c_int
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    bs, be = GEOM[fmt]
+    assert b.size >= n_blocks * bs
+    out = np.empty(n_blocks * be, np.float32)
+    if L.nfref_kquant_dequant(FMT[fmt], b.ctypes.data, n_blocks, out.ctypes.data) != 0:
+        raise ValueError(f"no reference CPU dequantizer for {fmt}")
     return out
 
 

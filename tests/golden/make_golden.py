@@ -25,6 +25,18 @@ small_linear_cases.npz
     restatement and checked here against a float64 evaluation of the same
     dequantized values (relative error <= 1e-5 normwise).
 
+kquant_reference_vectors.npz
+    Inputs and outputs of the reference's own CPU dequantizers
+    ref_dequant_q4_1 .. ref_dequant_q5_k (kquant_dequant_test.cpp:118-224),
+    compiled from that file by `make -C oracle ref` into
+    oracle/_ref/libnfref_kquant.so (only where the reference tree is
+    present).  Per format: `<fmt>_reftest_*` is the test's own input pattern
+    (bytes (i*73+17) & 0xFF, bytes 0-1 of block b = its truncating fp16
+    encoding of 0.01*(b+1); kquant_dequant_test.cpp:240-252) over the test's
+    block count, `<fmt>_rand_*` is synthetic.kquant_blocks(fmt, .., seed=900+i)
+    over 2048 elements.  The oracle must reproduce every output bit (NaN as a
+    class); the script asserts it before writing.
+
 synthetic_sha256.json
     SHA-256 of the deterministic synthetic inputs of the BASELINE configs
     (weights seeded N*7 + K, activations seeded K), so any host can check it
@@ -159,6 +171,43 @@ def write_small_cases(path: Path):
     np.savez_compressed(path, **arrays)
 
 
+KQ_REF_FORMATS = [("q4_1", 8), ("q5_0", 8), ("q5_1", 8), ("q2_k", 4), ("q3_k", 4), ("q4_k", 4), ("q5_k", 4)]
+
+
+def reftest_pattern(fmt: str, n_blocks: int) -> np.ndarray:
+    """kquant_dequant_test.cpp:240-252: pseudo-random bytes, then bytes 0-1 of
+    every block set to the test's fp16 encoding of 0.01 * (b + 1)."""
+    bs, _ = syn.KQ_GEOM[fmt]
+    raw = ((np.arange(n_blocks * bs, dtype=np.int64) * 73 + 17) & 0xFF).astype(np.uint8).reshape(n_blocks, bs)
+    for b in range(n_blocks):
+        h = trunc_f16(np.float32(0.01) * np.float32(b + 1))
+        raw[b, 0], raw[b, 1] = h & 0xFF, h >> 8
+    return raw
+
+
+def _same_bits_nan_class(a: np.ndarray, b: np.ndarray) -> bool:
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+def write_kquant_vectors(path: Path):
+    if not orc.ref_kquant_available():
+        print("oracle/_ref/libnfref_kquant.so not built (needs the reference tree):", path.name, "kept as is")
+        return
+    arrays = {}
+    for i, (fmt, n_ref) in enumerate(KQ_REF_FORMATS):
+        _, be = syn.KQ_GEOM[fmt]
+        for tag, blocks in (("reftest", reftest_pattern(fmt, n_ref)),
+                            ("rand", syn.kquant_blocks(fmt, 2048 // be, seed=900 + i))):
+            n = blocks.shape[0]
+            want = orc.ref_kquant_dequant(blocks, fmt, n)
+            got = orc.dequant(blocks, fmt, n * be)
+            assert _same_bits_nan_class(got, want), (fmt, tag)
+            arrays[f"{fmt}_{tag}_blocks"] = blocks
+            arrays[f"{fmt}_{tag}_f32"] = want
+    np.savez_compressed(path, **arrays)
+
+
 def config_inputs():
     """(label, fmt, N, K) of every distinct weight shape of the configs, plus
     activation shapes (label, M, K)."""
@@ -187,6 +236,7 @@ def write_hashes(path: Path):
 def main():
     write_known_answers(HERE / "known_answer_blocks.npz")
     write_small_cases(HERE / "small_linear_cases.npz")
+    write_kquant_vectors(HERE / "kquant_reference_vectors.npz")
     write_hashes(HERE / "synthetic_sha256.json")
     print("wrote", *(p.name for p in sorted(HERE.glob("*.npz"))), "synthetic_sha256.json")
 

@@ -12,6 +12,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 REPO = Path(__file__).resolve().parents[1]
 REF_DEQUANT = REPO / "oracle" / "_ref" / "dequant_test"
+REF_KQUANT = REPO / "oracle" / "_ref" / "kquant_dequant_test"
 
 
 @pytest.mark.skipif(not REF_DEQUANT.exists(), reason="reference test binary not built (needs the reference sources)")
@@ -22,6 +23,16 @@ def test_reference_dequant_test_binary_passes():
     print(r.stdout, r.stderr)
     assert r.returncode == 0
     assert "OK: all Phase 17 dequant tests passed" in r.stdout
+
+
+@pytest.mark.skipif(not REF_KQUANT.exists(), reason="reference test binary not built (needs the reference sources)")
+def test_reference_kquant_dequant_test_binary_passes():
+    """tests/driver/kquant_dequant_test.cpp: dequant_q4_1 .. dequant_q5_k on
+    the GPU against the test's own CPU dequantizers (tolerance 1e-3)."""
+    r = subprocess.run([str(REF_KQUANT)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0
+    assert "OK: all Phase 25 K-quant dequant tests passed" in r.stdout
 
 
 LIFECYCLE = r"""

@@ -172,6 +172,30 @@ def test_plan_dequant_count_from_output_size(lib):
         plan(lib, "dequant_q4_0", [D(abi.NF_DTYPE_Q4_0, 7 * 18)], [D(abi.NF_DTYPE_F32, 256 * 4)])
 
 
+KQ_OPS = {"q4_1": (abi.NF_DTYPE_Q4_1, 20, 32), "q5_0": (abi.NF_DTYPE_Q5_0, 22, 32),
+          "q5_1": (abi.NF_DTYPE_Q5_1, 24, 32), "q2_k": (abi.NF_DTYPE_Q2_K, 84, 256),
+          "q3_k": (abi.NF_DTYPE_Q3_K, 110, 256), "q4_k": (abi.NF_DTYPE_Q4_K, 144, 256),
+          "q5_k": (abi.NF_DTYPE_Q5_K, 176, 256), "q6_k": (abi.NF_DTYPE_Q6_K, 210, 256)}
+
+
+@pytest.mark.parametrize("fmt", sorted(KQ_OPS))
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+def test_plan_kquant_dequant_ops(lib, fmt, f16):
+    """The dequant ops of metal_provider.mm:3159-3176: count from the output
+    size, ceil(count / block elements) blocks of input required."""
+    dt, bs, be = KQ_OPS[fmt]
+    e = 2 if f16 else 4
+    odt = abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32
+    op = f"dequant_{fmt}" + ("_f16" if f16 else "")
+    count = 3 * be - 5  # ragged: the last block is partial
+    p = plan(lib, op, [D(dt, 3 * bs)], [D(odt, count * e)])
+    assert (p["kernel"], p["count"], p["weight_bytes"], p["out_bytes"]) == (
+        f"dequant_{fmt}_{'f16' if f16 else 'f32'}", count, 3 * bs, count * e)
+    with pytest.raises(NfError) as err:
+        plan(lib, op, [D(dt, 3 * bs - 1)], [D(odt, count * e)])
+    assert err.value.status == abi.NF_ERROR_INVALID_ARG
+
+
 def test_plan_dense_linear_dtypes(lib):
     M, N, K = 3, 5, 16
     p = plan(lib, "linear", [D(abi.NF_DTYPE_F16, M * K * 2), D(abi.NF_DTYPE_F16, N * K * 2)],
