@@ -71,7 +71,7 @@ def parse(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--sweep", action="store_true", help="configs[4] GEMV/MFMA crossover sweep")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
-    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "dq"], default=None,
+    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "dq", "up"], default=None,
                     help="run one configs[i] section alone and print its JSON (profiling aid)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 4 device-to-device copies of BYTES (reference for HBM byte counters)")
@@ -431,6 +431,35 @@ def run_dq(prov, n_elems: int = 11008 * 4096, copies: int = 2) -> dict:
     return res
 
 
+def run_upload(prov, mb: int = 512) -> dict:
+    """Weight upload of one `mb` MiB tensor from pageable host memory (as
+    from an mmap of a GGUF file): the reference model layer's map / memcpy /
+    unmap (llama_dag_builder.hpp:146-156) on a fresh buffer, cold (pinned
+    staging newly allocated) and warm (staging reused from the provider's
+    pool), and the one-copy nf_hip_buffer_write.  Host wall time, GB/s."""
+    from neurofabric_amd import abi
+    n = mb << 20
+    src = np.random.default_rng(0).integers(0, 256, n, dtype=np.uint8)
+    res = {}
+    prov.release_staging()
+    for label in ("map_memcpy_unmap_cold", "map_memcpy_unmap_warm", "buffer_write"):
+        b = prov.alloc(abi.NF_DTYPE_U8, n)
+        t0 = time.perf_counter()
+        if label == "buffer_write":
+            b.write(src)
+        else:
+            ptr = b.map()
+            C.memmove(ptr, src.ctypes.data, n)
+            b.unmap()
+        dt = time.perf_counter() - t0
+        ok = bool(np.array_equal(b.read(np.uint8, count=1 << 20, offset=n - (1 << 20)), src[-(1 << 20):]))
+        b.release()
+        res[label] = {"GB_s": n / dt / 1e9, "seconds": dt, "bytes": n, "tail_check": ok}
+        log(f"[bench] upload {mb} MiB {label}: {n / dt / 1e9:.1f} GB/s")
+    prov.release_staging()
+    return res
+
+
 def load_pmc_summary():
     if PMC_SUMMARY.exists():
         try:
@@ -458,7 +487,7 @@ def main(argv=None) -> int:
     if args.only:
         sections = {"c0": lambda: run_c0(prov, args.mode), "c2": lambda: run_c2(prov),
                     "c3": lambda: run_c3(prov, args.mode), "c4": lambda: crossover_sweep(prov),
-                    "dq": lambda: run_dq(prov)}
+                    "dq": lambda: run_dq(prov), "up": lambda: run_upload(prov)}
         print(json.dumps({args.only: sections[args.only]()}), flush=True)
         return 0
 
@@ -510,6 +539,7 @@ def main(argv=None) -> int:
         extra["c3_llama3_8b_q8_0_decode"] = run_c3(prov, args.mode)
         extra["c2_prefill_f16"] = run_c2(prov)
         extra["dequant_7b_ffn_weight"] = run_dq(prov)
+        extra["weight_upload_512MiB"] = run_upload(prov)
     if args.sweep:
         extra["c4_crossover"] = crossover_sweep(prov)
 

@@ -154,6 +154,25 @@ NF_API nf_status nf_hip_get_stream(nf_provider self, void **stream);
  * hand-off to other HIP code in the same process). */
 NF_API nf_status nf_hip_buffer_device_ptr(nf_buffer buf, void **dev_ptr);
 
+/* Copy `bytes` bytes between host memory of any kind (pageable, such as an
+ * mmap of a GGUF file, or pinned) and the byte range [offset, offset+bytes)
+ * of a buffer.  Ordered on the provider stream after every dispatch already
+ * issued; complete on return.  NF_ERROR_INVALID_ARG for a range outside the
+ * buffer or a mapped buffer.  No counterpart in the reference's ABI: it is
+ * the one-copy form of the weight upload the reference's model layer does
+ * with map + memcpy + unmap (model/model/llama_dag_builder.hpp:146-156,
+ * load_weight), which costs a staging copy here (31 GB/s from pageable
+ * memory on MI355X against ~15 GB/s for map/memcpy/unmap with a warm
+ * staging pool). */
+NF_API nf_status nf_hip_buffer_write(nf_buffer buf, uint64_t offset, const void *src, uint64_t bytes);
+NF_API nf_status nf_hip_buffer_read(nf_buffer buf, uint64_t offset, void *dst, uint64_t bytes);
+
+/* Frees the pinned staging blocks that unmapping large buffers (>= 64 MiB)
+ * leaves in the provider's pool for reuse (at most 2 GiB), e.g. once model
+ * weights are uploaded.  Shutdown frees them too.  NULL = the provider this
+ * library registers. */
+NF_API void nf_hip_release_staging(nf_provider self);
+
 /* Last error text recorded by the provider (thread-local, never NULL). */
 NF_API const char *nf_hip_last_error(void);
 

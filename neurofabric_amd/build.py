@@ -37,7 +37,6 @@ HIP_SOURCES = [
     CSRC / "kernels" / "skinny.hip",
     CSRC / "kernels" / "generic.hip",
     CSRC / "kernels" / "dense.hip",
-    CSRC / "kernels" / "kquant.hip",
 ]
 CXX_SOURCES = [CSRC / "plan.cpp"]
 

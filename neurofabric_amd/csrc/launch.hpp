@@ -24,11 +24,9 @@ struct Workspace {
   uint32_t cnt_len = 0;
 };
 
-hipError_t launch_dequant(QFmt q, EType out_t, const void* w, void* out, uint64_t count,
+// Every block format; `in_bytes` (the input buffer size) bounds every read of `w`.
+hipError_t launch_dequant(QFmt q, EType out_t, const void* w, uint64_t in_bytes, void* out, uint64_t count,
                           hipStream_t s);
-// Q4_1, Q5_0, Q5_1, Q2_K .. Q6_K; `in_bytes` bounds every read of `w`.
-hipError_t launch_kquant_dequant(QFmt q, EType out_t, const void* w, uint64_t in_bytes, void* out,
-                                 uint64_t count, hipStream_t s);
 
 hipError_t launch_gemv(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                        uint32_t N, uint32_t K, hipStream_t s);

@@ -79,6 +79,11 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     lib.nf_hip_run_tasks.restype = C.c_int
     lib.nf_hip_buffer_device_ptr.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
     lib.nf_hip_buffer_device_ptr.restype = C.c_int
+    for fn in ("nf_hip_buffer_write", "nf_hip_buffer_read"):
+        getattr(lib, fn).argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64]
+        getattr(lib, fn).restype = C.c_int
+    lib.nf_hip_release_staging.argtypes = [C.c_void_p]
+    lib.nf_hip_release_staging.restype = None
     lib.nf_hip_enable_timing.argtypes = [C.c_bool]
     lib.nf_hip_enable_timing.restype = None
     lib.nf_hip_get_timing_count.argtypes = []
@@ -138,6 +143,21 @@ class Buffer:
             C.memmove(out.ctypes.data, ptr, out.nbytes)
         finally:
             self.unmap()
+        return out
+
+    def write(self, data, offset: int = 0) -> None:
+        """nf_hip_buffer_write: one copy from host memory into [offset, offset + nbytes)."""
+        raw = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+        self.prov.check(self.prov.lib.nf_hip_buffer_write(self.handle, offset, raw.ctypes.data, raw.nbytes),
+                        "buffer_write")
+
+    def read(self, dtype=np.uint8, count: int | None = None, offset: int = 0) -> np.ndarray:
+        """nf_hip_buffer_read of `count` elements of `dtype` from byte `offset`."""
+        dt = np.dtype(dtype)
+        n = (self.nbytes - offset) // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        self.prov.check(self.prov.lib.nf_hip_buffer_read(self.handle, offset, out.ctypes.data, out.nbytes),
+                        "buffer_read")
         return out
 
     def cache_sync(self, op: int = abi.NF_CACHE_INVALIDATE) -> None:
@@ -311,6 +331,9 @@ class Provider:
 
     def set_skinny_max_m(self, f16: int) -> None:
         self.lib.nf_hip_set_skinny_max_m(f16)
+
+    def release_staging(self) -> None:
+        self.lib.nf_hip_release_staging(self.handle)
 
     def launch_count(self) -> int:
         """Launches enqueued so far (a merged GEMV group counts once)."""
