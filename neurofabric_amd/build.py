@@ -37,8 +37,10 @@ HIP_SOURCES = [
     CSRC / "kernels" / "skinny.hip",
     CSRC / "kernels" / "generic.hip",
     CSRC / "kernels" / "dense.hip",
+    CSRC / "kernels" / "layer.hip",
+    CSRC / "kernels" / "attention.hip",
 ]
-CXX_SOURCES = [CSRC / "plan.cpp"]
+CXX_SOURCES = [CSRC / "plan.cpp", CSRC / "plan_layer.cpp"]
 
 COMMON_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-fvisibility=hidden",
                 f"-I{REPO / 'include'}", f"-I{CSRC}"]

@@ -1,0 +1,344 @@
+// layer.hip — the layer ops around the linears: element-wise add / mul,
+// silu, gelu, relu, the attention_prefill mock, rms_norm, rope, rope_batch,
+// softmax, embedding_lookup and argmax (metal_provider.mm:44-147, 1002-1150,
+// 1601-1619).  All are HBM- or latency-bound; fp32 arithmetic, f16 variants
+// read and write halves (selected by the output dtype, as the reference does).
+//
+// Numerics: add and mul are single IEEE operations (f16: computed in half
+// precision and rounded once, as half * half / half + half), so they match
+// the reference bit for bit.  The transcendental ops use the device's
+// accurate expf / tanhf / powf / sincosf / sqrt; row reductions (rms_norm's
+// sum of squares, softmax's sum) are tree sums in fp32 rather than the
+// reference's sequential loop, so those ops agree with it to rounding.
+#include "../launch.hpp"
+#include "common.hpp"
+
+namespace nfk {
+
+using EwFnK = nfhip::EwFn;
+
+namespace layer {
+
+constexpr int kThreads = 256;
+
+// ---- element-wise -----------------------------------------------------------
+
+template <EwFnK F>
+__device__ __forceinline__ float unary_f(float x) {
+  if constexpr (F == EwFnK::Silu) {
+    return x / (1.0f + expf(-x));
+  } else if constexpr (F == EwFnK::Gelu) {
+    const float x3 = x * x * x;
+    return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x3)));
+  } else {
+    return x > 0.0f ? x : 0.0f;
+  }
+}
+
+// 16-byte chunks (4 f32 / 8 f16) per thread when every pointer is 16-byte
+// aligned; otherwise one element per thread.
+template <typename T, EwFnK F, bool VEC>
+__global__ __launch_bounds__(kThreads) void binary_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                          T* __restrict__ out, uint64_t n) {
+  constexpr int V = VEC ? 16 / (int)sizeof(T) : 1;
+  const uint64_t i0 = ((uint64_t)blockIdx.x * kThreads + threadIdx.x) * V;
+  if (i0 >= n) return;
+  if (VEC && i0 + V <= n) {
+    typedef T vec_t __attribute__((ext_vector_type(V)));
+    const vec_t x = *reinterpret_cast<const vec_t*>(a + i0);
+    const vec_t y = *reinterpret_cast<const vec_t*>(b + i0);
+    *reinterpret_cast<vec_t*>(out + i0) = F == EwFnK::Add ? x + y : x * y;
+  } else {
+    for (uint64_t i = i0; i < n && i < i0 + V; ++i) out[i] = F == EwFnK::Add ? (T)(a[i] + b[i]) : (T)(a[i] * b[i]);
+  }
+}
+
+template <typename T, EwFnK F, bool VEC>
+__global__ __launch_bounds__(kThreads) void unary_kernel(const T* __restrict__ in, T* out, uint64_t n) {
+  constexpr int V = VEC ? 16 / (int)sizeof(T) : 1;
+  const uint64_t i0 = ((uint64_t)blockIdx.x * kThreads + threadIdx.x) * V;
+  if (i0 >= n) return;
+  if (VEC && i0 + V <= n) {
+    typedef T vec_t __attribute__((ext_vector_type(V)));
+    vec_t x = *reinterpret_cast<const vec_t*>(in + i0);
+#pragma unroll
+    for (int j = 0; j < V; ++j) x[j] = (T)unary_f<F>((float)x[j]);
+    *reinterpret_cast<vec_t*>(out + i0) = x;
+  } else {
+    for (uint64_t i = i0; i < n && i < i0 + V; ++i) out[i] = (T)unary_f<F>((float)in[i]);
+  }
+}
+
+// attention_prefill mock: k = x * 0.5, v = x * -0.25 (metal_provider.mm:56-66).
+__global__ __launch_bounds__(kThreads) void mock_prefill_kernel(const float* __restrict__ in, float* __restrict__ k,
+                                                                float* __restrict__ v, uint64_t nk, uint64_t nv) {
+  const uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < nk) k[i] = in[i] * 0.5f;
+  if (i < nv) v[i] = in[i] * -0.25f;
+}
+
+// ---- row reductions -----------------------------------------------------------
+
+// Sum over the workgroup (256 threads = 4 waves): wave sums by shuffle, then
+// the four wave sums in a fixed order.  Every thread gets the total.
+__device__ __forceinline__ float block_sum(float x, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
+__device__ __forceinline__ float block_max(float x, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  const float t = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return t;
+}
+
+// rms_norm: one workgroup per row of `dim` (metal_provider.mm:85-102, 1069-1084).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const T* __restrict__ in, const float* __restrict__ w,
+                                                            T* __restrict__ out, uint32_t dim, float eps) {
+  __shared__ float red[4];
+  const uint64_t base = (uint64_t)blockIdx.x * dim;
+  float ss = 0.0f;
+  for (uint32_t j = threadIdx.x; j < dim; j += kThreads) {
+    const float v = (float)in[base + j];
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float rms = 1.0f / sqrtf(ss / (float)dim + eps);
+  for (uint32_t j = threadIdx.x; j < dim; j += kThreads) out[base + j] = (T)((float)in[base + j] * rms * w[j]);
+}
+
+// softmax over rows of `dim` (metal_provider.mm:1002-1030).
+__global__ __launch_bounds__(kThreads) void softmax_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                           uint32_t dim) {
+  __shared__ float red[4];
+  const uint64_t base = (uint64_t)blockIdx.x * dim;
+  float m = -INFINITY;
+  for (uint32_t j = threadIdx.x; j < dim; j += kThreads) m = fmaxf(m, in[base + j]);
+  m = block_max(m, red);
+  float s = 0.0f;
+  for (uint32_t j = threadIdx.x; j < dim; j += kThreads) {
+    const float e = expf(in[base + j] - m);
+    out[base + j] = e;
+    s += e;
+  }
+  s = block_sum(s, red);
+  const float inv = 1.0f / s;
+  // each thread rescales exactly the elements it wrote, so no barrier is needed
+  for (uint32_t j = threadIdx.x; j < dim; j += kThreads) out[base + j] *= inv;
+}
+
+// argmax of each row (metal_provider.mm:1601-1619): the first index of the
+// largest non-NaN value, or 0 when the row starts with NaN (the reference's
+// strict `>` scan never leaves a NaN start).
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restrict__ in, int32_t* __restrict__ out,
+                                                          uint32_t dim) {
+  __shared__ float rv[4];
+  __shared__ uint32_t ri[4];
+  const uint64_t base = (uint64_t)blockIdx.x * dim;
+  constexpr uint32_t kNone = 0xFFFFFFFFu;
+  if (dim == 0) {  // no elements: the reference's scan returns its start, 0
+    if (threadIdx.x == 0) out[blockIdx.x] = 0;
+    return;
+  }
+  float best = -INFINITY;
+  uint32_t idx = kNone;
+  for (uint32_t j = threadIdx.x; j < dim; j += kThreads) {
+    const float x = in[base + j];
+    if (!isnan(x) && (idx == kNone || x > best)) {
+      best = x;
+      idx = j;
+    }
+  }
+  auto better = [](float b2, uint32_t i2, float b1, uint32_t i1) {
+    if (i2 == kNone) return false;
+    if (i1 == kNone) return true;
+    return b2 > b1 || (b2 == b1 && i2 < i1);
+  };
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float b2 = __shfl_xor(best, o);
+    const uint32_t i2 = __shfl_xor(idx, o);
+    if (better(b2, i2, best, idx)) {
+      best = b2;
+      idx = i2;
+    }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    rv[w] = best;
+    ri[w] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = rv[0];
+    uint32_t i = ri[0];
+    for (int k = 1; k < 4; ++k)
+      if (better(rv[k], ri[k], b, i)) {
+        b = rv[k];
+        i = ri[k];
+      }
+    out[blockIdx.x] = isnan(in[base]) ? 0 : (int32_t)i;
+  }
+}
+
+// ---- position encodings and lookups --------------------------------------------
+
+// RoPE on rows of head_dim: pairs (p, p + head_dim/2) rotated by pos * theta^(-2p/head_dim).
+// rope_batch: [seq, n_heads, head_dim], pos = token + step (metal_provider.mm:125-147);
+// rope: every row at pos = step (metal_provider.mm:104-122, with the rotation
+// the kernel intends for both halves of each row).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rope_kernel(const T* __restrict__ in, T* __restrict__ out, uint64_t n,
+                                                        uint32_t head_dim, uint32_t row_span, uint32_t step,
+                                                        float theta, bool batch) {
+  const uint64_t id = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (id >= n) return;
+  const uint32_t half = head_dim / 2;
+  const uint32_t e = (uint32_t)(id % head_dim);
+  const uint32_t pair = e % half;
+  const uint64_t pos = batch ? id / row_span + step : step;
+  const float freq = 1.0f / powf(theta, (float)(2 * pair) / (float)head_dim);
+  const float angle = (float)pos * freq;
+  float s, c;
+  sincosf(angle, &s, &c);
+  const uint64_t base = id - e;
+  const float x0 = (float)in[base + pair];
+  const float x1 = (float)in[base + pair + half];
+  out[id] = (T)(e < half ? x0 * c - x1 * s : x0 * s + x1 * c);
+}
+
+// embedding_lookup: out[t, :] = weights[ids[t], :] for t < seq_len; a token
+// id outside the table writes zeros (the reference reads out of bounds).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void embedding_kernel(const T* __restrict__ w, uint32_t vocab,
+                                                             const int32_t* __restrict__ ids, T* __restrict__ out,
+                                                             uint64_t n, uint32_t dim, uint32_t seq_len) {
+  const uint64_t id = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (id >= n) return;
+  const uint64_t t = id / dim;
+  if (t >= seq_len) return;
+  const int32_t tok = ids[t];
+  out[id] = (tok >= 0 && (uint32_t)tok < vocab) ? w[(uint64_t)tok * dim + id % dim] : (T)0.0f;
+}
+
+inline dim3 grid_for(uint64_t threads) { return dim3((unsigned)((threads + kThreads - 1) / kThreads)); }
+
+inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <typename T, EwFnK F>
+hipError_t binary_t(const void* a, const void* b, void* out, uint64_t n, hipStream_t s) {
+  constexpr int V = 16 / (int)sizeof(T);
+  if (a16(a) && a16(b) && a16(out))
+    binary_kernel<T, F, true><<<grid_for((n + V - 1) / V), kThreads, 0, s>>>((const T*)a, (const T*)b, (T*)out, n);
+  else
+    binary_kernel<T, F, false><<<grid_for(n), kThreads, 0, s>>>((const T*)a, (const T*)b, (T*)out, n);
+  return hipGetLastError();
+}
+
+template <typename T, EwFnK F>
+hipError_t unary_t(const void* in, void* out, uint64_t n, hipStream_t s) {
+  constexpr int V = 16 / (int)sizeof(T);
+  if (a16(in) && a16(out))
+    unary_kernel<T, F, true><<<grid_for((n + V - 1) / V), kThreads, 0, s>>>((const T*)in, (T*)out, n);
+  else
+    unary_kernel<T, F, false><<<grid_for(n), kThreads, 0, s>>>((const T*)in, (T*)out, n);
+  return hipGetLastError();
+}
+
+}  // namespace layer
+}  // namespace nfk
+
+namespace nfhip {
+
+using nfk::EwFnK;
+using nfk::half_t;
+
+
+hipError_t launch_binary(EwFn fn, EType t, const void* a, const void* b, void* out, uint64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  using namespace nfk::layer;
+  if (t == EType::F16)
+    return fn == EwFn::Add ? binary_t<half_t, EwFnK::Add>(a, b, out, n, s) : binary_t<half_t, EwFnK::Mul>(a, b, out, n, s);
+  return fn == EwFn::Add ? binary_t<float, EwFnK::Add>(a, b, out, n, s) : binary_t<float, EwFnK::Mul>(a, b, out, n, s);
+}
+
+hipError_t launch_unary(EwFn fn, EType t, const void* in, void* out, uint64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  using namespace nfk::layer;
+  if (fn == EwFn::Relu) return unary_t<float, EwFnK::Relu>(in, out, n, s);
+  if (t == EType::F16)
+    return fn == EwFn::Silu ? unary_t<half_t, EwFnK::Silu>(in, out, n, s) : unary_t<half_t, EwFnK::Gelu>(in, out, n, s);
+  return fn == EwFn::Silu ? unary_t<float, EwFnK::Silu>(in, out, n, s) : unary_t<float, EwFnK::Gelu>(in, out, n, s);
+}
+
+hipError_t launch_mock_prefill(const void* in, void* k, void* v, uint64_t nk, uint64_t nv, hipStream_t s) {
+  const uint64_t n = nk > nv ? nk : nv;
+  if (n == 0) return hipSuccess;
+  nfk::layer::mock_prefill_kernel<<<nfk::layer::grid_for(n), nfk::layer::kThreads, 0, s>>>(
+      (const float*)in, (float*)k, (float*)v, nk, nv);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(EType t, const void* in, const void* w, void* out, uint32_t rows, uint32_t dim, float eps,
+                           hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  using namespace nfk::layer;
+  if (t == EType::F16)
+    rms_norm_kernel<half_t><<<rows, kThreads, 0, s>>>((const half_t*)in, (const float*)w, (half_t*)out, dim, eps);
+  else
+    rms_norm_kernel<float><<<rows, kThreads, 0, s>>>((const float*)in, (const float*)w, (float*)out, dim, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope(EType t, bool batch, const void* in, void* out, uint64_t n, uint32_t n_heads,
+                       uint32_t head_dim, uint32_t step, float theta, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  using namespace nfk::layer;
+  const uint32_t span = batch ? n_heads * head_dim : head_dim;
+  if (t == EType::F16)
+    rope_kernel<half_t><<<grid_for(n), kThreads, 0, s>>>((const half_t*)in, (half_t*)out, n, head_dim, span, step,
+                                                         theta, batch);
+  else
+    rope_kernel<float><<<grid_for(n), kThreads, 0, s>>>((const float*)in, (float*)out, n, head_dim, span, step,
+                                                        theta, batch);
+  return hipGetLastError();
+}
+
+hipError_t launch_softmax(const void* in, void* out, uint32_t rows, uint32_t dim, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  nfk::layer::softmax_kernel<<<rows, nfk::layer::kThreads, 0, s>>>((const float*)in, (float*)out, dim);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax(const void* in, void* out, uint32_t rows, uint32_t dim, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  nfk::layer::argmax_kernel<<<rows, nfk::layer::kThreads, 0, s>>>((const float*)in, (int32_t*)out, dim);
+  return hipGetLastError();
+}
+
+hipError_t launch_embedding(EType t, const void* w, uint32_t vocab, const void* ids, void* out, uint64_t n,
+                            uint32_t dim, uint32_t seq_len, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  using namespace nfk::layer;
+  if (t == EType::F16)
+    embedding_kernel<half_t><<<grid_for(n), kThreads, 0, s>>>((const half_t*)w, vocab, (const int32_t*)ids,
+                                                              (half_t*)out, n, dim, seq_len);
+  else
+    embedding_kernel<float><<<grid_for(n), kThreads, 0, s>>>((const float*)w, vocab, (const int32_t*)ids,
+                                                             (float*)out, n, dim, seq_len);
+  return hipGetLastError();
+}
+
+}  // namespace nfhip

@@ -80,4 +80,32 @@ hipError_t launch_dense_mfma_f32(EType a, EType b, EType c, const void* A, const
 hipError_t launch_dense(EType a, EType b, EType c, const void* A, const void* B, void* C,
                         uint32_t M, uint32_t N, uint32_t K, const Workspace& ws, hipStream_t s);
 
+// ---- layer ops (kernels/layer.hip) -------------------------------------------
+hipError_t launch_binary(EwFn fn, EType t, const void* a, const void* b, void* out, uint64_t n, hipStream_t s);
+hipError_t launch_unary(EwFn fn, EType t, const void* in, void* out, uint64_t n, hipStream_t s);
+hipError_t launch_mock_prefill(const void* in, void* k, void* v, uint64_t nk, uint64_t nv, hipStream_t s);
+hipError_t launch_rms_norm(EType t, const void* in, const void* w, void* out, uint32_t rows, uint32_t dim, float eps,
+                           hipStream_t s);
+// batch: rope_batch ([seq, n_heads, head_dim], pos = token + step); else rope (pos = step).
+hipError_t launch_rope(EType t, bool batch, const void* in, void* out, uint64_t n, uint32_t n_heads,
+                       uint32_t head_dim, uint32_t step, float theta, hipStream_t s);
+hipError_t launch_softmax(const void* in, void* out, uint32_t rows, uint32_t dim, hipStream_t s);
+hipError_t launch_argmax(const void* in, void* out, uint32_t rows, uint32_t dim, hipStream_t s);
+hipError_t launch_embedding(EType t, const void* w, uint32_t vocab, const void* ids, void* out, uint64_t n,
+                            uint32_t dim, uint32_t seq_len, hipStream_t s);
+
+// ---- attention (kernels/attention.hip) ---------------------------------------
+struct AttnArgs {
+  const void* q = nullptr;
+  const void* k_new = nullptr;  // Cached / Gqa: rows appended to the cache first
+  const void* v_new = nullptr;
+  void* k = nullptr;  // Plain: K; Cached / Gqa: cache_k; Paged: K pool
+  void* v = nullptr;
+  const uint32_t* block_table = nullptr;  // Paged
+  void* out = nullptr;
+  LayerParams lp;
+  uint64_t pool_blocks = 0;  // Paged: whole blocks the pools hold
+};
+hipError_t launch_attention(EType t, const AttnArgs& a, hipStream_t s);
+
 }  // namespace nfhip

@@ -96,13 +96,21 @@ nf_status read_mnk(const uint8_t* pc, uint32_t pc_size, uint32_t* M, uint32_t* N
 }  // namespace
 
 bool op_known(const char* op_name) {
-  return op_name && op_table().count(op_name) != 0;
+  return op_name && (op_table().count(op_name) != 0 || layer_op_known(op_name));
+}
+
+bool op_reads_push_constants(const char* op_name) {
+  if (!op_name) return false;
+  auto it = op_table().find(op_name);
+  if (it != op_table().end()) return it->second.kind != OpKind::Dequant;
+  return layer_op_reads_push_constants(op_name);
 }
 
 nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint32_t n_in,
                     const nf_tensor_desc* const* outs, uint32_t n_out, const uint8_t* pc,
                     uint32_t pc_size, const Tuning& tuning, Plan* plan, std::string* why) {
   if (!op_name) return fail(why, "null op name");
+  if (layer_op_known(op_name)) return make_layer_plan(op_name, ins, n_in, outs, n_out, pc, pc_size, plan, why);
   auto it = op_table().find(op_name);
   if (it == op_table().end()) {
     if (why) *why = std::string("unsupported op '") + op_name + "'";

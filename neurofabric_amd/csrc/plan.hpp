@@ -13,7 +13,7 @@
 
 namespace nfhip {
 
-enum class OpKind { Dequant, FusedLinear, DenseLinear };
+enum class OpKind { Dequant, FusedLinear, DenseLinear, Layer };
 // Q4_0 and Q8_0 serve the fused linear kernels; every format serves the
 // standalone dequant ops.
 enum class QFmt { None, Q4_0, Q8_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K };
@@ -24,7 +24,47 @@ enum class Path {
   Skinny,    // small-batch MFMA kernel, gemv crossover < M <= skinny crossover
   GemmMfma,  // LDS-tiled MFMA kernel (prefill, f16), M > skinny crossover
   Generic,   // flat-index fallback for K % 32 != 0
-  Dense      // dense linear (weights already dequantized)
+  Dense,     // dense linear (weights already dequantized)
+  // the layer ops around the linears (plan_layer.cpp)
+  Binary,      // metal_vector_add, elementwise_mul
+  Unary,       // silu, gelu, mock_relu
+  MockPrefill, // attention_prefill (k = x/2, v = -x/4)
+  RmsNorm,
+  Rope,        // single-token rope
+  RopeBatch,
+  Softmax,
+  Embedding,
+  Argmax,
+  Attention    // every attention op (causal, cached, flash, gqa, paged)
+};
+
+// Element-wise functions of the Binary / Unary paths.
+enum class EwFn { Add, Mul, Silu, Gelu, Relu };
+
+// KV addressing and query layout of an attention op.
+enum class AttnMode {
+  Plain,   // causal_attention: Q, K, V, out [n_heads, seq_len, head_dim]
+  Cached,  // causal_attention_cached, flash_attention_cached: Q/out [seq, n_heads, dim],
+           // K_new/V_new [seq, n_kv, dim], cache [n_kv, max_seq, dim]
+  Gqa,     // flash_attention_gqa: Q/out [n_heads, seq, dim], K_new/V_new [n_kv, seq, dim]
+  Paged    // flash_attention_paged: pools [block][n_kv][block_size][dim] + block table
+};
+
+// Parameters of the layer ops, from the push constants
+// {seq_len@0, n_heads@4, head_dim@8, epsilon@12, theta@16, M@20, N@24, K@28,
+//  step_idx@32, max_seq_len@36, window_size@40} (metal_provider.mm:71-84).
+struct LayerParams {
+  EwFn fn = EwFn::Add;
+  AttnMode attn = AttnMode::Plain;
+  uint32_t rows = 0, dim = 0;  // rms_norm / softmax / argmax / embedding
+  uint32_t seq_len = 0, n_heads = 0, n_kv = 0, head_dim = 0;
+  uint32_t step = 0, max_seq = 0, window = 0;
+  uint32_t n_blocks = 0, block_size = 0, q_offset = 0;  // paged attention
+  uint64_t count2 = 0;  // attention_prefill: elements of the second output
+  float eps = 0.f, theta = 0.f;
+  bool decode = false;  // attention with step_idx > 0 (one query token)
+  bool append = false;  // attention op that first writes K_new / V_new into the cache
+  bool noop = false;    // nothing to launch (decode at step >= max_seq_len, as the reference)
 };
 
 // Switch points between the kernel families of the fused op: the VALU GEMV
@@ -59,6 +99,8 @@ struct Plan {
   uint64_t in_bytes = 0;  // dequant: size of the quantized input buffer
   uint64_t weight_bytes = 0, act_bytes = 0, out_bytes = 0, flops = 0;
   std::string kernel;
+  LayerParams lp;
+  uint32_t writes_inputs = 0;  // bit i: the op writes input i (KV cache append, in-place relu)
 };
 
 // Bytes and elements of one block (gguf_loader.hpp:64-74): Q4_0 = 2 (fp16
@@ -97,5 +139,16 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
 
 // True when `op_name` is served by this provider.
 bool op_known(const char* op_name);
+
+// True when the op reads the task descriptor's push constants.
+bool op_reads_push_constants(const char* op_name);
+
+// The layer ops (plan_layer.cpp).  `pc` is the whole push-constant block
+// (fields past pc_size read as zero).
+bool layer_op_known(const char* op_name);
+bool layer_op_reads_push_constants(const char* op_name);
+nf_status make_layer_plan(const char* op_name, const nf_tensor_desc* const* ins, uint32_t n_in,
+                          const nf_tensor_desc* const* outs, uint32_t n_out, const uint8_t* pc,
+                          uint32_t pc_size, Plan* plan, std::string* why);
 
 }  // namespace nfhip

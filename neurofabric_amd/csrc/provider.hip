@@ -459,9 +459,7 @@ void hip_buffer_free(nf_provider, nf_buffer buf) {
 nf_status hip_buffer_map(nf_provider, nf_buffer buf, void** out) { return buf_map(buf, out); }
 nf_status hip_buffer_unmap(nf_provider, nf_buffer buf) { return buf_unmap(buf); }
 
-bool reads_push_constants(const char* op) {
-  return std::strstr(op, "linear") != nullptr;
-}
+bool reads_push_constants(const char* op) { return op_reads_push_constants(op); }
 
 // The engine passes &task_desc.inputs[0]; step back to the descriptor to
 // read its push constants (metal_provider.mm:2301-2307).
@@ -500,6 +498,46 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, int g
       return launch_generic(pl.q, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, s);
     case Path::Dense:
       return launch_dense(pl.a, pl.b, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.M, pl.N, pl.K, ws, s);
+    case Path::Binary:
+      return launch_binary(pl.lp.fn, pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.count, s);
+    case Path::Unary:  // mock_relu without an output runs in place
+      return launch_unary(pl.lp.fn, pl.c, in[0]->dev, (pl.writes_inputs & 1u) ? in[0]->dev : out[0]->dev, pl.count, s);
+    case Path::MockPrefill:
+      return launch_mock_prefill(in[0]->dev, out[0]->dev, out[1]->dev, pl.count, pl.lp.count2, s);
+    case Path::RmsNorm:
+      return launch_rms_norm(pl.c, in[0]->dev, in[1]->dev, out[0]->dev, pl.lp.rows, pl.lp.dim, pl.lp.eps, s);
+    case Path::Rope:
+    case Path::RopeBatch:
+      return launch_rope(pl.c, pl.path == Path::RopeBatch, in[0]->dev, out[0]->dev, pl.count, pl.lp.n_heads,
+                         pl.lp.head_dim, pl.lp.step, pl.lp.theta, s);
+    case Path::Softmax:
+      return launch_softmax(in[0]->dev, out[0]->dev, pl.lp.rows, pl.lp.dim, s);
+    case Path::Embedding:
+      return launch_embedding(pl.c, in[0]->dev, pl.lp.rows, in[1]->dev, out[0]->dev, pl.count, pl.lp.dim,
+                              pl.lp.seq_len, s);
+    case Path::Argmax:
+      return launch_argmax(in[0]->dev, out[0]->dev, pl.lp.rows, pl.lp.dim, s);
+    case Path::Attention: {
+      AttnArgs a;
+      a.q = in[0]->dev;
+      a.lp = pl.lp;
+      a.out = out[0]->dev;
+      if (pl.lp.attn == AttnMode::Plain) {
+        a.k = in[1]->dev;
+        a.v = in[2]->dev;
+      } else if (pl.lp.attn == AttnMode::Paged) {
+        a.k = in[1]->dev;
+        a.v = in[2]->dev;
+        a.block_table = static_cast<const uint32_t*>(in[3]->dev);
+        a.pool_blocks = pl.lp.count2;
+      } else {
+        a.k_new = in[1]->dev;
+        a.v_new = in[2]->dev;
+        a.k = in[3]->dev;
+        a.v = in[4]->dev;
+      }
+      return launch_attention(pl.c, a, s);
+    }
   }
   return hipErrorInvalidValue;
 }
@@ -550,6 +588,9 @@ nf_status prepare(Provider* p, const char* op_name, const nf_buffer* inputs, uin
     const nf_task_desc* td = enclosing_task(inputs);
     pc_size = td->push_constants_size;
     pc = td->push_constants;
+    // The reference binds the descriptor's whole 64-byte block whenever its
+    // size is non-zero (metal_provider.mm:2460), so layer ops read every field.
+    if (pc_size > 0 && layer_op_known(op_name)) pc_size = NF_MAX_PUSH_CONSTANTS;
   }
   std::string why;
   nf_status st = make_plan(op_name, in_d, n_in, out_d, n_out, pc, pc_size, p->tuning, &pr->pl, &why);
@@ -571,8 +612,10 @@ nf_status launch(Provider* p, const Prepared* prs, uint32_t n) {
       rec = &p->ring[p->timing_head.fetch_add(1, std::memory_order_relaxed) % kTimingRing];
       std::strncpy(rec->op, prs[0].op, 63);
       rec->op[63] = '\0';
-      rec->dtype = (uint8_t)prs[0].out[0]->desc.dtype;
-      rec->elems = (uint32_t)(prs[0].pl.path == Path::Dequant ? prs[0].pl.count : (uint64_t)prs[0].pl.M * prs[0].pl.N);
+      rec->dtype = (uint8_t)(prs[0].n_out ? prs[0].out[0] : prs[0].in[0])->desc.dtype;
+      const Plan& rp = prs[0].pl;
+      rec->elems = (uint32_t)((rp.op == OpKind::FusedLinear || rp.op == OpKind::DenseLinear) ? (uint64_t)rp.M * rp.N
+                                                                                              : rp.count);
       (void)hipEventRecord(rec->start, p->stream);
     }
     p->launch_groups.fetch_add(1, std::memory_order_relaxed);
@@ -596,15 +639,23 @@ nf_status launch(Provider* p, const Prepared* prs, uint32_t n) {
     for (uint32_t j = 0; j < n; ++j) {
       const uint64_t seq = ++p->issued_seq;
       for (uint32_t i = 0; i < prs[j].n_out; ++i) prs[j].out[i]->last_write_seq.store(seq);
+      for (uint32_t i = 0; i < prs[j].n_in; ++i)
+        if (prs[j].pl.writes_inputs & (1u << i)) prs[j].in[i]->last_write_seq.store(seq);
     }
   }
   // Buffer flags are updated outside the provider lock (map takes the
   // buffer lock first, then the provider lock).
-  for (uint32_t j = 0; j < n; ++j)
+  for (uint32_t j = 0; j < n; ++j) {
     for (uint32_t i = 0; i < prs[j].n_out; ++i) {
       std::lock_guard<std::mutex> bl(prs[j].out[i]->mu);
       prs[j].out[i]->host_valid = false;
     }
+    for (uint32_t i = 0; i < prs[j].n_in; ++i)
+      if (prs[j].pl.writes_inputs & (1u << i)) {
+        std::lock_guard<std::mutex> bl(prs[j].in[i]->mu);
+        prs[j].in[i]->host_valid = false;
+      }
+  }
   if (e != hipSuccess) return map_hip(e, (std::string("launch ") + prs[0].pl.kernel).c_str());
   return NF_OK;
 }

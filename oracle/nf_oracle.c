@@ -8,6 +8,7 @@
  */
 #include "nf_oracle.h"
 
+#include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
@@ -405,4 +406,271 @@ void nf_oracle_fused_f32(const float *A, const uint8_t *W, int qfmt, float *C, u
 void nf_oracle_fused_f16(const uint16_t *A, const uint8_t *W, int qfmt, uint16_t *C, uint32_t M,
                          uint32_t N, uint32_t K, uint32_t n0, uint32_t n1, uint32_t threads) {
     fused_run(A, W, qfmt, 1, C, M, N, K, n0, n1, threads);
+}
+
+/* ---- layer ops around the linears ---------------------------------------- */
+/*
+ * Each loop below follows the reference kernel's per-thread code
+ * (plugins/metal/src/metal_provider.mm) in fp32, with libm's expf / tanhf /
+ * powf / cosf / sinf / sqrtf for Metal's exp / tanh / pow / cos / sin / rsqrt.
+ * f16 inputs and outputs are fp16 bits (uint16), converted exactly on load
+ * and rounded to nearest even on store.
+ */
+
+static inline float ld_t(const void *p, uint64_t i, int f16) {
+    return f16 ? nf_oracle_f16_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+}
+
+static inline void st_t(void *p, uint64_t i, float v, int f16) {
+    if (f16)
+        ((uint16_t *)p)[i] = nf_oracle_f32_to_f16_rne(v);
+    else
+        ((float *)p)[i] = v;
+}
+
+/* silu :1032-1037 (f16 :1108-1113), gelu :1039-1045 (:1115-1121), relu :51-54 */
+void nf_oracle_unary(int fn, const void *in, void *out, uint64_t n, int f16) {
+    for (uint64_t i = 0; i < n; ++i) {
+        const float x = ld_t(in, i, f16);
+        float y;
+        if (fn == 0) {
+            y = x / (1.0f + expf(-x));
+        } else if (fn == 1) {
+            const float x3 = x * x * x;
+            y = 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x3)));
+        } else {
+            y = x > 0.0f ? x : 0.0f;
+        }
+        st_t(out, i, y, f16);
+    }
+}
+
+/* metal_vector_add / elementwise_mul :44-49, 1047-1052 (f16 :1123-1135: the
+ * product / sum of two halves rounded once to half). */
+void nf_oracle_binary(int fn, const void *a, const void *b, void *out, uint64_t n, int f16) {
+    for (uint64_t i = 0; i < n; ++i) {
+        const float x = ld_t(a, i, f16), y = ld_t(b, i, f16);
+        /* for halves, x*y and x+y in fp32 round to the same half as a native
+         * half operation: the fp32 result is exact (product) or rounds far
+         * below half precision without creating a tie (sum) */
+        st_t(out, i, fn == 0 ? x + y : x * y, f16);
+    }
+}
+
+/* rms_norm :85-102 (f16 :1069-1084, weights f32) */
+void nf_oracle_rms_norm(const void *in, const float *w, void *out, uint32_t rows, uint32_t dim, float eps,
+                        int f16) {
+    for (uint32_t r = 0; r < rows; ++r) {
+        const uint64_t base = (uint64_t)r * dim;
+        float sum_sq = 0.0f;
+        for (uint32_t j = 0; j < dim; ++j) {
+            const float v = ld_t(in, base + j, f16);
+            sum_sq += v * v;
+        }
+        const float rms = 1.0f / sqrtf(sum_sq / (float)dim + eps);
+        for (uint32_t j = 0; j < dim; ++j) st_t(out, base + j, ld_t(in, base + j, f16) * rms * w[j], f16);
+    }
+}
+
+/* rope_batch :125-147 (f16 :1086-1106); rope :104-122 with pos = step for
+ * every row (batch = 0).  row_span = n_heads * head_dim for rope_batch. */
+void nf_oracle_rope(const void *in, void *out, uint64_t n, uint32_t n_heads, uint32_t head_dim, uint32_t step,
+                    float theta, int batch, int f16) {
+    const uint32_t half = head_dim / 2;
+    const uint64_t span = batch ? (uint64_t)n_heads * head_dim : head_dim;
+    for (uint64_t id = 0; id < n; ++id) {
+        const uint32_t e = (uint32_t)(id % head_dim);
+        const uint32_t pair = e % half;
+        const uint64_t pos = batch ? id / span + step : step;
+        const float freq = 1.0f / powf(theta, (float)(2 * pair) / (float)head_dim);
+        const float angle = (float)pos * freq;
+        const float c = cosf(angle), sn = sinf(angle);
+        const uint64_t base = id - e;
+        const float x0 = ld_t(in, base + pair, f16), x1 = ld_t(in, base + pair + half, f16);
+        st_t(out, id, e < half ? x0 * c - x1 * sn : x0 * sn + x1 * c, f16);
+    }
+}
+
+/* softmax :1002-1030 */
+void nf_oracle_softmax(const float *in, float *out, uint32_t rows, uint32_t dim) {
+    for (uint32_t r = 0; r < rows; ++r) {
+        const uint64_t base = (uint64_t)r * dim;
+        float mx = in[base];
+        for (uint32_t j = 1; j < dim; ++j)
+            if (in[base + j] > mx) mx = in[base + j];
+        float sum = 0.0f;
+        for (uint32_t j = 0; j < dim; ++j) {
+            const float e = expf(in[base + j] - mx);
+            out[base + j] = e;
+            sum += e;
+        }
+        const float inv = 1.0f / sum;
+        for (uint32_t j = 0; j < dim; ++j) out[base + j] *= inv;
+    }
+}
+
+/* argmax_rows :1601-1619 */
+void nf_oracle_argmax(const float *in, int32_t *out, uint32_t rows, uint32_t dim) {
+    for (uint32_t r = 0; r < rows; ++r) {
+        const uint64_t base = (uint64_t)r * dim;
+        if (dim == 0) { /* the kernel's start value, never replaced */
+            out[r] = 0;
+            continue;
+        }
+        float best = in[base];
+        int32_t idx = 0;
+        for (uint32_t j = 1; j < dim; ++j)
+            if (in[base + j] > best) {
+                best = in[base + j];
+                idx = (int32_t)j;
+            }
+        out[r] = idx;
+    }
+}
+
+/* embedding_lookup :1054-1067 (f16 :1137-1150); a token outside the table's
+ * `vocab` rows yields zeros (the reference reads out of bounds there). */
+void nf_oracle_embedding(const void *w, uint32_t vocab, const int32_t *ids, void *out, uint64_t n, uint32_t dim,
+                         uint32_t seq_len, int f16) {
+    for (uint64_t id = 0; id < n; ++id) {
+        const uint64_t t = id / dim;
+        if (t >= seq_len) continue;
+        const int32_t tok = ids[t];
+        float v = 0.0f;
+        if (tok >= 0 && (uint32_t)tok < vocab) v = ld_t(w, (uint64_t)tok * dim + id % dim, f16);
+        st_t(out, id, v, f16);
+    }
+}
+
+/* ---- attention ----------------------------------------------------------------
+ * prm[] = {mode, variant, n_heads, n_kv, head_dim, seq_len, step, max_seq,
+ *          window, block_size, n_blocks, q_offset, pool_blocks}
+ * mode:    0 causal_attention [heads, seq, dim]            (:166-213)
+ *          1 cached: Q/out [seq, heads, dim], cache [kv, max_seq, dim] (:217-341, 344-497)
+ *          2 gqa: Q/out [heads, seq, dim]                   (:1715-1806)
+ *          3 paged: pools [block][kv][bs][dim] + table       (:1622-1712)
+ * variant: 0 two-pass (causal_attention, causal_attention_cached)
+ *          1 32-key tiles, online (flash_attention_cached / _f16)
+ *          2 per-key online (flash_attention_gqa)
+ *          3 per-block online (flash_attention_paged)
+ * The cached modes append K_new / V_new to the caches first (all appended
+ * rows are visible to every query, the intent of the reference kernels).
+ * A paged block index at or past pool_blocks is skipped. */
+
+#define NF_NEG_INF (-1e30f)
+
+static inline uint64_t attn_q_row(const uint32_t *P, uint32_t q, uint32_t h) {
+    const uint32_t mode = P[0], H = P[2], D = P[4], S = P[5], step = P[6];
+    if (mode == 0) return ((uint64_t)h * S + q) * D;
+    if (mode == 1) return step ? (uint64_t)h * D : ((uint64_t)q * H + h) * D;
+    if (mode == 2) return step ? (uint64_t)h * D : ((uint64_t)h * S + q) * D;
+    return ((uint64_t)(P[11] + q) * H + h) * D;
+}
+
+static inline int64_t attn_kv_row(const uint32_t *P, const uint32_t *table, uint32_t kvh, uint32_t pos) {
+    const uint32_t mode = P[0], KV = P[3], D = P[4], S = P[5], max_seq = P[7], bs = P[9];
+    if (mode == 0) return (int64_t)(((uint64_t)kvh * S + pos) * D);
+    if (mode == 1 || mode == 2) return (int64_t)(((uint64_t)kvh * max_seq + pos) * D);
+    const uint32_t phys = table[pos / bs];
+    if (phys >= P[12]) return -1;
+    return (int64_t)((((uint64_t)phys * KV + kvh) * bs + pos % bs) * D);
+}
+
+static float attn_dot(const void *Q, uint64_t qrow, const void *K, int64_t krow, uint32_t D, int f16) {
+    float dot = 0.0f;
+    for (uint32_t d = 0; d < D; ++d) dot += ld_t(Q, qrow + d, f16) * ld_t(K, (uint64_t)krow + d, f16);
+    return dot;
+}
+
+void nf_oracle_attention(const uint32_t *P, int f16, const void *Q, const void *K_new, const void *V_new, void *K,
+                         void *V, const uint32_t *table, void *out) {
+    const uint32_t mode = P[0], variant = P[1], H = P[2], KV = P[3], D = P[4], S = P[5], step = P[6];
+    const uint32_t max_seq = P[7], window = P[8], bs = P[9], n_blocks = P[10];
+    const int decode = mode != 0 && step > 0;
+    if (mode == 1 || mode == 2) {
+        if (decode && step >= max_seq) return;
+        const uint32_t tokens = decode ? 1 : S, first = decode ? step : 0;
+        for (uint32_t kvh = 0; kvh < KV; ++kvh)
+            for (uint32_t t = 0; t < tokens; ++t)
+                for (uint32_t d = 0; d < D; ++d) {
+                    const uint64_t src = mode == 1 ? ((uint64_t)t * KV + kvh) * D + d : ((uint64_t)kvh * tokens + t) * D + d;
+                    const uint64_t dst = ((uint64_t)kvh * max_seq + first + t) * D + d;
+                    st_t(K, dst, ld_t(K_new, src, f16), f16);
+                    st_t(V, dst, ld_t(V_new, src, f16), f16);
+                }
+    }
+    const float scale = 1.0f / sqrtf((float)D);
+    const uint32_t nq = decode ? 1 : S;
+    float *acc = (float *)malloc(sizeof(float) * D);
+    for (uint32_t q = 0; q < nq; ++q)
+        for (uint32_t h = 0; h < H; ++h) {
+            const uint32_t kvh = (uint32_t)((uint64_t)h * KV / H);
+            const uint32_t pos = decode ? step : q;
+            uint32_t lo = 0;
+            if (mode == 1 && window > 0 && pos >= window) lo = pos - window + 1;
+            int64_t hi = pos;
+            if (mode == 3) {
+                const int64_t cap = (int64_t)n_blocks * bs - 1;
+                if (hi > cap) hi = cap;
+            }
+            const uint64_t qrow = attn_q_row(P, q, h);
+            for (uint32_t d = 0; d < D; ++d) acc[d] = 0.0f;
+            float res_scale;
+            if (variant == 0) {
+                float mx = NF_NEG_INF;
+                for (int64_t k = lo; k <= hi; ++k) {
+                    const float dot = attn_dot(Q, qrow, K, attn_kv_row(P, table, kvh, (uint32_t)k), D, f16) * scale;
+                    if (dot > mx) mx = dot;
+                }
+                float sum = 0.0f;
+                for (int64_t k = lo; k <= hi; ++k)
+                    sum += expf(attn_dot(Q, qrow, K, attn_kv_row(P, table, kvh, (uint32_t)k), D, f16) * scale - mx);
+                for (int64_t k = lo; k <= hi; ++k) {
+                    const int64_t row = attn_kv_row(P, table, kvh, (uint32_t)k);
+                    const float w = expf(attn_dot(Q, qrow, K, row, D, f16) * scale - mx) / sum;
+                    for (uint32_t d = 0; d < D; ++d) acc[d] += w * ld_t(V, (uint64_t)row + d, f16);
+                }
+                res_scale = 1.0f;
+            } else {
+                float m = NF_NEG_INF, l = 0.0f;
+                const uint32_t tile = variant == 1 ? 32u : variant == 2 ? 1u : bs;
+                /* paged tiles are the logical blocks, aligned at 0 */
+                for (int64_t t0 = lo; t0 <= hi; t0 += tile) {
+                    int64_t t1 = t0 + tile - 1;
+                    if (t1 > hi) t1 = hi;
+                    float tmax = NF_NEG_INF;
+                    int any = 0;
+                    for (int64_t k = t0; k <= t1; ++k) {
+                        const int64_t row = attn_kv_row(P, table, kvh, (uint32_t)k);
+                        if (row < 0) continue;
+                        any = 1;
+                        const float dot = attn_dot(Q, qrow, K, row, D, f16) * scale;
+                        if (dot > tmax) tmax = dot;
+                    }
+                    if (!any) continue;
+                    const float m_new = m > tmax ? m : tmax;
+                    const float corr = expf(m - m_new);
+                    if (variant == 2) {
+                        const int64_t row = attn_kv_row(P, table, kvh, (uint32_t)t0);
+                        const float e = expf(tmax - m_new);
+                        l = l * corr + e;
+                        for (uint32_t d = 0; d < D; ++d) acc[d] = acc[d] * corr + e * ld_t(V, (uint64_t)row + d, f16);
+                    } else {
+                        for (uint32_t d = 0; d < D; ++d) acc[d] *= corr;
+                        l *= corr;
+                        for (int64_t k = t0; k <= t1; ++k) {
+                            const int64_t row = attn_kv_row(P, table, kvh, (uint32_t)k);
+                            if (row < 0) continue;
+                            const float w = expf(attn_dot(Q, qrow, K, row, D, f16) * scale - m_new);
+                            l += w;
+                            for (uint32_t d = 0; d < D; ++d) acc[d] += w * ld_t(V, (uint64_t)row + d, f16);
+                        }
+                    }
+                    m = m_new;
+                }
+                res_scale = l > 0.0f ? 1.0f / l : 0.0f;
+            }
+            for (uint32_t d = 0; d < D; ++d) st_t(out, qrow + d, acc[d] * res_scale, f16);
+        }
+    free(acc);
 }

@@ -25,6 +25,10 @@
  *                             the same f32 value (metal_provider.mm:761-900),
  *                             except q3_k_f16, whose kernel reads raw bytes
  *                             as scales (metal_provider.mm:833-848)
+ *   nf_oracle_unary/binary/rms_norm/rope/softmax/argmax/embedding/attention
+ *                             the layer-op kernels, metal_provider.mm:44-497,
+ *                             1002-1150, 1273-1394, 1601-1906, in their loop
+ *                             order (pins: tests/test_oracle_layer.py)
  *   nf_oracle_linear_*        naive sequential-k loop, dequant_test.cpp:313-319,
  *                             with B stored [N,K] (dequant_test.cpp:321-325)
  *   nf_oracle_fused_*         dequant_q4_0_linear_tiled[_f16] semantics,
@@ -71,6 +75,24 @@ int nf_oracle_dequant(int fmt, const uint8_t *blocks, uint64_t in_bytes, uint64_
                       void *out);
 uint32_t nf_oracle_block_bytes(int fmt);
 uint32_t nf_oracle_block_elems(int fmt);
+
+/* Layer ops around the linears (metal_provider.mm line ranges in
+ * nf_oracle.c).  f16 = 1: inputs and outputs are fp16 bits.
+ * unary fn: 0 silu, 1 gelu, 2 relu; binary fn: 0 add, 1 mul. */
+void nf_oracle_unary(int fn, const void *in, void *out, uint64_t n, int f16);
+void nf_oracle_binary(int fn, const void *a, const void *b, void *out, uint64_t n, int f16);
+void nf_oracle_rms_norm(const void *in, const float *w, void *out, uint32_t rows, uint32_t dim, float eps,
+                        int f16);
+void nf_oracle_rope(const void *in, void *out, uint64_t n, uint32_t n_heads, uint32_t head_dim, uint32_t step,
+                    float theta, int batch, int f16);
+void nf_oracle_softmax(const float *in, float *out, uint32_t rows, uint32_t dim);
+void nf_oracle_argmax(const float *in, int32_t *out, uint32_t rows, uint32_t dim);
+void nf_oracle_embedding(const void *w, uint32_t vocab, const int32_t *ids, void *out, uint64_t n, uint32_t dim,
+                         uint32_t seq_len, int f16);
+/* prm = {mode, variant, n_heads, n_kv, head_dim, seq_len, step, max_seq,
+ * window, block_size, n_blocks, q_offset, pool_blocks}; see nf_oracle.c. */
+void nf_oracle_attention(const uint32_t *prm, int f16, const void *Q, const void *K_new, const void *V_new,
+                         void *K, void *V, const uint32_t *table, void *out);
 
 /* C[M,N] = A[M,K] * B[N,K]^T, fp32 accumulation in k order. */
 void nf_oracle_linear_f32(const float *A, const float *B, float *C,

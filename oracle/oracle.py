@@ -171,3 +171,110 @@ def available() -> bool:
 
 __all__ = ["build", "lib", "f16_to_f32", "f32_to_f16_rne", "f32_to_f16_trunc", "dequant",
            "linear_f32", "linear_f16", "fused", "Q4_0", "Q8_0", "available"]
+
+
+# ---- layer ops --------------------------------------------------------------
+
+UNARY = {"silu": 0, "gelu": 1, "relu": 2}
+BINARY = {"add": 0, "mul": 1}
+ATTN_MODE = {"plain": 0, "cached": 1, "gqa": 2, "paged": 3}
+# softmax arithmetic of each reference attention op
+ATTN_VARIANT = {"causal_attention": (0, 0), "causal_attention_cached": (1, 0), "flash_attention_cached": (1, 1),
+                "flash_attention_gqa": (2, 2), "flash_attention_paged": (3, 3)}
+
+
+def _layer_lib():
+    L = lib()
+    if not getattr(L, "_layer_ready", False):
+        vp, u32, u64, f32, i = C.c_void_p, C.c_uint32, C.c_uint64, C.c_float, C.c_int
+        L.nf_oracle_unary.argtypes = [i, vp, vp, u64, i]
+        L.nf_oracle_binary.argtypes = [i, vp, vp, vp, u64, i]
+        L.nf_oracle_rms_norm.argtypes = [vp, vp, vp, u32, u32, f32, i]
+        L.nf_oracle_rope.argtypes = [vp, vp, u64, u32, u32, u32, f32, i, i]
+        L.nf_oracle_softmax.argtypes = [vp, vp, u32, u32]
+        L.nf_oracle_argmax.argtypes = [vp, vp, u32, u32]
+        L.nf_oracle_embedding.argtypes = [vp, u32, vp, vp, u64, u32, u32, i]
+        L.nf_oracle_attention.argtypes = [vp, i, vp, vp, vp, vp, vp, vp, vp]
+        L._layer_ready = True
+    return L
+
+
+def _arr(x, f16):
+    """float32 array, or fp16 bits (uint16) when f16."""
+    return np.ascontiguousarray(x, np.uint16 if f16 else np.float32).reshape(-1)
+
+
+def unary(fn: str, x, f16: bool = False) -> np.ndarray:
+    a = _arr(x, f16)
+    out = np.empty_like(a)
+    _layer_lib().nf_oracle_unary(UNARY[fn], a.ctypes.data, out.ctypes.data, a.size, int(f16))
+    return out
+
+
+def binary(fn: str, a, b, f16: bool = False) -> np.ndarray:
+    a, b = _arr(a, f16), _arr(b, f16)
+    out = np.empty_like(a)
+    _layer_lib().nf_oracle_binary(BINARY[fn], a.ctypes.data, b.ctypes.data, out.ctypes.data, a.size, int(f16))
+    return out
+
+
+def rms_norm(x, w, dim: int, eps: float, f16: bool = False) -> np.ndarray:
+    a = _arr(x, f16)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(a)
+    _layer_lib().nf_oracle_rms_norm(a.ctypes.data, w.ctypes.data, out.ctypes.data, a.size // dim, dim, eps, int(f16))
+    return out
+
+
+def rope(x, n_heads: int, head_dim: int, step: int, theta: float, batch: bool = True, f16: bool = False):
+    a = _arr(x, f16)
+    out = np.empty_like(a)
+    _layer_lib().nf_oracle_rope(a.ctypes.data, out.ctypes.data, a.size, n_heads, head_dim, step, theta, int(batch),
+                                int(f16))
+    return out
+
+
+def softmax(x, rows: int, dim: int) -> np.ndarray:
+    a = _arr(x, False)
+    out = np.empty(rows * dim, np.float32)
+    _layer_lib().nf_oracle_softmax(a.ctypes.data, out.ctypes.data, rows, dim)
+    return out
+
+
+def argmax(x, rows: int, dim: int) -> np.ndarray:
+    a = _arr(x, False)
+    out = np.empty(rows, np.int32)
+    _layer_lib().nf_oracle_argmax(a.ctypes.data, out.ctypes.data, rows, dim)
+    return out
+
+
+def embedding(w, ids, n: int, dim: int, seq_len: int, f16: bool = False, out=None) -> np.ndarray:
+    wa = _arr(w, f16)
+    ids = np.ascontiguousarray(ids, np.int32)
+    if out is None:
+        out = np.zeros(n, np.uint16 if f16 else np.float32)
+    _layer_lib().nf_oracle_embedding(wa.ctypes.data, wa.size // dim, ids.ctypes.data, out.ctypes.data, n, dim,
+                                     seq_len, int(f16))
+    return out
+
+
+def attention(op: str, prm: dict, q, k_new=None, v_new=None, k=None, v=None, table=None, out=None,
+              f16: bool = False):
+    """The attention op `op` with the reference's softmax arithmetic.  prm
+    keys: n_heads, n_kv, head_dim, seq_len, step, max_seq, window,
+    block_size, n_blocks, q_offset, pool_blocks.  k / v are the caches
+    (modified in place for the cached ops), K / V for causal_attention, the
+    pools for paged.  Returns `out`."""
+    mode, variant = ATTN_VARIANT[op]
+    P = np.array([mode, variant] + [int(prm.get(key, 0)) for key in
+                 ("n_heads", "n_kv", "head_dim", "seq_len", "step", "max_seq", "window", "block_size",
+                  "n_blocks", "q_offset", "pool_blocks")], np.uint32)
+    q = _arr(q, f16)
+    bufs = [None if b is None else _arr(b, f16) for b in (k_new, v_new)]
+    assert k.dtype == (np.uint16 if f16 else np.float32) and v.dtype == k.dtype and k.flags.c_contiguous
+    tb = None if table is None else np.ascontiguousarray(table, np.uint32)
+    assert out is not None and out.flags.c_contiguous
+    ptr = lambda a: None if a is None else a.ctypes.data  # noqa: E731
+    _layer_lib().nf_oracle_attention(P.ctypes.data, int(f16), q.ctypes.data, ptr(bufs[0]), ptr(bufs[1]),
+                                     k.ctypes.data, v.ctypes.data, ptr(tb), out.ctypes.data)
+    return out

@@ -35,6 +35,30 @@ def test_reference_kquant_dequant_test_binary_passes():
     assert "OK: all Phase 25 K-quant dequant tests passed" in r.stdout
 
 
+# The reference's other driver tests this provider serves, with the line each
+# prints when every check passed (tests/driver/<name>.cpp).
+REF_LAYER_TESTS = {
+    "transformer_test": "=== ALL PASSED ===",          # softmax, silu, mul, embedding, argmax,
+                                                        # causal_attention[_cached], single layer
+    "gqa_attention_test": "=== All GQA attention tests passed ===",
+    "paged_attn_test": "All 3 paged_attn tests passed.",
+    "fp16_kernel_test": "All 7 tests PASSED",
+    "dag_inference_test": "=== ALL PASSED ===",         # 2-layer model through PipelineEngine
+    "multi_layer_test": "=== ALL PASSED ===",
+}
+
+
+@pytest.mark.parametrize("name", sorted(REF_LAYER_TESTS))
+def test_reference_layer_test_binaries_pass(name):
+    exe = REPO / "oracle" / "_ref" / name
+    if not exe.exists():
+        pytest.skip("reference test binary not built (needs the reference sources)")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-4000:], r.stderr[-2000:])
+    assert r.returncode == 0
+    assert REF_LAYER_TESTS[name] in r.stdout
+
+
 LIFECYCLE = r"""
 import sys
 sys.path.insert(0, %r)

@@ -196,6 +196,29 @@ def test_plan_kquant_dequant_ops(lib, fmt, f16):
     assert err.value.status == abi.NF_ERROR_INVALID_ARG
 
 
+def test_plan_layer_ops(lib):
+    """The layer ops of metal_provider.mm:3180-3204: f16 variant from the
+    output dtype, counts from the output size or the push constants."""
+    F32, F16 = abi.NF_DTYPE_F32, abi.NF_DTYPE_F16
+    p = plan(lib, "silu", [D(F16, 64)], [D(F16, 64)])
+    assert (p["kernel"], p["count"]) == ("silu_f16", 32)
+    p = plan(lib, "metal_vector_add", [D(F32, 400), D(F32, 400)], [D(F32, 400)])
+    assert (p["kernel"], p["count"]) == ("vector_add_f32", 100)
+    pc = push_constants(head_dim=64, epsilon=1e-5)
+    p = plan(lib, "rms_norm", [D(F32, 3 * 64 * 4), D(F32, 64 * 4)], [D(F32, 3 * 64 * 4)], pc=pc)
+    assert (p["kernel"], p["count"]) == ("rms_norm_f32", 192)
+    p = plan(lib, "argmax", [D(F32, 2 * 10 * 4)], [D(abi.NF_DTYPE_I32, 8)], pc=push_constants(seq_len=2, N=10))
+    assert (p["kernel"], p["count"]) == ("argmax_f32", 2)
+    pc = push_constants(seq_len=1, n_heads=8, head_dim=64, M=2, step_idx=5, max_seq_len=16)
+    ins = [D(F16, 8 * 64 * 2), D(F16, 2 * 64 * 2), D(F16, 2 * 64 * 2), D(F16, 2 * 16 * 64 * 2), D(F16, 2 * 16 * 64 * 2)]
+    p = plan(lib, "flash_attention_gqa", ins, [D(F16, 8 * 64 * 2)], pc=pc)
+    assert (p["kernel"], p["count"]) == ("attention_gqa_decode_f16", 8)
+    with pytest.raises(NfError):  # caches too small for n_kv * max_seq * head_dim
+        plan(lib, "flash_attention_gqa", ins[:3] + [D(F16, 100), D(F16, 100)], [D(F16, 8 * 64 * 2)], pc=pc)
+    with pytest.raises(NfError):  # attention without push constants
+        plan(lib, "flash_attention_gqa", ins, [D(F16, 8 * 64 * 2)])
+
+
 def test_plan_dense_linear_dtypes(lib):
     M, N, K = 3, 5, 16
     p = plan(lib, "linear", [D(abi.NF_DTYPE_F16, M * K * 2), D(abi.NF_DTYPE_F16, N * K * 2)],
@@ -208,7 +231,7 @@ def test_plan_dense_linear_dtypes(lib):
 
 def test_plan_unknown_op(lib):
     with pytest.raises(NfError) as e:
-        plan(lib, "rms_norm", [D(0, 4)], [D(0, 4)])
+        plan(lib, "sparse_moe_router", [D(0, 4)], [D(0, 4)])
     assert e.value.status == abi.NF_ERROR_UNSUPPORTED_OP
 
 
