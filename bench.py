@@ -71,7 +71,7 @@ def parse(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--sweep", action="store_true", help="configs[4] GEMV/MFMA crossover sweep")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
-    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "dq", "up"], default=None,
+    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "dq", "up", "layer"], default=None,
                     help="run one configs[i] section alone and print its JSON (profiling aid)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 4 device-to-device copies of BYTES (reference for HBM byte counters)")
@@ -431,6 +431,86 @@ def run_dq(prov, n_elems: int = 11008 * 4096, copies: int = 2) -> dict:
     return res
 
 
+def run_layer(prov) -> dict:
+    """The layer ops around the linears at Llama-class shapes: decode
+    attention over a 4096-token KV cache (GB/s of cache + q/out bytes),
+    causal prefill attention over 2048 tokens (TFLOP/s, the causal half:
+    2 * S^2 * head_dim * n_heads), rms_norm / rope_batch / silu / add /
+    embedding over 2048 x 4096 tokens (GB/s), softmax and argmax over
+    32 x 128256 logits.  Graph replay of 2 rotated buffer sets."""
+    from neurofabric_amd import abi
+    from neurofabric_amd.plugin import push_constants
+    r = np.random.default_rng(0)
+    F32, F16, I32 = abi.NF_DTYPE_F32, abi.NF_DTYPE_F16, abi.NF_DTYPE_I32
+    res = {}
+
+    def buf(n, dt, fill=True):
+        e = 2 if dt == F16 else 4
+        if not fill:
+            return prov.alloc(dt, n * e)
+        x = r.standard_normal(n).astype(np.float32)
+        arr = x.astype(np.float16) if dt == F16 else (x.astype(np.int32) if dt == I32 else x)
+        return prov.alloc_array(arr, dt)
+
+    def measure(name, op, make, pc, flops=0, copies=2, steps=10):
+        st = Step(prov)
+        for _ in range(copies):
+            ins, outs = make()
+            st.buffers += ins + outs
+            td = prov.task(op, ins, outs, pc=pc)
+            p = prov.plan(op, [Step._desc(b) for b in ins], [Step._desc(b) for b in outs], pc=pc)
+            st.kernels.add(p["kernel"])
+            st.weight_bytes += p["weight_bytes"]
+            st.act_bytes += p["act_bytes"]
+            st.out_bytes += p["out_bytes"]
+            st.descs.append(td)
+        st.finish()
+        # graph replay: these kernels run for microseconds, less than the
+        # host needs to enqueue a dispatch, so eager timing would measure the host
+        t = time_step(prov, st, steps, 2, "graph")
+        us = t["ms_per_step"] * 1e3 / copies
+        d = {"us_per_launch": us, "GB_s": st.bytes / copies / (us * 1e-6) / 1e9, "kernel": sorted(st.kernels)[0]}
+        d["frac_of_hbm_peak"] = d["GB_s"] / HBM_PEAK_GBS
+        if flops:
+            d["TFLOP_s"] = flops / (us * 1e-6) / 1e12
+        res[name] = d
+        log(f"[bench] {name}: {us:.1f} us, {d['GB_s']:.0f} GB/s" + (f", {d['TFLOP_s']:.1f} TFLOP/s" if flops else ""))
+        st.release()
+
+    H, KV, D, ctx = 32, 8, 128, 4096
+    for f16 in (True, False):
+        dt = F16 if f16 else F32
+        pc = push_constants(seq_len=1, n_heads=H, head_dim=D, M=KV, step_idx=ctx - 1, max_seq_len=ctx)
+        measure(f"decode_attention_gqa_{'f16' if f16 else 'f32'}_h32kv8d128_ctx4096", "flash_attention_gqa",
+                lambda: ([buf(H * D, dt), buf(KV * D, dt), buf(KV * D, dt), buf(KV * ctx * D, dt),
+                          buf(KV * ctx * D, dt)], [buf(H * D, dt, False)]), pc)
+    S = 2048
+    pc = push_constants(seq_len=S, n_heads=H, head_dim=D, M=KV, step_idx=0, max_seq_len=S)
+    measure("prefill_attention_f16_h32kv8d128_s2048", "flash_attention_cached",
+            lambda: ([buf(S * H * D, F16), buf(S * KV * D, F16), buf(S * KV * D, F16), buf(KV * S * D, F16, False),
+                      buf(KV * S * D, F16, False)], [buf(S * H * D, F16, False)]), pc,
+            flops=2 * S * S * D * H, steps=3)
+    T, E = 2048, 4096
+    for f16 in (True, False):
+        dt, tag = (F16, "f16") if f16 else (F32, "f32")
+        measure(f"rms_norm_{tag}_2048x4096", "rms_norm", lambda: ([buf(T * E, dt), buf(E, F32)], [buf(T * E, dt, False)]),
+                push_constants(head_dim=E, epsilon=1e-5))
+        measure(f"rope_batch_{tag}_2048x32x128", "rope_batch", lambda: ([buf(T * H * D, dt)], [buf(T * H * D, dt, False)]),
+                push_constants(n_heads=H, head_dim=D, theta=10000.0, step_idx=0))
+        measure(f"silu_{tag}_2048x11008", "silu", lambda: ([buf(T * 11008, dt)], [buf(T * 11008, dt, False)]), None)
+        measure(f"vector_add_{tag}_2048x4096", "metal_vector_add",
+                lambda: ([buf(T * E, dt), buf(T * E, dt)], [buf(T * E, dt, False)]), None)
+    V = 128256
+    measure("softmax_f32_32x128256", "softmax", lambda: ([buf(32 * V, F32)], [buf(32 * V, F32, False)]),
+            push_constants(seq_len=32, head_dim=V))
+    measure("argmax_f32_32x128256", "argmax", lambda: ([buf(32 * V, F32)], [buf(32, I32, False)]),
+            push_constants(seq_len=32, N=V))
+    ids = lambda: prov.alloc_array(r.integers(0, 32000, T).astype(np.int32), I32)  # noqa: E731
+    measure("embedding_lookup_f16_2048x4096", "embedding_lookup",
+            lambda: ([buf(32000 * E, F16), ids()], [buf(T * E, F16, False)]), push_constants(seq_len=T, head_dim=E))
+    return res
+
+
 def run_upload(prov, mb: int = 512) -> dict:
     """Weight upload of one `mb` MiB tensor from pageable host memory (as
     from an mmap of a GGUF file): the reference model layer's map / memcpy /
@@ -487,7 +567,8 @@ def main(argv=None) -> int:
     if args.only:
         sections = {"c0": lambda: run_c0(prov, args.mode), "c2": lambda: run_c2(prov),
                     "c3": lambda: run_c3(prov, args.mode), "c4": lambda: crossover_sweep(prov),
-                    "dq": lambda: run_dq(prov), "up": lambda: run_upload(prov)}
+                    "dq": lambda: run_dq(prov), "up": lambda: run_upload(prov),
+                    "layer": lambda: run_layer(prov)}
         print(json.dumps({args.only: sections[args.only]()}), flush=True)
         return 0
 
@@ -540,6 +621,7 @@ def main(argv=None) -> int:
         extra["c2_prefill_f16"] = run_c2(prov)
         extra["dequant_7b_ffn_weight"] = run_dq(prov)
         extra["weight_upload_512MiB"] = run_upload(prov)
+        extra["layer_ops"] = run_layer(prov)
     if args.sweep:
         extra["c4_crossover"] = crossover_sweep(prov)
 

@@ -47,6 +47,11 @@ struct Params {
   uint64_t pool_blocks;
   float scale;
   bool decode;
+  // decode: the split kernel reads key / value row `step` from K_new / V_new
+  // and the workgroup that owns it writes it into the cache
+  const void* k_new;
+  const void* v_new;
+  bool fused_append;
 };
 
 template <typename T>
@@ -56,7 +61,7 @@ __device__ __forceinline__ float f(T x) {
 
 // Element offset of the query (and output) row of (query token qi, head h).
 template <nfhip::AttnMode MODE>
-__device__ __forceinline__ uint64_t q_row(const Params& p, uint32_t qi, uint32_t h) {
+__host__ __device__ __forceinline__ uint64_t q_row(const Params& p, uint32_t qi, uint32_t h) {
   const uint64_t D = p.dim;
   if constexpr (MODE == nfhip::AttnMode::Plain) return ((uint64_t)h * p.seq_len + qi) * D;
   if constexpr (MODE == nfhip::AttnMode::Cached) return p.decode ? (uint64_t)h * D : ((uint64_t)qi * p.n_heads + h) * D;
@@ -77,9 +82,37 @@ __device__ __forceinline__ uint64_t kv_row(const Params& p, uint32_t kvh, uint32
   return (((uint64_t)phys * p.n_kv + kvh) * p.block_size + pos % p.block_size) * D;
 }
 
+constexpr int kBatch = 8;
+
+// Columns lane + 64 r of value rows t0 + j0 .. t0 + j0 + kBatch - 1.  Every
+// load is unconditional (a row past nk or without storage reads row 0, a
+// column past dim reads column dim - 1, both in bounds) so the whole batch
+// is in flight before the first use; ok[jj] marks the rows that count, and
+// the caller discards the others with a select (not a multiply by 0, which
+// would let a NaN in unused memory through).
+template <typename T, nfhip::AttnMode MODE, int R>
+__device__ __forceinline__ void load_v_batch(const Params& p, const T* V, uint32_t kvh, int64_t t0, int j0, int nk,
+                                             int lane, T (&x)[kBatch][R], bool (&ok)[kBatch]) {
+  const uint32_t D = p.dim;
+#pragma unroll
+  for (int jj = 0; jj < kBatch; ++jj) {
+    const int j = j0 + jj;
+    const uint64_t row = j < nk ? kv_row<MODE>(p, kvh, (uint32_t)(t0 + j)) : ~0ull;
+    ok[jj] = row != ~0ull;
+    const T* vr = V + (ok[jj] ? row : 0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r * 64 >= (int)D) break;  // uniform
+      const uint32_t d = lane + 64 * r;
+      x[jj][r] = vr[d < D ? d : D - 1];
+    }
+  }
+}
+
 template <typename T, nfhip::AttnMode MODE, int NW>
 __global__ __launch_bounds__(NW * 64) void attention_kernel(Params p) {
   __shared__ float qs[kMaxDim];
+  __shared__ float ps[NW][kTile];  // each wave's tile weights
   __shared__ float part_acc[NW][kMaxDim];
   __shared__ float part_m[NW], part_l[NW];
 
@@ -126,6 +159,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(Params p) {
       uint32_t d = 0;
       if constexpr (sizeof(T) == 4) {
         if ((D & 3) == 0 && (reinterpret_cast<uintptr_t>(kr) & 15) == 0)
+#pragma unroll 4
           for (; d + 4 <= D; d += 4) {
             const float4v x = *reinterpret_cast<const float4v*>(kr + d);
             dot += qs[d] * x[0];
@@ -135,6 +169,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(Params p) {
           }
       } else {
         if ((D & 7) == 0 && (reinterpret_cast<uintptr_t>(kr) & 15) == 0)
+#pragma unroll 4
           for (; d + 8 <= D; d += 8) {
             const half8 x = *reinterpret_cast<const half8*>(kr + d);
 #pragma unroll
@@ -159,17 +194,26 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(Params p) {
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] *= corr;
     const int nk = (int)((last - t0 + 1) < kTile ? (last - t0 + 1) : kTile);
-    for (int j = 0; j < nk; ++j) {
-      const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pw), j));
-      if (pj == 0.0f) continue;  // uniform: masked key or underflow
-      const uint64_t vrow = kv_row<MODE>(p, kvh, (uint32_t)(t0 + j));
-      const T* vr = V + vrow;
+    // value rows 8 at a time: the loads of a batch are all in flight before
+    // its FMAs (a masked or missing row contributes 0)
+    ps[wave][lane] = pw;  // read back by this wave only: LDS keeps a wave's accesses in order
+    __builtin_amdgcn_wave_barrier();
+    for (int j0 = 0; j0 < nk; j0 += kBatch) {
+      T x[kBatch][R];
+      bool ok[kBatch];
+      load_v_batch<T, MODE, R>(p, V, kvh, t0, j0, nk, lane, x, ok);
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const uint32_t d = lane + 64 * r;
-        if (d < D) acc[r] += pj * f(vr[d]);
+      for (int jj = 0; jj < kBatch; ++jj) {
+        if (!ok[jj]) continue;  // uniform
+        const float pj = ps[wave][j0 + jj];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (r * 64 >= (int)D) break;
+          acc[r] += pj * f(x[jj][r]);
+        }
       }
     }
+    __builtin_amdgcn_wave_barrier();
   }
 
   // merge the waves: out = sum_w acc_w e^(m_w - M) / sum_w l_w e^(m_w - M)
@@ -228,8 +272,375 @@ __global__ __launch_bounds__(256) void append_kernel(const T* __restrict__ kn, c
   cv[dst] = vn[id];
 }
 
+// ---- decode: split the keys over many workgroups ----------------------------------
+//
+// One query token per head, so the work is the KV cache read.  Workgroup =
+// one wave = (key split, KV head): it scores its keys for every query head
+// that reads this KV head (up to kMaxGroup of them), so each key / value
+// row is loaded once for the whole group, and writes one partial (m, l,
+// acc[dim]) per query head to the workspace.  A second kernel merges the
+// splits of each head in split order (deterministic).
+
+constexpr int kMaxGroup = 8;
+constexpr int kBatchDecode = 16;
+constexpr int kMaxSplits = 4096;
+
+// Dot products of the lane's key row with the G query rows in LDS.  The row
+// is read in chunks of up to 8 16-byte loads, each chunk's loads all issued
+// before its FMAs.  `kr` must be a readable row (the caller substitutes row
+// 0 for a lane without a key and discards its score).
+template <typename T, int G>
+__device__ __forceinline__ void dot_rows(const T* kr, uint32_t D, const float (*qs)[kMaxDim], float (&dot)[G]) {
+  constexpr int V = 16 / (int)sizeof(T);  // elements per 16-byte load
+  typedef T vec_t __attribute__((ext_vector_type(V)));
+#pragma unroll
+  for (int g = 0; g < G; ++g) dot[g] = 0.0f;
+  uint32_t d = 0;
+  if ((D % V) == 0 && (reinterpret_cast<uintptr_t>(kr) & 15) == 0) {
+    for (; d + 8 * V <= D; d += 8 * V) {
+      vec_t x[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) x[c] = *reinterpret_cast<const vec_t*>(kr + d + c * V);
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float xf = (float)x[c][e];
+#pragma unroll
+          for (int g = 0; g < G; ++g) dot[g] += qs[g][d + c * V + e] * xf;
+        }
+    }
+    for (; d + V <= D; d += V) {
+      const vec_t x = *reinterpret_cast<const vec_t*>(kr + d);
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+#pragma unroll
+        for (int g = 0; g < G; ++g) dot[g] += qs[g][d + e] * (float)x[e];
+    }
+  }
+  for (; d < D; ++d) {
+    const float xf = f(kr[d]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) dot[g] += qs[g][d] * xf;
+  }
+}
+
+template <typename T, nfhip::AttnMode MODE, int G, int R>
+__global__ __launch_bounds__(64) void decode_split_kernel(Params p, uint32_t keys_per_split, uint32_t lo,
+                                                          float* __restrict__ part) {
+  constexpr int VEC = 16 / (int)sizeof(T);               // elements per 16-byte load
+  constexpr int KREG = sizeof(T) == 2 ? 16 : 16;         // 16-byte key loads held at once
+  constexpr int VB = R == 4 ? 32 : 64;                   // value rows loaded at once
+  typedef T vec_t __attribute__((ext_vector_type(VEC)));
+  __shared__ float qs[G][kMaxDim];
+  __shared__ __attribute__((aligned(16))) float ps[kTile][G < 4 ? G : 4 * ((G + 3) / 4)];  // tile weights [key][head]
+  const uint32_t split = blockIdx.x;
+  const uint32_t kvh = blockIdx.y;
+  const uint32_t H = p.n_heads, KV = p.n_kv, D = p.dim;
+  // query heads h with h * KV / H == kvh
+  const uint32_t h0 = (uint32_t)(((uint64_t)kvh * H + KV - 1) / KV);
+  const uint32_t h1 = (uint32_t)(((uint64_t)(kvh + 1) * H + KV - 1) / KV);
+  const int ng = (int)(h1 - h0);
+  const int lane = threadIdx.x;
+  const T* Q = static_cast<const T*>(p.q);
+  const T* K = static_cast<const T*>(p.k);
+  const T* V = static_cast<const T*>(p.v);
+  // key rows are read as 16-byte vectors when every row is aligned to them
+  const bool kvec = (D % VEC) == 0 && (reinterpret_cast<uintptr_t>(K) & 15) == 0 &&
+                    (!p.fused_append || (reinterpret_cast<uintptr_t>(p.k_new) & 15) == 0) &&
+                    (uint32_t)(D / VEC) <= (uint32_t)KREG;
+
+  // 1. query loads (consumed after the first tile's loads are issued)
+  T qraw[G][R];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t h = h0 + (uint32_t)(g < ng ? g : ng - 1);
+      const uint32_t d = lane + 64 * r;
+      qraw[g][r] = Q[q_row<MODE>(p, 0, h) + (d < D ? d : D - 1)];
+    }
+
+  int64_t last = p.step;
+  if constexpr (MODE == nfhip::AttnMode::Paged) {
+    const int64_t cap = (int64_t)p.n_blocks * p.block_size - 1;
+    if (last > cap) last = cap;
+  }
+  const int64_t k_begin = (int64_t)lo + (int64_t)split * keys_per_split;
+  int64_t k_end = k_begin + keys_per_split - 1;
+  if (k_end > last) k_end = last;
+  if (p.fused_append && k_begin <= (int64_t)p.step && (int64_t)p.step <= k_end) {
+    // this workgroup owns row `step` of KV head kvh: append it (nobody else reads it)
+    const uint64_t src = (uint64_t)kvh * D, dst = ((uint64_t)kvh * p.max_seq + p.step) * D;
+    for (uint32_t d = lane; d < D; d += 64) {
+      static_cast<T*>(p.k)[dst + d] = static_cast<const T*>(p.k_new)[src + d];
+      static_cast<T*>(p.v)[dst + d] = static_cast<const T*>(p.v_new)[src + d];
+    }
+  }
+
+  float acc[G][R];
+  float m[G], l[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[g][r] = 0.0f;
+  }
+
+  bool first = true;
+  for (int64_t t0 = k_begin; t0 <= k_end || first; t0 += kTile) {
+    const bool live_tile = t0 <= k_end;
+    // 2. this tile's key row (lane = key) and value rows, all loads issued
+    const int64_t kp = t0 + lane;
+    uint64_t krow = ~0ull;
+    if (live_tile && kp <= k_end) krow = kv_row<MODE>(p, kvh, (uint32_t)kp);
+    const T* kr = K + (krow != ~0ull ? krow : 0);
+    if (p.fused_append && kp == (int64_t)p.step) kr = static_cast<const T*>(p.k_new) + (uint64_t)kvh * D;
+    vec_t kx[KREG];
+    if (kvec) {
+#pragma unroll
+      for (int c = 0; c < KREG; ++c)
+        if (c * VEC < (int)D) kx[c] = *reinterpret_cast<const vec_t*>(kr + c * VEC);  // uniform bound
+    }
+    const int nk = live_tile ? (int)((k_end - t0 + 1) < kTile ? (k_end - t0 + 1) : kTile) : 0;
+    T x[VB][R];
+    bool ok[VB];
+#pragma unroll
+    for (int jj = 0; jj < VB; ++jj) {
+      const int j = jj;
+      const uint64_t row = j < nk ? kv_row<MODE>(p, kvh, (uint32_t)(t0 + j)) : ~0ull;
+      ok[jj] = row != ~0ull;
+      const T* vr = V + (ok[jj] ? row : 0);
+      if (p.fused_append && t0 + j == (int64_t)p.step) vr = static_cast<const T*>(p.v_new) + (uint64_t)kvh * D;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t d = lane + 64 * r;
+        x[jj][r] = vr[d < D ? d : D - 1];
+      }
+    }
+    if (first) {
+      // 3. queries to LDS once their loads are back
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint32_t d = lane + 64 * r;
+          if (d < (uint32_t)kMaxDim) qs[g][d] = (g < ng && d < D) ? f(qraw[g][r]) : 0.0f;
+        }
+      __syncthreads();
+      first = false;
+    }
+    if (!live_tile) break;
+    // 4. scores
+    float dot[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) dot[g] = 0.0f;
+    if (kvec) {
+#pragma unroll
+      for (int c = 0; c < KREG; ++c) {
+        if (c * VEC >= (int)D) break;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float xf = (float)kx[c][e];
+#pragma unroll
+          for (int g = 0; g < G; ++g) dot[g] += qs[g][c * VEC + e] * xf;
+        }
+      }
+    } else {
+      dot_rows<T, G>(kr, D, qs, dot);
+    }
+    float s[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) s[g] = krow != ~0ull ? dot[g] * p.scale : -INFINITY;
+    float pw[G];
+    bool any = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float tmax = s[g];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o));
+      pw[g] = 0.0f;
+      if (tmax == -INFINITY) continue;  // uniform
+      any = true;
+      const float m_new = fmaxf(m[g], tmax);
+      const float corr = expf(m[g] - m_new);
+      pw[g] = s[g] == -INFINITY ? 0.0f : expf(s[g] - m_new);
+      float ps = pw[g];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
+      l[g] = l[g] * corr + ps;
+      m[g] = m_new;
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[g][r] *= corr;
+    }
+    if (!any) continue;
+    // 5. P.V: the tile's weights go through LDS (one broadcast read per key
+    // and group of 4 heads); the first VB value rows are already in registers
+#pragma unroll
+    for (int g = 0; g < G; ++g) ps[lane][g] = pw[g];
+    __syncthreads();
+    for (int j0 = 0; j0 < nk; j0 += VB) {
+      if (j0 > 0) {
+#pragma unroll
+        for (int jj = 0; jj < VB; ++jj) {
+          const int j = j0 + jj;
+          const uint64_t row = j < nk ? kv_row<MODE>(p, kvh, (uint32_t)(t0 + j)) : ~0ull;
+          ok[jj] = row != ~0ull;
+          const T* vr = V + (ok[jj] ? row : 0);
+          if (p.fused_append && t0 + j == (int64_t)p.step)
+            vr = static_cast<const T*>(p.v_new) + (uint64_t)kvh * D;
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const uint32_t d = lane + 64 * r;
+            x[jj][r] = vr[d < D ? d : D - 1];
+          }
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < VB; ++jj) {
+        if (!ok[jj]) continue;  // uniform
+        float pj[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) pj[g] = ps[j0 + jj][g];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float xv = f(x[jj][r]);
+#pragma unroll
+          for (int g = 0; g < G; ++g) acc[g][r] += pj[g] * xv;
+        }
+      }
+    }
+    __syncthreads();  // ps is rewritten by the next tile
+  }
+
+  // partial of (split, head): [m, l, acc[0..D)]
+  const uint32_t stride = D + 2;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (g >= ng) break;
+    float* dst = part + ((uint64_t)split * H + h0 + g) * stride;
+    if (lane == 0) {
+      dst[0] = m[g];
+      dst[1] = l[g];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t dd = lane + 64 * r;
+      if (dd < D) dst[2 + dd] = acc[g][r];
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(1024) void decode_combine_kernel(const float* __restrict__ part, uint32_t n_splits,
+                                                              uint32_t H, uint32_t D, T* __restrict__ out,
+                                                              uint64_t out_row0, uint64_t out_head_stride) {
+  // weight of each split, e^(m_s - M) / sum_s l_s e^(m_s - M), formed once in
+  // LDS; then column d is summed over the splits by `groups` threads (split
+  // classes sp % groups) whose partials add in a fixed order
+  __shared__ float w[kMaxSplits];
+  __shared__ float red[1024];
+  __shared__ float mm[2];
+  const uint32_t h = blockIdx.x;
+  const uint32_t stride = D + 2;
+  const uint32_t t = threadIdx.x;
+  if (t < 64) {
+    float m = -INFINITY;
+    for (uint32_t sp = t; sp < n_splits; sp += 64) m = fmaxf(m, part[((uint64_t)sp * H + h) * stride]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (t == 0) mm[0] = m;
+  }
+  __syncthreads();
+  const float M = mm[0];
+  for (uint32_t sp = t; sp < n_splits; sp += 1024) {
+    const float m = part[((uint64_t)sp * H + h) * stride];
+    w[sp] = m == -INFINITY ? 0.0f : expf(m - M);
+  }
+  __syncthreads();
+  if (t < 64) {
+    float L = 0.0f;
+    for (uint32_t sp = t; sp < n_splits; sp += 64) L += part[((uint64_t)sp * H + h) * stride + 1] * w[sp];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
+    if (t == 0) mm[1] = L > 0.0f ? 1.0f / L : 0.0f;
+  }
+  const uint32_t dpad = (D + 63) / 64 * 64;
+  const uint32_t groups = 1024 / dpad;
+  const uint32_t grp = t / dpad, d = t % dpad;
+  float o = 0.0f;
+  if (grp < groups && d < D) {
+    const uint64_t step = (uint64_t)H * stride;
+    const float* src = part + (uint64_t)h * stride + 2 + d;
+#pragma unroll 8
+    for (uint32_t sp = grp; sp < n_splits; sp += groups) o += src[sp * step] * w[sp];
+  }
+  red[t] = o;
+  __syncthreads();
+  if (grp == 0 && d < D) {
+    float sum = 0.0f;
+    for (uint32_t g = 0; g < groups; ++g) sum += red[g * dpad + d];
+    out[out_row0 + (uint64_t)h * out_head_stride + d] = (T)(sum * mm[1]);
+  }
+}
+
+// Decode with the split kernels; hipErrorNotSupported when the group or the
+// workspace does not fit (the caller then runs the one-workgroup-per-head kernel).
 template <typename T, nfhip::AttnMode MODE>
-hipError_t run(const Params& p, uint32_t nq, hipStream_t s) {
+hipError_t run_decode_split(const Params& p, float* ws, size_t ws_floats, hipStream_t s) {
+  const uint32_t H = p.n_heads, KV = p.n_kv;
+  const uint32_t gmax = (H + KV - 1) / KV;
+  if (!ws || gmax > (uint32_t)kMaxGroup) return hipErrorNotSupported;
+  uint32_t lo = 0;
+  if constexpr (MODE == nfhip::AttnMode::Cached)
+    if (p.window > 0 && p.step >= p.window) lo = p.step - p.window + 1;
+  int64_t last = p.step;
+  if constexpr (MODE == nfhip::AttnMode::Paged) {
+    const int64_t cap = (int64_t)p.n_blocks * p.block_size - 1;
+    if (last > cap) last = cap;
+  }
+  const uint64_t n_keys = last >= (int64_t)lo ? (uint64_t)(last - lo + 1) : 1;
+  // about 512 workgroups, whole 64-key tiles, at most 1024 keys each
+  uint64_t kps = (n_keys * KV + 511) / 512;
+  kps = (kps + kTile - 1) / kTile * kTile;
+  if (kps < (uint64_t)kTile) kps = kTile;
+  if (kps > 1024) kps = 1024;
+  const uint64_t n_splits = (n_keys + kps - 1) / kps;
+  if (n_splits > (uint64_t)kMaxSplits || n_splits * H * (p.dim + 2) > ws_floats) return hipErrorNotSupported;
+  const dim3 grid((unsigned)n_splits, KV);
+  const int R = p.dim <= 64 ? 1 : p.dim <= 128 ? 2 : 4;
+  const int G = gmax == 1 ? 1 : gmax == 2 ? 2 : gmax <= 4 ? 4 : 8;
+#define NF_DECODE_SPLIT(GG, RR) \
+  if (G == GG && R == RR) decode_split_kernel<T, MODE, GG, RR><<<grid, 64, 0, s>>>(p, (uint32_t)kps, lo, ws);
+  NF_DECODE_SPLIT(1, 1) NF_DECODE_SPLIT(1, 2) NF_DECODE_SPLIT(1, 4)
+  NF_DECODE_SPLIT(2, 1) NF_DECODE_SPLIT(2, 2) NF_DECODE_SPLIT(2, 4)
+  NF_DECODE_SPLIT(4, 1) NF_DECODE_SPLIT(4, 2) NF_DECODE_SPLIT(4, 4)
+  NF_DECODE_SPLIT(8, 1) NF_DECODE_SPLIT(8, 2) NF_DECODE_SPLIT(8, 4)
+#undef NF_DECODE_SPLIT
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // output rows: [n_heads, dim] at the query row of token 0
+  const uint64_t row0 = q_row<MODE>(p, 0, 0);
+  decode_combine_kernel<T><<<H, 1024, 0, s>>>(ws, (uint32_t)n_splits, H, p.dim, static_cast<T*>(p.out), row0,
+                                             p.dim);
+  return hipGetLastError();
+}
+
+template <typename T, nfhip::AttnMode MODE>
+hipError_t run(const Params& p, uint32_t nq, float* ws, size_t ws_floats, hipStream_t s) {
+  if (p.decode) {
+    const hipError_t e = run_decode_split<T, MODE>(p, ws, ws_floats, s);
+    if (e != hipErrorNotSupported) return e;
+    if (p.fused_append) {  // the split kernel declined: append here first
+      const uint64_t n = (uint64_t)p.n_kv * p.dim;
+      append_kernel<T, MODE == nfhip::AttnMode::Gqa><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+          static_cast<const T*>(p.k_new), static_cast<const T*>(p.v_new), static_cast<T*>(p.k),
+          static_cast<T*>(p.v), p.n_kv, 1, p.dim, p.max_seq, p.step);
+      const hipError_t e2 = hipGetLastError();
+      if (e2 != hipSuccess) return e2;
+    }
+  }
   // decode: one query per head, so more waves per workgroup split the keys
   if (p.decode)
     attention_kernel<T, MODE, 16><<<dim3(nq, p.n_heads), 1024, 0, s>>>(p);
@@ -244,7 +655,9 @@ hipError_t launch_t(const nfhip::AttnArgs& a, hipStream_t s) {
   if (lp.noop) return hipSuccess;
   const uint32_t nq = lp.decode ? 1 : lp.seq_len;
   if (nq == 0) return hipSuccess;
-  if (lp.append) {
+  // decode appends inside the split kernel when that path runs
+  const bool fuse = lp.append && lp.decode && a.ws != nullptr;
+  if (lp.append && !fuse) {
     const uint32_t tokens = lp.decode ? 1 : lp.seq_len;
     const uint64_t n = (uint64_t)lp.n_kv * tokens * lp.head_dim;
     const dim3 grid((unsigned)((n + 255) / 256));
@@ -277,11 +690,14 @@ hipError_t launch_t(const nfhip::AttnArgs& a, hipStream_t s) {
   p.pool_blocks = a.pool_blocks;
   p.scale = 1.0f / sqrtf((float)lp.head_dim);
   p.decode = lp.decode;
+  p.k_new = a.k_new;
+  p.v_new = a.v_new;
+  p.fused_append = fuse;
   switch (lp.attn) {
-    case nfhip::AttnMode::Plain: return run<T, nfhip::AttnMode::Plain>(p, nq, s);
-    case nfhip::AttnMode::Cached: return run<T, nfhip::AttnMode::Cached>(p, nq, s);
-    case nfhip::AttnMode::Gqa: return run<T, nfhip::AttnMode::Gqa>(p, nq, s);
-    default: return run<T, nfhip::AttnMode::Paged>(p, nq, s);
+    case nfhip::AttnMode::Plain: return run<T, nfhip::AttnMode::Plain>(p, nq, a.ws, a.ws_floats, s);
+    case nfhip::AttnMode::Cached: return run<T, nfhip::AttnMode::Cached>(p, nq, a.ws, a.ws_floats, s);
+    case nfhip::AttnMode::Gqa: return run<T, nfhip::AttnMode::Gqa>(p, nq, a.ws, a.ws_floats, s);
+    default: return run<T, nfhip::AttnMode::Paged>(p, nq, a.ws, a.ws_floats, s);
   }
 }
 

@@ -105,6 +105,8 @@ struct AttnArgs {
   void* out = nullptr;
   LayerParams lp;
   uint64_t pool_blocks = 0;  // Paged: whole blocks the pools hold
+  float* ws = nullptr;       // decode partials (the provider's split-K workspace)
+  size_t ws_floats = 0;
 };
 hipError_t launch_attention(EType t, const AttnArgs& a, hipStream_t s);
 

@@ -536,6 +536,8 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, int g
         a.k = in[3]->dev;
         a.v = in[4]->dev;
       }
+      a.ws = ws.part;
+      a.ws_floats = ws.part_floats;
       return launch_attention(pl.c, a, s);
     }
   }
