@@ -193,30 +193,151 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restric
   }
 }
 
+// ---- wide rows: each row split over many workgroups -------------------------------
+//
+// A row of a 128K-entry vocabulary in one workgroup leaves most of the chip
+// idle, so wide rows go in kChunk-element chunks: the first kernel reduces
+// each chunk (softmax: its max and its sum of e^(x - max); argmax: its best
+// value and index) into the workspace, the second merges a row's chunks in
+// chunk order (deterministic) and, for softmax, writes the chunk's outputs.
+
+constexpr uint32_t kChunk = 4096;
+
+__global__ __launch_bounds__(kThreads) void softmax_chunk_kernel(const float* __restrict__ in, uint32_t dim,
+                                                                 uint32_t chunks, float* __restrict__ part) {
+  __shared__ float red[4];
+  const uint32_t c = blockIdx.x, row = blockIdx.y;
+  const uint64_t base = (uint64_t)row * dim;
+  const uint32_t j0 = c * kChunk, j1 = min(dim, j0 + kChunk);
+  float m = -INFINITY;
+  for (uint32_t j = j0 + threadIdx.x; j < j1; j += kThreads) m = fmaxf(m, in[base + j]);
+  m = block_max(m, red);
+  float sum = 0.0f;
+  for (uint32_t j = j0 + threadIdx.x; j < j1; j += kThreads) sum += expf(in[base + j] - m);
+  sum = block_sum(sum, red);
+  if (threadIdx.x == 0) {
+    part[((uint64_t)row * chunks + c) * 2] = m;
+    part[((uint64_t)row * chunks + c) * 2 + 1] = sum;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void softmax_write_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                                 uint32_t dim, uint32_t chunks,
+                                                                 const float* __restrict__ part) {
+  const uint32_t c = blockIdx.x, row = blockIdx.y;
+  const float* pr = part + (uint64_t)row * chunks * 2;
+  float M = -INFINITY;
+  for (uint32_t k = 0; k < chunks; ++k) M = fmaxf(M, pr[2 * k]);
+  float S = 0.0f;
+  for (uint32_t k = 0; k < chunks; ++k) S += pr[2 * k + 1] * expf(pr[2 * k] - M);
+  const float inv = 1.0f / S;
+  const uint64_t base = (uint64_t)row * dim;
+  const uint32_t j0 = c * kChunk, j1 = min(dim, j0 + kChunk);
+  for (uint32_t j = j0 + threadIdx.x; j < j1; j += kThreads) out[base + j] = expf(in[base + j] - M) * inv;
+}
+
+constexpr uint32_t kNoIdx = 0xFFFFFFFFu;
+
+__device__ __forceinline__ bool arg_better(float b2, uint32_t i2, float b1, uint32_t i1) {
+  if (i2 == kNoIdx) return false;
+  if (i1 == kNoIdx) return true;
+  return b2 > b1 || (b2 == b1 && i2 < i1);
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_chunk_kernel(const float* __restrict__ in, uint32_t dim,
+                                                                uint32_t chunks, float* __restrict__ part) {
+  __shared__ float rv[4];
+  __shared__ uint32_t ri[4];
+  const uint32_t c = blockIdx.x, row = blockIdx.y;
+  const uint64_t base = (uint64_t)row * dim;
+  const uint32_t j0 = c * kChunk, j1 = min(dim, j0 + kChunk);
+  float best = -INFINITY;
+  uint32_t idx = kNoIdx;
+  for (uint32_t j = j0 + threadIdx.x; j < j1; j += kThreads) {
+    const float x = in[base + j];
+    if (!isnan(x) && (idx == kNoIdx || x > best)) {
+      best = x;
+      idx = j;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float b2 = __shfl_xor(best, o);
+    const uint32_t i2 = __shfl_xor(idx, o);
+    if (arg_better(b2, i2, best, idx)) {
+      best = b2;
+      idx = i2;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    rv[threadIdx.x >> 6] = best;
+    ri[threadIdx.x >> 6] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = rv[0];
+    uint32_t i = ri[0];
+    for (int k = 1; k < 4; ++k)
+      if (arg_better(rv[k], ri[k], b, i)) {
+        b = rv[k];
+        i = ri[k];
+      }
+    part[((uint64_t)row * chunks + c) * 2] = b;
+    part[((uint64_t)row * chunks + c) * 2 + 1] = __uint_as_float(i);
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_merge_kernel(const float* __restrict__ in, uint32_t dim, uint32_t chunks,
+                                                          const float* __restrict__ part, int32_t* __restrict__ out) {
+  const uint32_t row = blockIdx.x;
+  if (threadIdx.x != 0) return;
+  const float* pr = part + (uint64_t)row * chunks * 2;
+  float b = -INFINITY;
+  uint32_t i = kNoIdx;
+  for (uint32_t k = 0; k < chunks; ++k) {
+    const uint32_t ik = __float_as_uint(pr[2 * k + 1]);
+    if (arg_better(pr[2 * k], ik, b, i)) {
+      b = pr[2 * k];
+      i = ik;
+    }
+  }
+  out[row] = isnan(in[(uint64_t)row * dim]) ? 0 : (int32_t)i;
+}
+
 // ---- position encodings and lookups --------------------------------------------
 
 // RoPE on rows of head_dim: pairs (p, p + head_dim/2) rotated by pos * theta^(-2p/head_dim).
 // rope_batch: [seq, n_heads, head_dim], pos = token + step (metal_provider.mm:125-147);
 // rope: every row at pos = step (metal_provider.mm:104-122, with the rotation
 // the kernel intends for both halves of each row).
+// One thread per (group of rows at one position, pair p): the rotation of
+// pair p is computed once and applied to every row of the group (the
+// n_heads rows of a token for rope_batch, up to kRopeRows rows for rope).
+constexpr uint32_t kRopeRows = 32;
+
 template <typename T>
-__global__ __launch_bounds__(kThreads) void rope_kernel(const T* __restrict__ in, T* __restrict__ out, uint64_t n,
-                                                        uint32_t head_dim, uint32_t row_span, uint32_t step,
+__global__ __launch_bounds__(kThreads) void rope_kernel(const T* __restrict__ in, T* __restrict__ out, uint64_t rows,
+                                                        uint32_t head_dim, uint32_t rows_per_group, uint32_t step,
                                                         float theta, bool batch) {
-  const uint64_t id = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (id >= n) return;
   const uint32_t half = head_dim / 2;
-  const uint32_t e = (uint32_t)(id % head_dim);
-  const uint32_t pair = e % half;
-  const uint64_t pos = batch ? id / row_span + step : step;
+  const uint64_t id = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  const uint64_t grp = id / half;
+  const uint32_t pair = (uint32_t)(id % half);
+  const uint64_t r0 = grp * rows_per_group;
+  if (r0 >= rows) return;
+  const uint64_t pos = batch ? grp + step : step;
   const float freq = 1.0f / powf(theta, (float)(2 * pair) / (float)head_dim);
   const float angle = (float)pos * freq;
   float s, c;
   sincosf(angle, &s, &c);
-  const uint64_t base = id - e;
-  const float x0 = (float)in[base + pair];
-  const float x1 = (float)in[base + pair + half];
-  out[id] = (T)(e < half ? x0 * c - x1 * s : x0 * s + x1 * c);
+  const uint64_t r1 = min(rows, r0 + rows_per_group);
+  for (uint64_t r = r0; r < r1; ++r) {
+    const uint64_t base = r * head_dim;
+    const float x0 = (float)in[base + pair];
+    const float x1 = (float)in[base + pair + half];
+    out[base + pair] = (T)(x0 * c - x1 * s);
+    out[base + pair + half] = (T)(x0 * s + x1 * c);
+  }
 }
 
 // embedding_lookup: out[t, :] = weights[ids[t], :] for t < seq_len; a token
@@ -306,25 +427,51 @@ hipError_t launch_rope(EType t, bool batch, const void* in, void* out, uint64_t 
                        uint32_t head_dim, uint32_t step, float theta, hipStream_t s) {
   if (n == 0) return hipSuccess;
   using namespace nfk::layer;
-  const uint32_t span = batch ? n_heads * head_dim : head_dim;
+  const uint64_t rows = n / head_dim;
+  const uint32_t per = batch ? n_heads : kRopeRows;  // rows sharing one position
+  const uint64_t groups = (rows + per - 1) / per;
+  const uint64_t threads = groups * (head_dim / 2);
   if (t == EType::F16)
-    rope_kernel<half_t><<<grid_for(n), kThreads, 0, s>>>((const half_t*)in, (half_t*)out, n, head_dim, span, step,
-                                                         theta, batch);
+    rope_kernel<half_t><<<grid_for(threads), kThreads, 0, s>>>((const half_t*)in, (half_t*)out, rows, head_dim, per,
+                                                               step, theta, batch);
   else
-    rope_kernel<float><<<grid_for(n), kThreads, 0, s>>>((const float*)in, (float*)out, n, head_dim, span, step,
-                                                        theta, batch);
+    rope_kernel<float><<<grid_for(threads), kThreads, 0, s>>>((const float*)in, (float*)out, rows, head_dim, per, step,
+                                                              theta, batch);
   return hipGetLastError();
 }
 
-hipError_t launch_softmax(const void* in, void* out, uint32_t rows, uint32_t dim, hipStream_t s) {
+// Rows wider than two chunks, with room for their partials in the
+// workspace, take the chunked kernels.
+static bool chunked(uint32_t rows, uint32_t dim, size_t ws_floats, uint32_t* chunks) {
+  *chunks = (dim + nfk::layer::kChunk - 1) / nfk::layer::kChunk;
+  return dim > 2 * nfk::layer::kChunk && (size_t)rows * *chunks * 2 <= ws_floats;
+}
+
+hipError_t launch_softmax(const void* in, void* out, uint32_t rows, uint32_t dim, float* ws, size_t ws_floats,
+                          hipStream_t s) {
   if (rows == 0) return hipSuccess;
-  nfk::layer::softmax_kernel<<<rows, nfk::layer::kThreads, 0, s>>>((const float*)in, (float*)out, dim);
+  using namespace nfk::layer;
+  uint32_t chunks = 0;
+  if (ws && chunked(rows, dim, ws_floats, &chunks)) {
+    softmax_chunk_kernel<<<dim3(chunks, rows), kThreads, 0, s>>>((const float*)in, dim, chunks, ws);
+    softmax_write_kernel<<<dim3(chunks, rows), kThreads, 0, s>>>((const float*)in, (float*)out, dim, chunks, ws);
+    return hipGetLastError();
+  }
+  softmax_kernel<<<rows, kThreads, 0, s>>>((const float*)in, (float*)out, dim);
   return hipGetLastError();
 }
 
-hipError_t launch_argmax(const void* in, void* out, uint32_t rows, uint32_t dim, hipStream_t s) {
+hipError_t launch_argmax(const void* in, void* out, uint32_t rows, uint32_t dim, float* ws, size_t ws_floats,
+                         hipStream_t s) {
   if (rows == 0) return hipSuccess;
-  nfk::layer::argmax_kernel<<<rows, nfk::layer::kThreads, 0, s>>>((const float*)in, (int32_t*)out, dim);
+  using namespace nfk::layer;
+  uint32_t chunks = 0;
+  if (ws && chunked(rows, dim, ws_floats, &chunks)) {
+    argmax_chunk_kernel<<<dim3(chunks, rows), kThreads, 0, s>>>((const float*)in, dim, chunks, ws);
+    argmax_merge_kernel<<<rows, 64, 0, s>>>((const float*)in, dim, chunks, ws, (int32_t*)out);
+    return hipGetLastError();
+  }
+  argmax_kernel<<<rows, kThreads, 0, s>>>((const float*)in, (int32_t*)out, dim);
   return hipGetLastError();
 }
 

@@ -89,8 +89,11 @@ hipError_t launch_rms_norm(EType t, const void* in, const void* w, void* out, ui
 // batch: rope_batch ([seq, n_heads, head_dim], pos = token + step); else rope (pos = step).
 hipError_t launch_rope(EType t, bool batch, const void* in, void* out, uint64_t n, uint32_t n_heads,
                        uint32_t head_dim, uint32_t step, float theta, hipStream_t s);
-hipError_t launch_softmax(const void* in, void* out, uint32_t rows, uint32_t dim, hipStream_t s);
-hipError_t launch_argmax(const void* in, void* out, uint32_t rows, uint32_t dim, hipStream_t s);
+// ws: the provider workspace (partials of rows split into chunks), may be null
+hipError_t launch_softmax(const void* in, void* out, uint32_t rows, uint32_t dim, float* ws, size_t ws_floats,
+                          hipStream_t s);
+hipError_t launch_argmax(const void* in, void* out, uint32_t rows, uint32_t dim, float* ws, size_t ws_floats,
+                         hipStream_t s);
 hipError_t launch_embedding(EType t, const void* w, uint32_t vocab, const void* ids, void* out, uint64_t n,
                             uint32_t dim, uint32_t seq_len, hipStream_t s);
 

@@ -511,12 +511,12 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, int g
       return launch_rope(pl.c, pl.path == Path::RopeBatch, in[0]->dev, out[0]->dev, pl.count, pl.lp.n_heads,
                          pl.lp.head_dim, pl.lp.step, pl.lp.theta, s);
     case Path::Softmax:
-      return launch_softmax(in[0]->dev, out[0]->dev, pl.lp.rows, pl.lp.dim, s);
+      return launch_softmax(in[0]->dev, out[0]->dev, pl.lp.rows, pl.lp.dim, ws.part, ws.part_floats, s);
     case Path::Embedding:
       return launch_embedding(pl.c, in[0]->dev, pl.lp.rows, in[1]->dev, out[0]->dev, pl.count, pl.lp.dim,
                               pl.lp.seq_len, s);
     case Path::Argmax:
-      return launch_argmax(in[0]->dev, out[0]->dev, pl.lp.rows, pl.lp.dim, s);
+      return launch_argmax(in[0]->dev, out[0]->dev, pl.lp.rows, pl.lp.dim, ws.part, ws.part_floats, s);
     case Path::Attention: {
       AttnArgs a;
       a.q = in[0]->dev;
