@@ -78,6 +78,16 @@ NF_API void nf_hip_get_timings(char (*op_names)[64], double *gpu_ms, uint32_t ma
 NF_API void nf_hip_get_timings_ext(char (*op_names)[64], double *gpu_ms, uint8_t *dtypes,
                                    uint32_t *elem_counts, uint32_t max_count);
 
+/* The same four entry points under the Metal plugin's names
+ * (metal_provider.mm:2149-2189), for code that binds them by name:
+ * model/model/trace_export.hpp:20-25, tests/driver/benchmark_kernels.cpp,
+ * tests/driver/real_model_test.cpp. */
+NF_API void nf_metal_enable_timing(bool enable);
+NF_API uint32_t nf_metal_get_timing_count(void);
+NF_API void nf_metal_get_timings(char (*op_names)[64], double *gpu_ms, uint32_t max_count);
+NF_API void nf_metal_get_timings_ext(char (*op_names)[64], double *gpu_ms, uint8_t *dtypes,
+                                     uint32_t *elem_counts, uint32_t max_count);
+
 /* ---- MI355X extensions (no counterpart in the reference) -------------- */
 
 /* Which kernel a dispatch would run and the work it represents.  Pure host

@@ -855,6 +855,19 @@ NF_API void nf_hip_get_timings(char (*op_names)[64], double* gpu_ms, uint32_t ma
   nf_hip_get_timings_ext(op_names, gpu_ms, nullptr, nullptr, max_count);
 }
 
+// The Metal plugin's timing entry points, under their own names, so code
+// that binds them by name (trace_export.hpp:20-25, benchmark_kernels.cpp,
+// real_model_test.cpp) links against this library unchanged.
+NF_API void nf_metal_enable_timing(bool enable) { nf_hip_enable_timing(enable); }
+NF_API uint32_t nf_metal_get_timing_count(void) { return nf_hip_get_timing_count(); }
+NF_API void nf_metal_get_timings(char (*op_names)[64], double* gpu_ms, uint32_t max_count) {
+  nf_hip_get_timings(op_names, gpu_ms, max_count);
+}
+NF_API void nf_metal_get_timings_ext(char (*op_names)[64], double* gpu_ms, uint8_t* dtypes, uint32_t* elem_counts,
+                                     uint32_t max_count) {
+  nf_hip_get_timings_ext(op_names, gpu_ms, dtypes, elem_counts, max_count);
+}
+
 NF_API nf_status nf_hip_plan_dispatch(const char* op_name, const nf_tensor_desc* in_descs,
                                       uint32_t n_in, const nf_tensor_desc* out_descs, uint32_t n_out,
                                       const void* push_constants, uint32_t push_constants_size,

@@ -45,6 +45,8 @@ REF_LAYER_TESTS = {
     "fp16_kernel_test": "All 7 tests PASSED",
     "dag_inference_test": "=== ALL PASSED ===",         # 2-layer model through PipelineEngine
     "multi_layer_test": "=== ALL PASSED ===",
+    "benchmark_kernels": "=== Benchmark complete ===",  # f16 vs f32 element-wise ops timed
+                                                        # through the nf_metal_* timing ring
 }
 
 
@@ -57,6 +59,35 @@ def test_reference_layer_test_binaries_pass(name):
     print(r.stdout[-4000:], r.stderr[-2000:])
     assert r.returncode == 0
     assert REF_LAYER_TESTS[name] in r.stdout
+
+
+def test_reference_trace_export_over_timing_ring(tmp_path):
+    """model/model/trace_export.hpp (the reference's Chrome-trace exporter,
+    compiled from where it lies by oracle/Makefile into trace_export_run)
+    reads this provider's GPU timing ring through the nf_metal_* names."""
+    import json
+    exe = REPO / "oracle" / "_ref" / "trace_export_run"
+    if not exe.exists():
+        pytest.skip("trace_export_run not built (needs the reference sources)")
+    out = tmp_path / "trace.json"
+    r = subprocess.run([str(exe), str(out)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "trace_export_run ok 3" in r.stdout
+    ev = json.loads(out.read_text())["traceEvents"]
+    assert [e["name"] for e in ev] == ["dequant_q4_0_linear", "dequant_q4_0", "silu"]
+    assert all(e["ph"] == "X" and e["dur"] > 0 for e in ev)
+    assert ev[1]["args"]["elements"] == 4096 * 4096 and ev[2]["args"]["dtype"] == "F32"
+
+
+def test_reference_nf_bench_runs():
+    """tools/nf_bench.cpp (buffer allocation, dispatch round trip,
+    linear / linear_tiled at 256..1024) linked against this provider."""
+    exe = REPO / "oracle" / "_ref" / "nf_bench"
+    if not exe.exists():
+        pytest.skip("nf_bench not built (needs the reference sources)")
+    r = subprocess.run([str(exe), "--iterations", "5"], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-3000:], r.stderr[-1000:])
+    assert r.returncode == 0 and "=== Benchmark complete ===" in r.stdout
 
 
 LIFECYCLE = r"""
