@@ -111,7 +111,8 @@ def test_error_codes(provider):
     no_pc = provider.task("dequant_q4_0_linear", [a, w], [c])
     assert provider.dispatch_task(no_pc) == abi.NF_ERROR_INVALID_ARG
     assert provider.dispatch_task(provider.task("dequant_q4_0_linear", [a], [c], 4, 8, 64)) == abi.NF_ERROR_INVALID_ARG
-    assert provider.dispatch_task(provider.task("flash_attention_gqa", [a], [c])) == abi.NF_ERROR_UNSUPPORTED_OP
+    assert provider.dispatch_task(provider.task("sparse_moe_router", [a], [c])) == abi.NF_ERROR_UNSUPPORTED_OP
+    assert provider.dispatch_task(provider.task("flash_attention_gqa", [a], [c])) == abi.NF_ERROR_INVALID_ARG
     provider.synchronize()
     for b in (a, w, c):
         b.release()
