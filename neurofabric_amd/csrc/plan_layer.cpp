@@ -42,6 +42,12 @@ const std::unordered_map<std::string, LayerInfo>& layer_table() {
       {"rms_norm", {Path::RmsNorm, EwFn::Add, AttnMode::Plain, true, true, false}},
       {"rope", {Path::Rope, EwFn::Add, AttnMode::Plain, true, false, false}},
       {"rope_batch", {Path::RopeBatch, EwFn::Add, AttnMode::Plain, true, true, false}},
+      // The name the model layer emits for the f16 rope in fp16 mode
+      // (arch_registry.hpp:140, 298-301; kernel metal_provider.mm:1086-1106).
+      // The Metal dispatch map (metal_provider.mm:3180-3204) has no entry for
+      // it, so there the fp16 rope silently does not run; here it is the f16
+      // rope_batch and takes f16 buffers only.
+      {"rope_batch_f16", {Path::RopeBatch, EwFn::Add, AttnMode::Plain, true, true, false}},
       {"softmax", {Path::Softmax, EwFn::Add, AttnMode::Plain, true, false, false}},
       {"embedding_lookup", {Path::Embedding, EwFn::Add, AttnMode::Plain, true, true, false}},
       {"argmax", {Path::Argmax, EwFn::Add, AttnMode::Plain, true, false, false}},
@@ -207,6 +213,8 @@ nf_status make_layer_plan(const char* op_name, const nf_tensor_desc* const* ins,
   // (is_f16 = out.dtype == F16); ops without one always compute in f32.
   const nf_tensor_desc* out0 = (n_out >= 1 && outs) ? outs[0] : nullptr;
   p.c = (info.f16_capable && out0 && out0->dtype == NF_DTYPE_F16) ? EType::F16 : EType::F32;
+  if (std::strcmp(op_name, "rope_batch_f16") == 0 && p.c != EType::F16)
+    return fail(why, "rope_batch_f16 takes an f16 output");
   p.a = p.b = p.c;
   const uint64_t elt = elt_bytes(p.c);
 

@@ -202,7 +202,12 @@ def test_rope_batch_and_rope(provider, seq, heads, dim, step):
     o.release()
     h = x.astype(np.float16).view(np.uint16)
     (o,) = _run(provider, "rope_batch", [h], [(F16, x.size * 2)], pc)
-    assert _ulp16_ok(_read(o, np.uint16), orc.rope(h, heads, dim, step, 10000.0, f16=True), ulps=1 + tol * 1024)
+    got16 = _read(o, np.uint16)
+    assert _ulp16_ok(got16, orc.rope(h, heads, dim, step, 10000.0, f16=True), ulps=1 + tol * 1024)
+    o.release()
+    # the name the model layer emits in fp16 mode runs the same kernel
+    (o,) = _run(provider, "rope_batch_f16", [h], [(F16, x.size * 2)], pc)
+    assert np.array_equal(_read(o, np.uint16), got16)
     o.release()
     (o,) = _run(provider, "rope", [x], [(F32, x.size * 4)], pc)
     assert np.max(np.abs(_read(o, np.float32) - orc.rope(x, heads, dim, step, 10000.0, batch=False))) < tol

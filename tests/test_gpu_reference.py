@@ -114,3 +114,107 @@ def test_register_init_shutdown_repeated():
     r = subprocess.run([sys.executable, "-c", LIFECYCLE % str(REPO)], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0 and "lifecycle ok" in r.stdout
+
+
+NF_GENERATE = REPO / "oracle" / "_ref" / "nf_generate"
+REF_GGUF = REPO / "oracle" / "_ref" / "ref_gguf"
+
+
+def _llama_prefill_logits(quant, ids, seed, zero_attention=False, f16=False):
+    """Last-position logits of the tiny synthetic model for prompt `ids`,
+    composed from the oracle's restatements of the ops the reference's step
+    graph emits (llama_dag_builder.hpp:1386-1530): embedding, rms_norm, fused
+    Q4_0 / warm-up-dequantized linears, rope_batch, flash_attention_cached,
+    residual adds, silu * up, final norm, lm_head `linear`.  With f16 every
+    activation and dequantized weight is fp16 and each op is its `_f16`
+    variant, as the app's --fp16 mode runs them.
+
+    zero_attention: the paged path of the reference's step graph reads K/V
+    pools that nothing writes (llama_dag_builder.hpp:1185-1194 zero them,
+    :1444-1450 gives flash_attention_paged no new K/V), so its attention
+    output is the weighted sum of zero value rows."""
+    import numpy as np
+
+    from neurofabric_amd import gguf_synth
+    from oracle import oracle as orc
+
+    D, L, H, KVH, F, V, _ = gguf_synth.SHAPES["tiny"]
+    hd, kvd, S, MS = D // H, KVH * (D // H), len(ids), 512
+    W = {n: np.frombuffer(b, np.uint8) for n, _, _, b in gguf_synth.tensors("tiny", quant, seed)}
+    f32 = lambda n: W[n].view(np.float32)  # noqa: E731
+    act = np.uint16 if f16 else np.float32
+
+    def lin(a, name, n, k):
+        return orc.fused(a, W[name], quant, S, n, k, f16=f16)
+
+    x = orc.dequant(W["token_embd.weight"], quant, V * D, f16=f16).reshape(V, D)[ids].astype(act)
+    for l in range(L):
+        b = f"blk.{l}."
+        h = orc.rms_norm(x, f32(b + "attn_norm.weight"), D, 1e-5, f16=f16)
+        q, k, v = lin(h, b + "attn_q.weight", D, D), lin(h, b + "attn_k.weight", kvd, D), lin(h, b + "attn_v.weight", kvd, D)
+        q = orc.rope(q, H, hd, 0, 10000.0, f16=f16)
+        k = orc.rope(k, KVH, hd, 0, 10000.0, f16=f16)
+        kc, vc = np.zeros(KVH * MS * hd, act), np.zeros(KVH * MS * hd, act)
+        att = np.zeros(S * D, act)
+        orc.attention("flash_attention_cached", dict(n_heads=H, n_kv=KVH, head_dim=hd, seq_len=S, step=0,
+                                                     max_seq=MS), q, k, v, k=kc, v=vc, out=att, f16=f16)
+        if zero_attention:
+            att[:] = 0
+        x = orc.binary("add", x, lin(att, b + "attn_output.weight", D, D), f16=f16)
+        h2 = orc.rms_norm(x, f32(b + "ffn_norm.weight"), D, 1e-5, f16=f16)
+        g = orc.unary("silu", lin(h2, b + "ffn_gate.weight", F, D), f16=f16)
+        m = orc.binary("mul", g, lin(h2, b + "ffn_up.weight", F, D), f16=f16)
+        x = orc.binary("add", x, orc.fused(m, W[b + "ffn_down.weight"], quant, S, D, F, f16=f16), f16=f16)
+    hf = orc.rms_norm(x, f32("output_norm.weight"), D, 1e-5, f16=f16)
+    lm = orc.dequant(W["output.weight"], quant, V * D, f16=f16)
+    if f16:
+        return orc.f16_to_f32(orc.linear_f16(hf, lm, S, V, D)[S - 1])
+    return orc.linear_f32(hf, lm, S, V, D)[S - 1]
+
+
+@pytest.mark.skipif(not (NF_GENERATE.exists() and REF_GGUF.exists()),
+                    reason="reference app not built (needs the reference sources)")
+@pytest.mark.parametrize("quant,flags,tol", [
+    ("q4_0", [], 2e-3),            # fused dequant_q4_0_linear + flash_attention_cached
+    ("q8_0", [], 2e-3),            # warm-up dequant_q8_0 + dense linear
+    ("q4_0", ["--paged"], 2e-3),   # flash_attention_paged through the NeuralOS runtime
+    ("q4_0", ["--fp16"], 2e-2),    # f16 activations and f16 layer ops (~10 fp16 ulps at |logit| ~3)
+])
+def test_reference_nf_generate_end_to_end(tmp_path, quant, flags, tol):
+    """apps/nf_generate.cpp, the reference's text-generation app, compiled
+    from its source and linked against this provider: loads a random-weight
+    GGUF through the reference's loader, warms up, prefills, and decodes
+    greedily.  The five largest prefill logits it prints are checked against
+    the oracle's forward pass of the same model (tolerance 2e-3 absolute on
+    logits of magnitude ~3; the fp16 run against the oracle's f16 chain,
+    2e-2).  The printed values carry 4 decimals."""
+    import re
+
+    import numpy as np
+
+    from neurofabric_amd import gguf_synth
+
+    seed = 11
+    path = tmp_path / "tiny.gguf"
+    gguf_synth.write(str(path), "tiny", quant, seed=seed)
+    prompt = "Hello world"
+    tk = subprocess.run([str(REF_GGUF), str(path), prompt], capture_output=True, text=True, timeout=60)
+    assert tk.returncode == 0
+    ids = [int(x) for x in tk.stdout.splitlines()[-2].split()[1:]]
+    print("case", quant, flags, "prompt ids", len(ids), flush=True)
+    r = subprocess.run([str(NF_GENERATE), str(path), prompt, "--max-tokens", "6", "--temperature", "0",
+                        "--seed", "1", *flags], capture_output=True, text=True, errors="replace",
+                       timeout=120)
+    print(r.stdout[-2000:], r.stderr[-4000:])
+    assert r.returncode == 0
+    m = re.search(r"decode: [\d.]+ ms \((\d+) tokens", r.stderr)
+    assert m and int(m.group(1)) >= 1
+    top = [(int(i), float(v)) for i, v in re.findall(r"top\d: id=(\d+) val=(-?[\d.]+)", r.stderr)]
+    assert len(top) == 5
+    ref = _llama_prefill_logits(quant, ids, seed, zero_attention="--paged" in flags, f16="--fp16" in flags)
+    assert np.isfinite(ref).all() and np.abs(ref).max() > 0.1
+    fifth = np.sort(ref)[-5]
+    print("printed top-5 vs oracle:", [(tid, val, round(float(ref[tid]), 4)) for tid, val in top])
+    for tid, val in top:
+        assert abs(ref[tid] - val) <= tol + 1e-4, (tid, val, ref[tid])
+        assert val >= fifth - tol - 1e-4

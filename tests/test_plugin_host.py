@@ -217,6 +217,12 @@ def test_plan_layer_ops(lib):
         plan(lib, "flash_attention_gqa", ins[:3] + [D(F16, 100), D(F16, 100)], [D(F16, 8 * 64 * 2)], pc=pc)
     with pytest.raises(NfError):  # attention without push constants
         plan(lib, "flash_attention_gqa", ins, [D(F16, 8 * 64 * 2)])
+    # rope_batch_f16, the model layer's fp16 rope name: f16 buffers only
+    pc = push_constants(seq_len=2, n_heads=4, head_dim=64, theta=10000.0)
+    p = plan(lib, "rope_batch_f16", [D(F16, 2 * 4 * 64 * 2)], [D(F16, 2 * 4 * 64 * 2)], pc=pc)
+    assert p["kernel"] == "rope_batch_f16"
+    with pytest.raises(NfError):
+        plan(lib, "rope_batch_f16", [D(F32, 2 * 4 * 64 * 4)], [D(F32, 2 * 4 * 64 * 4)], pc=pc)
 
 
 def test_plan_dense_linear_dtypes(lib):
