@@ -378,6 +378,86 @@ hipError_t unary_t(const void* in, void* out, uint64_t n, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ---- MoE (metal_provider.mm:1907-1997) ----------------------------------------
+// Gating: one thread per token, the reference's sequence of operations: max
+// over all n_experts logits, p_i = exp(l_i - max) summed in index order over
+// the first min(n_experts, 64), p_i / sum, then an insertion into the top_k
+// (<= 8) list with a strict '>' (earlier experts win ties, zero or NaN
+// probabilities are never selected), renormalized by the selected sum.  p_i
+// is recomputed instead of stored: the same expf of the same argument.  The
+// list lives in registers: every index below is a compile-time constant.
+__global__ __launch_bounds__(256) void moe_gate_kernel(const float* __restrict__ logits,
+                                                       int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                       uint32_t batch, uint32_t n, uint32_t top_k) {
+  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  const float* l = logits + (size_t)b * n;
+  const uint32_t ne = n < 64 ? n : 64;
+  float mx = n ? l[0] : 0.f;
+  for (uint32_t i = 1; i < n; ++i) mx = l[i] > mx ? l[i] : mx;
+  float sum = 0.f;
+  for (uint32_t i = 0; i < ne; ++i) sum = __fadd_rn(sum, expf(l[i] - mx));
+  int32_t sid[8];
+  float sp[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    sid[k] = -1;
+    sp[k] = 0.f;
+  }
+  for (uint32_t i = 0; i < ne; ++i) {
+    const float p = __fdiv_rn(expf(l[i] - mx), sum);
+    int pos = (int)top_k;  // first slot p beats, or none
+#pragma unroll
+    for (int k = 7; k >= 0; --k)
+      if (k < (int)top_k && p > sp[k]) pos = k;
+    // pos is the FIRST slot whose value p exceeds: the list is kept in
+    // descending order, so every slot after it is exceeded too.
+#pragma unroll
+    for (int k = 7; k >= 1; --k) {
+      const bool shift = k > pos, here = k == pos;
+      sp[k] = shift ? sp[k - 1] : (here ? p : sp[k]);
+      sid[k] = shift ? sid[k - 1] : (here ? (int32_t)i : sid[k]);
+    }
+    if (pos == 0) {
+      sp[0] = p;
+      sid[0] = (int32_t)i;
+    }
+  }
+  float ssum = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < (int)top_k) ssum = __fadd_rn(ssum, sp[k]);
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < (int)top_k) {
+      ids[(size_t)b * top_k + k] = sid[k];
+      wts[(size_t)b * top_k + k] = ssum > 0.f ? __fdiv_rn(sp[k], ssum) : 0.f;
+    }
+}
+
+// Scatter-gather: out[b, d] = sum_k w[b, k] * E[ids[b, k], d] in k order,
+// unfused multiply then add; ids < 0 (unfilled slots) and ids past the rows
+// of E present are skipped.  Threads run along d, so each selected expert
+// row is read with coalesced loads.
+__global__ __launch_bounds__(256) void moe_scatter_kernel(const float* __restrict__ E, uint32_t rows,
+                                                          const int32_t* __restrict__ ids,
+                                                          const float* __restrict__ w, float* __restrict__ out,
+                                                          uint32_t batch, uint32_t top_k, uint32_t dim) {
+  // a rounded multiply, then a rounded add: never fused into one FMA
+#pragma clang fp contract(off)
+  const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= dim) return;
+  for (uint32_t b = blockIdx.y; b < batch; b += gridDim.y) {
+    float v = 0.f;
+    for (uint32_t k = 0; k < top_k; ++k) {
+      const int32_t e = ids[(size_t)b * top_k + k];
+      if (e < 0 || (uint32_t)e >= rows) continue;
+      v += w[(size_t)b * top_k + k] * E[(size_t)e * dim + d];
+    }
+    out[(size_t)b * dim + d] = v;
+  }
+}
+
 }  // namespace layer
 }  // namespace nfk
 
@@ -485,6 +565,23 @@ hipError_t launch_embedding(EType t, const void* w, uint32_t vocab, const void* 
   else
     embedding_kernel<float><<<grid_for(n), kThreads, 0, s>>>((const float*)w, vocab, (const int32_t*)ids,
                                                              (float*)out, n, dim, seq_len);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_gate(const void* logits, void* ids, void* weights, uint32_t batch, uint32_t n_experts,
+                           uint32_t top_k, hipStream_t s) {
+  if (batch == 0 || top_k == 0) return hipSuccess;
+  nfk::layer::moe_gate_kernel<<<(batch + 255) / 256, 256, 0, s>>>((const float*)logits, (int32_t*)ids,
+                                                                    (float*)weights, batch, n_experts, top_k);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_scatter(const void* experts, uint32_t expert_rows, const void* ids, const void* weights,
+                              void* out, uint32_t batch, uint32_t top_k, uint32_t dim, hipStream_t s) {
+  if (batch == 0 || dim == 0) return hipSuccess;
+  const dim3 grid((dim + 255) / 256, batch < 65535u ? batch : 65535u);
+  nfk::layer::moe_scatter_kernel<<<grid, 256, 0, s>>>((const float*)experts, expert_rows, (const int32_t*)ids,
+                                                      (const float*)weights, (float*)out, batch, top_k, dim);
   return hipGetLastError();
 }
 

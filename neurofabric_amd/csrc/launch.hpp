@@ -94,6 +94,13 @@ hipError_t launch_softmax(const void* in, void* out, uint32_t rows, uint32_t dim
                           hipStream_t s);
 hipError_t launch_argmax(const void* in, void* out, uint32_t rows, uint32_t dim, float* ws, size_t ws_floats,
                          hipStream_t s);
+// MoE (metal_provider.mm:1907-1997): per token, softmax over the first
+// min(n_experts, 64) gate logits, the top_k (<= 8) largest in index order of
+// ties, renormalized; and the weighted sum of the selected experts' rows.
+hipError_t launch_moe_gate(const void* logits, void* ids, void* weights, uint32_t batch, uint32_t n_experts,
+                           uint32_t top_k, hipStream_t s);
+hipError_t launch_moe_scatter(const void* experts, uint32_t expert_rows, const void* ids, const void* weights,
+                              void* out, uint32_t batch, uint32_t top_k, uint32_t dim, hipStream_t s);
 hipError_t launch_embedding(EType t, const void* w, uint32_t vocab, const void* ids, void* out, uint64_t n,
                             uint32_t dim, uint32_t seq_len, hipStream_t s);
 

@@ -35,7 +35,9 @@ enum class Path {
   Softmax,
   Embedding,
   Argmax,
-  Attention    // every attention op (causal, cached, flash, gqa, paged)
+  Attention,   // every attention op (causal, cached, flash, gqa, paged)
+  MoeGate,     // moe_top_k_gating
+  MoeScatter   // moe_scatter_gather
 };
 
 // Element-wise functions of the Binary / Unary paths.
@@ -60,6 +62,7 @@ struct LayerParams {
   uint32_t seq_len = 0, n_heads = 0, n_kv = 0, head_dim = 0;
   uint32_t step = 0, max_seq = 0, window = 0;
   uint32_t n_blocks = 0, block_size = 0, q_offset = 0;  // paged attention
+  uint32_t n_experts = 0, top_k = 0;                     // MoE gating / scatter-gather
   uint64_t count2 = 0;  // attention_prefill: elements of the second output
   float eps = 0.f, theta = 0.f;
   bool decode = false;  // attention with step_idx > 0 (one query token)

@@ -56,6 +56,8 @@ const std::unordered_map<std::string, LayerInfo>& layer_table() {
       {"flash_attention_cached", {Path::Attention, EwFn::Add, AttnMode::Cached, true, true, true}},
       {"flash_attention_gqa", {Path::Attention, EwFn::Add, AttnMode::Gqa, true, true, true}},
       {"flash_attention_paged", {Path::Attention, EwFn::Add, AttnMode::Paged, true, false, false}},
+      {"moe_top_k_gating", {Path::MoeGate, EwFn::Add, AttnMode::Plain, true, false, false}},
+      {"moe_scatter_gather", {Path::MoeScatter, EwFn::Add, AttnMode::Plain, true, false, false}},
   };
   return t;
 }
@@ -332,6 +334,41 @@ nf_status make_layer_plan(const char* op_name, const nf_tensor_desc* const* ins,
       p.act_bytes = (uint64_t)lp.rows * lp.dim * 4;
       p.out_bytes = lp.rows * 4ull;
       p.kernel = "argmax_f32";
+      break;
+    }
+    case Path::MoeGate: {
+      // gate logits [batch, n_experts] -> expert ids (int32) and weights (f32),
+      // [batch, top_k] each; batch = seq_len, n_experts = M, top_k = min(N, 8)
+      // (metal_provider.mm:1907-1962, host 3080-3112)
+      if (n_in < 1 || n_out < 2 || !ins[0] || !out0 || !outs[1]) return fail(why, "takes 1 input and 2 outputs");
+      lp.rows = pc.present ? pc.seq_len : 1;
+      lp.n_experts = pc.M;
+      lp.top_k = std::min<uint32_t>(pc.N, 8);
+      p.count = (uint64_t)lp.rows * lp.top_k;
+      if (!fits(ins[0], (uint64_t)lp.rows * lp.n_experts, 4)) return fail(why, "logits hold fewer than seq_len * M floats");
+      if (!fits(out0, p.count, 4) || !fits(outs[1], p.count, 4))
+        return fail(why, "outputs hold fewer than seq_len * min(N, 8) entries");
+      p.act_bytes = (uint64_t)lp.rows * lp.n_experts * 4;
+      p.out_bytes = p.count * 8;
+      p.kernel = "moe_top_k_gating_f32";
+      break;
+    }
+    case Path::MoeScatter: {
+      // expert outputs [rows, dim], ids and weights [batch, top_k] -> out
+      // [batch, dim]; batch = seq_len, top_k = N, dim = K
+      // (metal_provider.mm:1964-1997, host 3114-3150)
+      if (n_in < 3 || n_out < 1 || !ins[0] || !ins[1] || !ins[2] || !out0) return fail(why, "takes 3 inputs and 1 output");
+      lp.rows = pc.present ? pc.seq_len : 1;
+      lp.top_k = pc.N;
+      lp.dim = pc.K;
+      lp.n_experts = lp.dim ? (uint32_t)std::min<uint64_t>(ins[0]->size_bytes / (4ull * lp.dim), 0xFFFFFFFFu) : 0;
+      p.count = (uint64_t)lp.rows * lp.dim;
+      if (!fits(ins[1], (uint64_t)lp.rows * lp.top_k, 4) || !fits(ins[2], (uint64_t)lp.rows * lp.top_k, 4))
+        return fail(why, "ids / weights hold fewer than seq_len * N entries");
+      if (!fits(out0, p.count, 4)) return fail(why, "output holds fewer than seq_len * K floats");
+      p.act_bytes = (uint64_t)lp.rows * lp.top_k * (8 + 4ull * lp.dim);
+      p.out_bytes = p.count * 4;
+      p.kernel = "moe_scatter_gather_f32";
       break;
     }
     case Path::Attention: {

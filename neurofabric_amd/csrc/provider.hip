@@ -515,6 +515,11 @@ hipError_t run_plan(const Plan& pl, Buffer* const* in, Buffer* const* out, int g
     case Path::Embedding:
       return launch_embedding(pl.c, in[0]->dev, pl.lp.rows, in[1]->dev, out[0]->dev, pl.count, pl.lp.dim,
                               pl.lp.seq_len, s);
+    case Path::MoeGate:
+      return launch_moe_gate(in[0]->dev, out[0]->dev, out[1]->dev, pl.lp.rows, pl.lp.n_experts, pl.lp.top_k, s);
+    case Path::MoeScatter:
+      return launch_moe_scatter(in[0]->dev, pl.lp.n_experts, in[1]->dev, in[2]->dev, out[0]->dev, pl.lp.rows,
+                                pl.lp.top_k, pl.lp.dim, s);
     case Path::Argmax:
       return launch_argmax(in[0]->dev, out[0]->dev, pl.lp.rows, pl.lp.dim, ws.part, ws.part_floats, s);
     case Path::Attention: {

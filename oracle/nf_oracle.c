@@ -528,6 +528,64 @@ void nf_oracle_argmax(const float *in, int32_t *out, uint32_t rows, uint32_t dim
     }
 }
 
+/* moe_top_k_gating :1907-1962.  Per token: max over all n_experts logits,
+ * softmax over the first min(n_experts, 64), insertion of each probability
+ * into a descending top_k (<= 8) list at the first slot it strictly exceeds,
+ * renormalization by the selected sum.  n_experts = 0 selects nothing (the
+ * reference reads logits[0] there, which is out of bounds). */
+void nf_oracle_moe_gate(const float *logits, int32_t *ids, float *w, uint32_t batch, uint32_t n_experts,
+                        uint32_t top_k) {
+    if (top_k > 8) top_k = 8;
+    for (uint32_t b = 0; b < batch; ++b) {
+        const float *l = logits + (uint64_t)b * n_experts;
+        float max_val = n_experts ? l[0] : 0.0f;
+        for (uint32_t i = 1; i < n_experts; ++i)
+            if (l[i] > max_val) max_val = l[i];
+        float probs[64], sum = 0.0f;
+        for (uint32_t i = 0; i < n_experts && i < 64; ++i) {
+            probs[i] = expf(l[i] - max_val);
+            sum += probs[i];
+        }
+        for (uint32_t i = 0; i < n_experts && i < 64; ++i) probs[i] /= sum;
+        int32_t sel_ids[8] = {-1, -1, -1, -1, -1, -1, -1, -1};
+        float sel_p[8] = {0};
+        for (uint32_t i = 0; i < n_experts && i < 64; ++i)
+            for (uint32_t k = 0; k < top_k; ++k)
+                if (probs[i] > sel_p[k]) {
+                    for (uint32_t j = top_k - 1; j > k; --j) {
+                        sel_ids[j] = sel_ids[j - 1];
+                        sel_p[j] = sel_p[j - 1];
+                    }
+                    sel_ids[k] = (int32_t)i;
+                    sel_p[k] = probs[i];
+                    break;
+                }
+        float sel_sum = 0.0f;
+        for (uint32_t k = 0; k < top_k; ++k) sel_sum += sel_p[k];
+        for (uint32_t k = 0; k < top_k; ++k) {
+            ids[(uint64_t)b * top_k + k] = sel_ids[k];
+            w[(uint64_t)b * top_k + k] = sel_sum > 0.0f ? sel_p[k] / sel_sum : 0.0f;
+        }
+    }
+}
+
+/* moe_scatter_gather :1964-1997.  out[b, d] = sum over k of w[b,k] *
+ * experts[ids[b,k], d], k in order; ids < 0 are skipped, and so are ids at or
+ * past `rows` (the expert rows present; the reference reads out of bounds). */
+void nf_oracle_moe_scatter(const float *experts, uint32_t rows, const int32_t *ids, const float *w, float *out,
+                           uint32_t batch, uint32_t top_k, uint32_t dim) {
+    for (uint32_t b = 0; b < batch; ++b)
+        for (uint32_t d = 0; d < dim; ++d) {
+            float val = 0.0f;
+            for (uint32_t k = 0; k < top_k; ++k) {
+                const int32_t e = ids[(uint64_t)b * top_k + k];
+                if (e < 0 || (uint32_t)e >= rows) continue;
+                val += w[(uint64_t)b * top_k + k] * experts[(uint64_t)e * dim + d];
+            }
+            out[(uint64_t)b * dim + d] = val;
+        }
+}
+
 /* embedding_lookup :1054-1067 (f16 :1137-1150); a token outside the table's
  * `vocab` rows yields zeros (the reference reads out of bounds there). */
 void nf_oracle_embedding(const void *w, uint32_t vocab, const int32_t *ids, void *out, uint64_t n, uint32_t dim,

@@ -87,6 +87,10 @@ void nf_oracle_rope(const void *in, void *out, uint64_t n, uint32_t n_heads, uin
                     float theta, int batch, int f16);
 void nf_oracle_softmax(const float *in, float *out, uint32_t rows, uint32_t dim);
 void nf_oracle_argmax(const float *in, int32_t *out, uint32_t rows, uint32_t dim);
+void nf_oracle_moe_gate(const float *logits, int32_t *ids, float *w, uint32_t batch, uint32_t n_experts,
+                        uint32_t top_k);
+void nf_oracle_moe_scatter(const float *experts, uint32_t rows, const int32_t *ids, const float *w, float *out,
+                           uint32_t batch, uint32_t top_k, uint32_t dim);
 void nf_oracle_embedding(const void *w, uint32_t vocab, const int32_t *ids, void *out, uint64_t n, uint32_t dim,
                          uint32_t seq_len, int f16);
 /* prm = {mode, variant, n_heads, n_kv, head_dim, seq_len, step, max_seq,

@@ -193,6 +193,8 @@ def _layer_lib():
         L.nf_oracle_rope.argtypes = [vp, vp, u64, u32, u32, u32, f32, i, i]
         L.nf_oracle_softmax.argtypes = [vp, vp, u32, u32]
         L.nf_oracle_argmax.argtypes = [vp, vp, u32, u32]
+        L.nf_oracle_moe_gate.argtypes = [vp, vp, vp, u32, u32, u32]
+        L.nf_oracle_moe_scatter.argtypes = [vp, u32, vp, vp, vp, u32, u32, u32]
         L.nf_oracle_embedding.argtypes = [vp, u32, vp, vp, u64, u32, u32, i]
         L.nf_oracle_attention.argtypes = [vp, i, vp, vp, vp, vp, vp, vp, vp]
         L._layer_ready = True
@@ -246,6 +248,26 @@ def argmax(x, rows: int, dim: int) -> np.ndarray:
     out = np.empty(rows, np.int32)
     _layer_lib().nf_oracle_argmax(a.ctypes.data, out.ctypes.data, rows, dim)
     return out
+
+
+def moe_gate(logits, batch: int, n_experts: int, top_k: int):
+    """(ids int32 [batch, min(top_k, 8)], weights float32 [batch, min(top_k, 8)])."""
+    a = np.ascontiguousarray(logits, np.float32).reshape(-1)
+    k = min(top_k, 8)
+    ids = np.zeros(batch * k, np.int32)
+    w = np.zeros(batch * k, np.float32)
+    _layer_lib().nf_oracle_moe_gate(a.ctypes.data, ids.ctypes.data, w.ctypes.data, batch, n_experts, top_k)
+    return ids.reshape(batch, k), w.reshape(batch, k)
+
+
+def moe_scatter(experts, ids, w, batch: int, top_k: int, dim: int) -> np.ndarray:
+    e = np.ascontiguousarray(experts, np.float32).reshape(-1)
+    ids = np.ascontiguousarray(ids, np.int32).reshape(-1)
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)
+    out = np.zeros(batch * dim, np.float32)
+    _layer_lib().nf_oracle_moe_scatter(e.ctypes.data, e.size // dim if dim else 0, ids.ctypes.data, w.ctypes.data,
+                                       out.ctypes.data, batch, top_k, dim)
+    return out.reshape(batch, dim)
 
 
 def embedding(w, ids, n: int, dim: int, seq_len: int, f16: bool = False, out=None) -> np.ndarray:

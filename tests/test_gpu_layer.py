@@ -334,3 +334,53 @@ def test_attention_rejects_prefill_longer_than_cache(provider):
         provider.dispatch("flash_attention_cached", [q, q, q, c, c], [o], pc=pc)
     for b in (q, c, o):
         b.release()
+
+
+# ---- MoE (metal_provider.mm:1907-1997) -------------------------------------------
+
+@pytest.mark.parametrize("batch,n,top_k", [(1, 8, 2), (37, 64, 8), (300, 100, 4), (5, 3, 12), (4, 6, 4)])
+def test_moe_top_k_gating(provider, batch, n, top_k):
+    rng = _rng(batch + n)
+    if n == 6:   # ties everywhere: the lowest expert ids win
+        logits = np.zeros((batch, n), np.float32)
+    else:        # a 1/16 grid: selections are decided, not rounding accidents
+        logits = (rng.integers(-64, 64, size=(batch, n)) / 16.0).astype(np.float32)
+    k = min(top_k, 8)
+    pc = push_constants(seq_len=batch, M=n, N=top_k)
+    ids_o, w_o = _run(provider, "moe_top_k_gating", [logits], [(I32, batch * k * 4), (F32, batch * k * 4)], pc)
+    ids, w = orc.moe_gate(logits, batch, n, top_k)
+    assert np.array_equal(_read(ids_o, np.int32).reshape(batch, k), ids)
+    # expf of the device and of libm may differ by an ulp: weights to a few ulps
+    assert np.allclose(_read(w_o, np.float32).reshape(batch, k), w, rtol=1e-6, atol=1e-7)
+    ids_o.release()
+    w_o.release()
+
+
+def test_moe_scatter_gather(provider):
+    rng = _rng(77)
+    n_exp, dim, batch, top_k = 8, 4096 + 3, 33, 2
+    E = rng.standard_normal((n_exp, dim)).astype(np.float32)
+    ids = rng.integers(-1, n_exp + 2, size=(batch, top_k)).astype(np.int32)   # includes -1 and ids past the rows
+    w = rng.random((batch, top_k)).astype(np.float32)
+    pc = push_constants(seq_len=batch, M=n_exp, N=top_k, K=dim)
+    (o,) = _run(provider, "moe_scatter_gather", [E, ids, w], [(F32, batch * dim * 4)], pc)
+    assert np.array_equal(_read(o, np.float32).reshape(batch, dim), orc.moe_scatter(E, ids, w, batch, top_k, dim))
+    o.release()
+
+
+def test_moe_gating_then_scatter_chain(provider):
+    """Gate logits -> top-2 ids and weights -> weighted sum of expert rows,
+    buffers passed from one op to the next on the device."""
+    rng = _rng(3)
+    batch, n_exp, dim = 16, 8, 256
+    logits = (rng.integers(-64, 64, size=(batch, n_exp)) / 16.0).astype(np.float32)
+    E = rng.standard_normal((n_exp, dim)).astype(np.float32)
+    ids_o, w_o = _run(provider, "moe_top_k_gating", [logits], [(I32, batch * 8), (F32, batch * 8)],
+                      push_constants(seq_len=batch, M=n_exp, N=2))
+    (o,) = _run(provider, "moe_scatter_gather", [E, ids_o, w_o], [(F32, batch * dim * 4)],
+                push_constants(seq_len=batch, M=n_exp, N=2, K=dim))
+    ids, w = orc.moe_gate(logits, batch, n_exp, 2)
+    want = orc.moe_scatter(E, ids, _read(w_o, np.float32).reshape(batch, 2), batch, 2, dim)
+    assert np.array_equal(_read(o, np.float32).reshape(batch, dim), want)
+    for b in (ids_o, w_o, o):
+        b.release()

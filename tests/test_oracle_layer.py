@@ -296,3 +296,68 @@ def test_planted_mistakes_are_caught():
         mapped = _attn64(q3[:32], kp.reshape(pool_blocks, 16, 32)[table].reshape(-1, 32),
                          vp.reshape(pool_blocks, 16, 32)[table].reshape(-1, 32), (0, 40))
         assert _rel(ident, mapped) > 1e-3
+
+
+# ---- MoE gating / scatter-gather (metal_provider.mm:1907-1997) ------------------
+
+def _gate64(logits, n, top_k):
+    """float64 restatement from the definition: softmax over the first
+    min(n, 64) experts (the max taken over all n), the top_k (<= 8) largest,
+    earlier expert first on ties, zero probabilities never selected,
+    renormalized."""
+    k = min(top_k, 8)
+    ne = min(n, 64)
+    ids = np.full((logits.shape[0], k), -1, np.int64)
+    w = np.zeros((logits.shape[0], k))
+    for b, row in enumerate(logits.astype(np.float64)):
+        p = np.exp(row[:ne] - row.max())
+        p /= p.sum()
+        order = sorted(range(ne), key=lambda i: (-p[i], i))
+        sel = [i for i in order[:k] if p[i] > 0]
+        ids[b, :len(sel)] = sel
+        s = sum(p[i] for i in sel)
+        w[b, :len(sel)] = [p[i] / s for i in sel]
+    return ids, w
+
+
+@pytest.mark.parametrize("n,top_k", [(1, 1), (5, 2), (8, 2), (8, 8), (64, 4), (100, 8), (40, 12)])
+def test_oracle_moe_gate_against_float64(n, top_k):
+    rng = _rng(n * 31 + top_k)
+    # logits on a 1/16 grid: distinct probabilities are >= 6 % apart, so the
+    # selection is decided, not a rounding accident
+    logits = (rng.integers(-64, 64, size=(37, n)) / 16.0).astype(np.float32)
+    ids, w = orc.moe_gate(logits, 37, n, top_k)
+    ids64, w64 = _gate64(logits, n, top_k)
+    assert np.array_equal(ids, ids64)
+    assert np.max(np.abs(w - w64)) < 2e-6
+    assert np.all(ids < 64)                       # experts past the 64th never selected
+    sel = ids >= 0
+    assert np.allclose(np.where(sel, w, 0).sum(1), 1.0, atol=2e-6)
+
+
+def test_oracle_moe_gate_ties_underflow_and_empty():
+    ids, w = orc.moe_gate(np.zeros((2, 6), np.float32), 2, 6, 4)      # all tied: lowest ids, equal weights
+    assert ids.tolist() == [[0, 1, 2, 3]] * 2 and np.allclose(w, 0.25)
+    lg = np.zeros((1, 5), np.float32)
+    lg[0, 3] = 1000.0                                                 # exp(-1000) = 0: never selected
+    ids, w = orc.moe_gate(lg, 1, 5, 3)
+    assert ids.tolist() == [[3, -1, -1]] and w.tolist() == [[1.0, 0.0, 0.0]]
+    ids, w = orc.moe_gate(np.zeros(0, np.float32), 2, 0, 2)            # no experts
+    assert ids.tolist() == [[-1, -1]] * 2 and not w.any()
+    # a planted mistake: '>=' in the insertion would put the LAST tied expert first
+    lg = np.array([[1.0, 1.0, 0.0]], np.float32)
+    assert orc.moe_gate(lg, 1, 3, 1)[0].tolist() == [[0]]
+
+
+def test_oracle_moe_scatter_against_float64():
+    rng = _rng(5)
+    E = rng.standard_normal((6, 40)).astype(np.float32)
+    ids = np.array([[0, 5], [-1, 2], [7, 1], [3, -1]], np.int32)     # -1 and 7 (past the 6 rows) skipped
+    w = rng.random((4, 2)).astype(np.float32)
+    out = orc.moe_scatter(E, ids, w, 4, 2, 40)
+    want = np.zeros((4, 40))
+    for b in range(4):
+        for k in range(2):
+            if 0 <= ids[b, k] < 6:
+                want[b] += float(w[b, k]) * E[ids[b, k]].astype(np.float64)
+    assert np.max(np.abs(out - want)) < 1e-6

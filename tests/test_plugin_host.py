@@ -217,6 +217,18 @@ def test_plan_layer_ops(lib):
         plan(lib, "flash_attention_gqa", ins[:3] + [D(F16, 100), D(F16, 100)], [D(F16, 8 * 64 * 2)], pc=pc)
     with pytest.raises(NfError):  # attention without push constants
         plan(lib, "flash_attention_gqa", ins, [D(F16, 8 * 64 * 2)])
+    # MoE: gating writes ids and weights, [seq_len, min(N, 8)] each
+    pc = push_constants(seq_len=3, M=16, N=12)
+    p = plan(lib, "moe_top_k_gating", [D(F32, 3 * 16 * 4)], [D(abi.NF_DTYPE_I32, 3 * 8 * 4), D(F32, 3 * 8 * 4)], pc=pc)
+    assert (p["kernel"], p["count"]) == ("moe_top_k_gating_f32", 24)
+    with pytest.raises(NfError):  # one output only
+        plan(lib, "moe_top_k_gating", [D(F32, 3 * 16 * 4)], [D(abi.NF_DTYPE_I32, 3 * 8 * 4)], pc=pc)
+    pc = push_constants(seq_len=3, M=16, N=2, K=64)
+    ins = [D(F32, 16 * 64 * 4), D(abi.NF_DTYPE_I32, 3 * 2 * 4), D(F32, 3 * 2 * 4)]
+    p = plan(lib, "moe_scatter_gather", ins, [D(F32, 3 * 64 * 4)], pc=pc)
+    assert (p["kernel"], p["count"]) == ("moe_scatter_gather_f32", 192)
+    with pytest.raises(NfError):  # output smaller than seq_len * K
+        plan(lib, "moe_scatter_gather", ins, [D(F32, 64 * 4)], pc=pc)
     # rope_batch_f16, the model layer's fp16 rope name: f16 buffers only
     pc = push_constants(seq_len=2, n_heads=4, head_dim=64, theta=10000.0)
     p = plan(lib, "rope_batch_f16", [D(F16, 2 * 4 * 64 * 2)], [D(F16, 2 * 4 * 64 * 2)], pc=pc)
@@ -280,3 +292,25 @@ def test_default_switch_points(lib):
     assert _fused(lib, 2, 28672, 8192)["kernel"] == "gemv_q4_0_f32"           # 2 x 8192 x 4 B + sums
     assert _fused(lib, 3, 28672, 8192)["kernel"] == "skinny_mfma_q4_0_f32"    # 4 x 8192 x 4 B > 120 KB
     assert _fused(lib, 16, 4096, 4096)["kernel"] == "skinny_mfma_q4_0_f32"
+
+
+# Every op name of the Metal provider's dispatch map (metal_provider.mm:3180-3209,
+# the dequant names registered from s_dequant_map) plus the model layer's fp16
+# rope name (arch_registry.hpp:140).
+REFERENCE_OP_NAMES = (
+    "argmax attention_prefill causal_attention causal_attention_cached elementwise_mul embedding_lookup "
+    "flash_attention_cached flash_attention_gqa flash_attention_paged gelu linear linear_tiled "
+    "metal_vector_add mock_relu moe_scatter_gather moe_top_k_gating rms_norm rope rope_batch rope_batch_f16 "
+    "silu softmax dequant_q4_0_linear dequant_q4_0_linear_f16 "
+    + " ".join(f"dequant_{f}{s}" for f in ("q4_0", "q8_0", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q4_k",
+                                           "q5_k", "q6_k") for s in ("", "_f16"))).split()
+
+
+@pytest.mark.parametrize("op", REFERENCE_OP_NAMES)
+def test_every_reference_op_name_is_served(lib, op):
+    """No name the reference's engine or model layer dispatches comes back
+    NF_ERROR_UNSUPPORTED_OP: with no buffers the planner answers
+    NF_ERROR_INVALID_ARG (arity) instead."""
+    with pytest.raises(NfError) as e:
+        plan(lib, op, [], [])
+    assert e.value.status == abi.NF_ERROR_INVALID_ARG, op
