@@ -247,6 +247,185 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(Params p) {
   }
 }
 
+// Prefill, many queries per workgroup: a workgroup takes kQB consecutive
+// query tokens of one head, and every 64-key tile of K and V is staged once
+// in LDS for all of them (f32; K transposed, Kt[d][key], so a lane scoring
+// key `lane` reads consecutive words).  Each wave scores and accumulates
+// kQW = 4 queries at once: per d, four K words feed 16 FMAs; per key, one
+// broadcast float4 of weights feeds 4 x R FMAs.  The per-query arithmetic is
+// the per-(query, head) kernel's online softmax over the same tiles.
+// head_dim <= 128 and a multiple of 4; not for paged pools or decode.
+constexpr int kQB = 16, kQW = 4, kMqDim = 128;
+
+template <typename T>
+struct Vec4 {
+  typedef T type __attribute__((ext_vector_type(4)));
+};
+
+template <typename T, nfhip::AttnMode MODE>
+__global__ __launch_bounds__(256) void attention_mq_kernel(Params p) {
+  __shared__ float Kt[kMqDim * kTile];
+  __shared__ float Vs[kTile * kMqDim];
+  __shared__ float qs[kQB * kMqDim];
+  __shared__ float4v ps[4][kTile];
+
+  typedef typename Vec4<T>::type T4;
+  const uint32_t h = blockIdx.y;
+  const uint32_t kvh = (uint32_t)((uint64_t)h * p.n_kv / p.n_heads);
+  const uint32_t D = p.dim, D4 = D / 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t q0 = blockIdx.x * kQB;
+  const uint32_t q1 = q0 + kQB < p.seq_len ? q0 + kQB : p.seq_len;
+  const T* Q = static_cast<const T*>(p.q);
+  const T* K = static_cast<const T*>(p.k);
+  const T* V = static_cast<const T*>(p.v);
+
+  auto lo_of = [&](uint32_t pos) -> uint32_t {
+    if constexpr (MODE == nfhip::AttnMode::Cached)
+      if (p.window > 0 && pos >= p.window) return pos - p.window + 1;
+    return 0u;
+  };
+  const uint32_t lo_blk = lo_of(q0), hi_blk = q1 - 1;
+
+  for (uint32_t i = tid; i < kQB * D4; i += 256) {
+    const uint32_t qq = i / D4, c = i % D4;
+    float4v v = {0.f, 0.f, 0.f, 0.f};
+    if (q0 + qq < q1) {
+      const T4 x = *reinterpret_cast<const T4*>(Q + q_row<MODE>(p, q0 + qq, h) + 4 * c);
+      v = float4v{f(x[0]), f(x[1]), f(x[2]), f(x[3])};
+    }
+    *reinterpret_cast<float4v*>(&qs[qq * kMqDim + 4 * c]) = v;
+  }
+
+  constexpr int R = kMqDim / 64;
+  float acc[kQW][R], m[kQW], l[kQW];
+  uint32_t qpos[kQW], qlo[kQW];
+  bool qok[kQW];
+#pragma unroll
+  for (int i = 0; i < kQW; ++i) {
+    qpos[i] = q0 + wave * kQW + i;
+    qok[i] = qpos[i] < q1;
+    qlo[i] = lo_of(qpos[i]);
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[i][r] = 0.f;
+  }
+
+  // The next tile's K and V are loaded into registers while the current
+  // one is computed.  Every load is unconditional: a key past the block's
+  // last query reads that query's row and a chunk past the row reads its
+  // last chunk (both in bounds); stage() writes zeros for them instead.
+  constexpr int kLd = kTile * (kMqDim / 4) / 256;
+  T4 kr[kLd], vr[kLd];
+  auto fetch = [&](int64_t t0) {
+#pragma unroll
+    for (int u = 0; u < kLd; ++u) {
+      const uint32_t i = tid + 256 * u;
+      const uint32_t kkey = i & (kTile - 1), kc = i / kTile < D4 ? i / kTile : D4 - 1;
+      const int64_t kt = t0 + kkey <= (int64_t)hi_blk ? t0 + kkey : (int64_t)hi_blk;
+      kr[u] = *reinterpret_cast<const T4*>(K + kv_row<MODE>(p, kvh, (uint32_t)kt) + 4 * kc);
+      const uint32_t vkey = i / D4 < (uint32_t)kTile ? i / D4 : kTile - 1, vc = i % D4;
+      const int64_t vt = t0 + vkey <= (int64_t)hi_blk ? t0 + vkey : (int64_t)hi_blk;
+      vr[u] = *reinterpret_cast<const T4*>(V + kv_row<MODE>(p, kvh, (uint32_t)vt) + 4 * vc);
+    }
+  };
+  auto stage = [&](int64_t t0) {
+#pragma unroll
+    for (int u = 0; u < kLd; ++u) {
+      const uint32_t i = tid + 256 * u;
+      if (i >= kTile * D4) break;  // uniform per unrolled step only at the tail
+      const uint32_t kkey = i & (kTile - 1), kc = i / kTile;
+      const bool kin = t0 + kkey <= (int64_t)hi_blk;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Kt[(4 * kc + j) * kTile + kkey] = kin ? f(kr[u][j]) : 0.f;
+      const uint32_t vkey = i / D4, vc = i % D4;
+      const bool vin = t0 + vkey <= (int64_t)hi_blk;
+      *reinterpret_cast<float4v*>(&Vs[vkey * kMqDim + 4 * vc]) =
+          vin ? float4v{f(vr[u][0]), f(vr[u][1]), f(vr[u][2]), f(vr[u][3])} : float4v{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  fetch(lo_blk);
+  for (int64_t t0 = lo_blk; t0 <= (int64_t)hi_blk; t0 += kTile) {
+    __syncthreads();  // the previous tile's readers are done
+    stage(t0);
+    __syncthreads();
+    if (t0 + kTile <= (int64_t)hi_blk) fetch(t0 + kTile);
+
+    // scores of key t0 + lane for the wave's queries
+    float s[kQW];
+#pragma unroll
+    for (int i = 0; i < kQW; ++i) s[i] = 0.f;
+    const float* qw = &qs[wave * kQW * kMqDim];
+    for (uint32_t d = 0; d < D; d += 4) {
+      const float k0 = Kt[d * kTile + lane], k1 = Kt[(d + 1) * kTile + lane];
+      const float k2 = Kt[(d + 2) * kTile + lane], k3 = Kt[(d + 3) * kTile + lane];
+#pragma unroll
+      for (int i = 0; i < kQW; ++i) {
+        const float4v qv = *reinterpret_cast<const float4v*>(&qw[i * kMqDim + d]);
+        s[i] += qv[0] * k0;
+        s[i] += qv[1] * k1;
+        s[i] += qv[2] * k2;
+        s[i] += qv[3] * k3;
+      }
+    }
+    const int64_t t = t0 + lane;
+    float pw[kQW];
+#pragma unroll
+    for (int i = 0; i < kQW; ++i) {
+      const bool in = qok[i] && t >= (int64_t)qlo[i] && t <= (int64_t)qpos[i];
+      const float si = in ? s[i] * p.scale : -INFINITY;
+      float tmax = si;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o));
+      if (tmax == -INFINITY) {  // no key of this tile for query i (uniform)
+        pw[i] = 0.f;
+        continue;
+      }
+      const float m_new = fmaxf(m[i], tmax);
+      const float corr = expf(m[i] - m_new);
+      pw[i] = in ? expf(si - m_new) : 0.f;
+      float psum = pw[i];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) psum += __shfl_xor(psum, o);
+      l[i] = l[i] * corr + psum;
+      m[i] = m_new;
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[i][r] *= corr;
+    }
+    ps[wave][lane] = float4v{pw[0], pw[1], pw[2], pw[3]};
+    __builtin_amdgcn_wave_barrier();
+    // keys past the wave's last query are no query's; keys between its
+    // queries carry weight 0 for the earlier ones
+    const int64_t wlast = (int64_t)(qok[kQW - 1] ? qpos[kQW - 1] : hi_blk);
+    const int nk = (int)((wlast - t0 + 1) < kTile ? (wlast - t0 + 1) : kTile);
+    for (int j = 0; j < nk; ++j) {
+      const float4v pj = ps[wave][j];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float v = Vs[j * kMqDim + lane + 64 * r];
+#pragma unroll
+        for (int i = 0; i < kQW; ++i) acc[i][r] += pj[i] * v;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  T* O = static_cast<T*>(p.out);
+#pragma unroll
+  for (int i = 0; i < kQW; ++i) {
+    if (!qok[i]) continue;
+    const float inv = l[i] > 0.f ? 1.0f / l[i] : 0.f;
+    const uint64_t orow = q_row<MODE>(p, qpos[i], h);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t d = lane + 64 * r;
+      if (d < D) O[orow + d] = (T)(acc[i][r] * inv);
+    }
+  }
+}
+
 // Append K_new / V_new rows to the caches: prefill rows 0..seq_len-1, decode
 // row `step`.  Cached: K_new [tokens, n_kv, dim]; Gqa: [n_kv, tokens, dim].
 template <typename T, bool HEAD_MAJOR>
@@ -642,10 +821,21 @@ hipError_t run(const Params& p, uint32_t nq, float* ws, size_t ws_floats, hipStr
     }
   }
   // decode: one query per head, so more waves per workgroup split the keys
-  if (p.decode)
+  if (p.decode) {
     attention_kernel<T, MODE, 16><<<dim3(nq, p.n_heads), 1024, 0, s>>>(p);
-  else
-    attention_kernel<T, MODE, 4><<<dim3(nq, p.n_heads), 256, 0, s>>>(p);
+    return hipGetLastError();
+  }
+  if constexpr (MODE != nfhip::AttnMode::Paged) {
+    // many queries per workgroup when the tiles fit and the rows allow
+    // 4-element vector loads
+    const bool aligned = ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k) |
+                           reinterpret_cast<uintptr_t>(p.v) | reinterpret_cast<uintptr_t>(p.out)) % 16) == 0;
+    if (p.dim <= (uint32_t)kMqDim && p.dim % 4 == 0 && aligned && nq >= 2) {
+      attention_mq_kernel<T, MODE><<<dim3((nq + kQB - 1) / kQB, p.n_heads), 256, 0, s>>>(p);
+      return hipGetLastError();
+    }
+  }
+  attention_kernel<T, MODE, 4><<<dim3(nq, p.n_heads), 256, 0, s>>>(p);
   return hipGetLastError();
 }
 

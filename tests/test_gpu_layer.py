@@ -284,6 +284,11 @@ def _attn_case(provider, op, f16, H, KV, D, S, step, max_seq, window=0, bs=16, n
 
 GPU_ATTN = [
     ("causal_attention", False, dict(H=4, KV=4, D=64, S=50, step=0, max_seq=0)),
+    # prefill shapes of the many-queries-per-workgroup kernel: a partial last
+    # query block, head_dim below 128, and head_dim 256 (the per-query kernel)
+    ("flash_attention_gqa", True, dict(H=16, KV=4, D=128, S=100, step=0, max_seq=128)),
+    ("causal_attention_cached", False, dict(H=4, KV=2, D=96, S=33, step=0, max_seq=40)),
+    ("flash_attention_cached", False, dict(H=2, KV=1, D=256, S=20, step=0, max_seq=32)),
     ("causal_attention_cached", False, dict(H=8, KV=2, D=64, S=70, step=0, max_seq=80)),
     ("causal_attention_cached", False, dict(H=8, KV=2, D=128, S=1, step=300, max_seq=512, window=100)),
     ("flash_attention_cached", False, dict(H=4, KV=4, D=128, S=130, step=0, max_seq=160, window=40)),
