@@ -397,7 +397,9 @@ __global__ __launch_bounds__(256) void attention_mq_kernel(Params p) {
     ps[wave][lane] = float4v{pw[0], pw[1], pw[2], pw[3]};
     __builtin_amdgcn_wave_barrier();
     // keys past the wave's last query are no query's; keys between its
-    // queries carry weight 0 for the earlier ones
+    // queries carry weight 0 for the earlier ones (their value rows are
+    // multiplied by that 0, so a non-finite value there would reach the
+    // earlier queries as NaN; the per-query kernel never reads such rows)
     const int64_t wlast = (int64_t)(qok[kQW - 1] ? qpos[kQW - 1] : hi_blk);
     const int nk = (int)((wlast - t0 + 1) < kTile ? (wlast - t0 + 1) : kTile);
     for (int j = 0; j < nk; ++j) {
