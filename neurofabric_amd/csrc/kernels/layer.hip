@@ -119,6 +119,45 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const T* __restrict_
   for (uint32_t j = threadIdx.x; j < dim; j += kThreads) out[base + j] = (T)((float)in[base + j] * rms * w[j]);
 }
 
+// The same with the row held in registers: 16-byte loads (NC per thread,
+// all issued before the sum; a chunk past the row re-reads the row's last
+// chunk and counts 0), then 16-byte stores.  dim % (16 / sizeof(T)) == 0.
+template <typename T, int NC>
+__global__ __launch_bounds__(kThreads) void rms_norm_vec_kernel(const T* __restrict__ in,
+                                                                const float* __restrict__ w,
+                                                                T* __restrict__ out, uint32_t dim, float eps) {
+  constexpr int VW = 16 / sizeof(T);
+  typedef T VecT __attribute__((ext_vector_type(VW)));
+  __shared__ float red[4];
+  const uint64_t base = (uint64_t)blockIdx.x * dim;
+  VecT v[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t j = (c * kThreads + threadIdx.x) * VW;
+    v[c] = *reinterpret_cast<const VecT*>(in + base + (j < dim ? j : dim - VW));
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t j = (c * kThreads + threadIdx.x) * VW;
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) part += (float)v[c][e] * (float)v[c][e];
+    ss += j < dim ? part : 0.0f;
+  }
+  ss = block_sum(ss, red);
+  const float rms = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t j = (c * kThreads + threadIdx.x) * VW;
+    if (j >= dim) continue;
+    VecT o;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) o[e] = (T)((float)v[c][e] * rms * w[j + e]);
+    *reinterpret_cast<VecT*>(out + base + j) = o;
+  }
+}
+
 // softmax over rows of `dim` (metal_provider.mm:1002-1030).
 __global__ __launch_bounds__(kThreads) void softmax_kernel(const float* __restrict__ in, float* __restrict__ out,
                                                            uint32_t dim) {
@@ -496,6 +535,25 @@ hipError_t launch_rms_norm(EType t, const void* in, const void* w, void* out, ui
                            hipStream_t s) {
   if (rows == 0) return hipSuccess;
   using namespace nfk::layer;
+  // rows held in registers when they split into 16-byte chunks, at most 8
+  // per thread (8192 f16 / 4096 f32 elements per 4 chunks, twice that for 8)
+  const uint32_t vw = t == EType::F16 ? 8u : 4u;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) % 16) == 0;
+  const uint32_t chunks = (dim + kThreads * vw - 1) / (kThreads * vw);
+  if (aligned && dim % vw == 0 && dim >= vw && chunks <= 8) {
+    const int nc = chunks <= 1 ? 1 : chunks <= 2 ? 2 : chunks <= 4 ? 4 : 8;
+#define NF_RMS_VEC(TT, NC)                                                                                      \
+  rms_norm_vec_kernel<TT, NC><<<rows, kThreads, 0, s>>>((const TT*)in, (const float*)w, (TT*)out, dim, eps)
+    if (t == EType::F16) {
+      if (nc == 1) NF_RMS_VEC(half_t, 1); else if (nc == 2) NF_RMS_VEC(half_t, 2);
+      else if (nc == 4) NF_RMS_VEC(half_t, 4); else NF_RMS_VEC(half_t, 8);
+    } else {
+      if (nc == 1) NF_RMS_VEC(float, 1); else if (nc == 2) NF_RMS_VEC(float, 2);
+      else if (nc == 4) NF_RMS_VEC(float, 4); else NF_RMS_VEC(float, 8);
+    }
+#undef NF_RMS_VEC
+    return hipGetLastError();
+  }
   if (t == EType::F16)
     rms_norm_kernel<half_t><<<rows, kThreads, 0, s>>>((const half_t*)in, (const float*)w, (half_t*)out, dim, eps);
   else

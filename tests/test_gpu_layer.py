@@ -113,7 +113,10 @@ def test_attention_prefill_mock(provider):
 
 # ---- norms, softmax, argmax, embedding, rope ------------------------------------------
 
-@pytest.mark.parametrize("rows,dim", [(1, 2048), (7, 64), (16, 4096), (3, 5000)])
+# rows held in registers (16-byte chunks: 1, 2, 4 or 8 per thread, partial
+# last chunks), and the element-wise kernel for widths that do not split
+@pytest.mark.parametrize("rows,dim", [(1, 2048), (7, 64), (16, 4096), (3, 5000), (2, 8192), (5, 12), (4, 30),
+                                      (2, 16384)])
 def test_rms_norm(provider, rows, dim):
     x = _rng(dim).standard_normal(rows * dim).astype(np.float32)
     w = _rng(dim + 1).standard_normal(dim).astype(np.float32)
