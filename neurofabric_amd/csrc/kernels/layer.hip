@@ -393,6 +393,26 @@ __global__ __launch_bounds__(kThreads) void embedding_kernel(const T* __restrict
   out[id] = (tok >= 0 && (uint32_t)tok < vocab) ? w[(uint64_t)tok * dim + id % dim] : (T)0.0f;
 }
 
+// The same in 16-byte chunks (rows of dim % (16 / sizeof(T)) == 0, so no
+// chunk straddles two rows): a thread copies one chunk of one token's row.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void embedding_vec_kernel(const T* __restrict__ w, uint32_t vocab,
+                                                                 const int32_t* __restrict__ ids,
+                                                                 T* __restrict__ out, uint64_t nchunks,
+                                                                 uint32_t row_chunks, uint32_t seq_len) {
+  constexpr int VW = 16 / sizeof(T);
+  typedef T VecT __attribute__((ext_vector_type(VW)));
+  const uint64_t id = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (id >= nchunks) return;
+  const uint64_t t = id / row_chunks;
+  if (t >= seq_len) return;
+  const int32_t tok = ids[t];
+  VecT v = {};
+  if (tok >= 0 && (uint32_t)tok < vocab)
+    v = reinterpret_cast<const VecT*>(w)[(uint64_t)tok * row_chunks + id % row_chunks];
+  reinterpret_cast<VecT*>(out)[id] = v;
+}
+
 inline dim3 grid_for(uint64_t threads) { return dim3((unsigned)((threads + kThreads - 1) / kThreads)); }
 
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -617,6 +637,17 @@ hipError_t launch_embedding(EType t, const void* w, uint32_t vocab, const void* 
                             uint32_t dim, uint32_t seq_len, hipStream_t s) {
   if (n == 0) return hipSuccess;
   using namespace nfk::layer;
+  const uint32_t vw = t == EType::F16 ? 8u : 4u;
+  if (dim % vw == 0 && n % vw == 0 && a16(w) && a16(out)) {
+    const uint64_t nc = n / vw;
+    if (t == EType::F16)
+      embedding_vec_kernel<half_t><<<grid_for(nc), kThreads, 0, s>>>((const half_t*)w, vocab, (const int32_t*)ids,
+                                                                      (half_t*)out, nc, dim / vw, seq_len);
+    else
+      embedding_vec_kernel<float><<<grid_for(nc), kThreads, 0, s>>>((const float*)w, vocab, (const int32_t*)ids,
+                                                                     (float*)out, nc, dim / vw, seq_len);
+    return hipGetLastError();
+  }
   if (t == EType::F16)
     embedding_kernel<half_t><<<grid_for(n), kThreads, 0, s>>>((const half_t*)w, vocab, (const int32_t*)ids,
                                                               (half_t*)out, n, dim, seq_len);

@@ -178,8 +178,9 @@ def test_argmax_width_zero_and_softmax_width_zero(provider):
         b.release()
 
 
-def test_embedding_lookup(provider):
-    vocab, dim, seq = 1000, 256, 12
+@pytest.mark.parametrize("dim", [256, 12, 7])  # 16-byte chunks (both types), f32 only, neither
+def test_embedding_lookup(provider, dim):
+    vocab, seq = 1000, 12
     w = _rng(5).standard_normal(vocab * dim).astype(np.float32)
     ids = np.array([0, 999, 5, 5, 17, -3, 1000, 123, 456, 789, 1, 2], np.int32)
     pc = push_constants(seq_len=seq, head_dim=dim)
