@@ -350,21 +350,24 @@ __global__ __launch_bounds__(64) void argmax_merge_kernel(const float* __restric
 // rope: every row at pos = step (metal_provider.mm:104-122, with the rotation
 // the kernel intends for both halves of each row).
 // One thread per (group of rows at one position, pair p): the rotation of
-// pair p is computed once and applied to every row of the group (the
-// n_heads rows of a token for rope_batch, up to kRopeRows rows for rope).
-constexpr uint32_t kRopeRows = 32;
+// pair p is computed once and applied to every row of the group (up to
+// kRopeRows of the n_heads rows of a token for rope_batch, a divisor of
+// n_heads so no group spans two tokens; kRopeRows rows for rope).  Small
+// groups keep many threads in flight: each row is a dependent load / store.
+constexpr uint32_t kRopeRows = 8;
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void rope_kernel(const T* __restrict__ in, T* __restrict__ out, uint64_t rows,
-                                                        uint32_t head_dim, uint32_t rows_per_group, uint32_t step,
-                                                        float theta, bool batch) {
+                                                        uint32_t head_dim, uint32_t rows_per_group,
+                                                        uint32_t rows_per_pos, uint32_t step, float theta,
+                                                        bool batch) {
   const uint32_t half = head_dim / 2;
   const uint64_t id = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
   const uint64_t grp = id / half;
   const uint32_t pair = (uint32_t)(id % half);
   const uint64_t r0 = grp * rows_per_group;
   if (r0 >= rows) return;
-  const uint64_t pos = batch ? grp + step : step;
+  const uint64_t pos = batch ? r0 / rows_per_pos + step : step;
   const float freq = 1.0f / powf(theta, (float)(2 * pair) / (float)head_dim);
   const float angle = (float)pos * freq;
   float s, c;
@@ -586,15 +589,20 @@ hipError_t launch_rope(EType t, bool batch, const void* in, void* out, uint64_t 
   if (n == 0) return hipSuccess;
   using namespace nfk::layer;
   const uint64_t rows = n / head_dim;
-  const uint32_t per = batch ? n_heads : kRopeRows;  // rows sharing one position
+  if (batch && n_heads == 0) return hipErrorInvalidValue;  // the planner rejects it first
+  uint32_t per = kRopeRows;  // rows sharing one position and one rotation
+  if (batch) {
+    per = n_heads < kRopeRows ? n_heads : kRopeRows;
+    while (n_heads % per) --per;
+  }
   const uint64_t groups = (rows + per - 1) / per;
   const uint64_t threads = groups * (head_dim / 2);
   if (t == EType::F16)
     rope_kernel<half_t><<<grid_for(threads), kThreads, 0, s>>>((const half_t*)in, (half_t*)out, rows, head_dim, per,
-                                                               step, theta, batch);
+                                                               n_heads, step, theta, batch);
   else
-    rope_kernel<float><<<grid_for(threads), kThreads, 0, s>>>((const float*)in, (float*)out, rows, head_dim, per, step,
-                                                              theta, batch);
+    rope_kernel<float><<<grid_for(threads), kThreads, 0, s>>>((const float*)in, (float*)out, rows, head_dim, per,
+                                                              n_heads, step, theta, batch);
   return hipGetLastError();
 }
 
