@@ -270,33 +270,80 @@ def time_dispatches(prov, st: Step, steps: int) -> dict:
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline (the oracle: restated reference CPU dequant + sequential-k loop)
+# CPU baseline: the reference's own CPU dequant + naive loop
+# (dequant_test.cpp:112-128, 313-319), compiled from the reference's source by
+# oracle/Makefile into oracle/_ref/libnfref_cpu_*.so; the oracle's restatement
+# of the same path when that library was not built.
 
-def cpu_baseline(threads: int, seconds: float) -> dict:
+REF_CPU_LIBS = {"v3": REPO / "oracle" / "_ref" / "libnfref_cpu_v3.so",
+                "release": REPO / "oracle" / "_ref" / "libnfref_cpu_release.so"}
+REF_CPU_FLAGS = {"v3": "g++ -O3 -DNDEBUG -march=x86-64-v3 -std=c++20",
+                 "release": "g++ -O3 -DNDEBUG -std=c++20 (the reference's Release flags)"}
+
+
+def _host_has(*flags) -> bool:
+    try:
+        text = Path("/proc/cpuinfo").read_text()
+    except OSError:
+        return False
+    line = next((l for l in text.splitlines() if l.startswith("flags")), "")
+    have = set(line.split(":", 1)[-1].split())
+    return all(f in have for f in flags)
+
+
+def _ref_cpu(variant: str):
+    path = REF_CPU_LIBS[variant]
+    if not path.exists() or (variant == "v3" and not _host_has("avx2", "fma", "bmi2")):
+        return None
+    L = C.CDLL(str(path))
+    L.nfref_cpu_fused.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p] + [C.c_uint32] * 6
+    L.nfref_cpu_fused.restype = C.c_int
+    return L
+
+
+def cpu_baseline(threads: int, seconds: float, variant: str = "v3") -> dict:
+    """configs[1] decode steps (155 Q4_0 linears at M=1) on the host cores,
+    repeated for about `seconds`; GB/s of algorithmic bytes."""
     from neurofabric_amd import synthetic as syn
-    from oracle import oracle as orc
+    ref = _ref_cpu(variant)
+    if ref is None and variant == "v3":
+        variant = "release"
+        ref = _ref_cpu(variant)
     shapes = syn.tinyllama_step_shapes()
     cache = {}
     for _, N, K in shapes:
         if (N, K) not in cache:
-            cache[(N, K)] = (syn.q4_0_weights(N, K, seed=N * 7 + K), syn.activations(1, K, seed=K))
+            cache[(N, K)] = (syn.q4_0_weights(N, K, seed=N * 7 + K), syn.activations(1, K, seed=K),
+                             np.zeros(N, np.float32))
     step_bytes = sum(cache[(N, K)][0].nbytes + K * 4 + N * 4 for _, N, K in shapes)
+    if ref is not None:
+        def linear(W, A, out, N, K):
+            if ref.nfref_cpu_fused(0, A.ctypes.data, W.ctypes.data, out.ctypes.data, 1, N, K, 0, N, threads) != 0:
+                raise RuntimeError("nfref_cpu_fused rejected its arguments")
+        kind, what = "reference", (f"the reference's own ref_dequant_q4_0 and naive fp32 loop "
+                                   f"(dequant_test.cpp:112-128, 313-319) built from its source with "
+                                   f"{REF_CPU_FLAGS[variant]}")
+    else:
+        from oracle import oracle as orc
+
+        def linear(W, A, out, N, K):
+            orc.fused(A, W, "q4_0", 1, N, K, threads=threads)
+        kind, what = "port", "the oracle's restatement of the reference CPU path (dequant + sequential-k fp32 loop)"
     reps = 0
     t0 = time.perf_counter()
     while True:
         for _, N, K in shapes:
-            W, A = cache[(N, K)]
-            orc.fused(A, W, "q4_0", 1, N, K, threads=threads)
+            W, A, out = cache[(N, K)]
+            linear(W, A, out, N, K)
         reps += 1
         if time.perf_counter() - t0 >= seconds:
             break
     dt = time.perf_counter() - t0
-    return {"value": step_bytes * reps / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "seconds": dt, "steps": reps, "tokens_per_s": reps / dt,
+    return {"value": step_bytes * reps / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+            "seconds": dt, "steps": reps, "tokens_per_s": reps / dt, "build": variant if ref else "oracle",
             "sample": f"{reps} whole configs[1] decode steps (155 Q4_0 linears, M=1, f32 activations, "
-                      f"{step_bytes / 1e6:.1f} MB of algorithmic bytes each) through the oracle's "
-                      f"restatement of the reference CPU path (dequant + sequential-k fp32 loop), "
-                      f"{threads} thread(s), {dt:.1f} s"}
+                      f"{step_bytes / 1e6:.1f} MB of algorithmic bytes each) through {what}, "
+                      f"{threads} thread(s), rows of N split across threads, {dt:.1f} s"}
 
 
 # ---------------------------------------------------------------------------
@@ -398,22 +445,27 @@ def run_c2(prov) -> dict:
 DQ_FORMATS = ["q4_0", "q8_0", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q4_k", "q5_k", "q6_k"]
 
 
-def run_dq(prov, n_elems: int = 11008 * 4096, copies: int = 2) -> dict:
+ROTATE_BYTES = 512 << 20  # 2x the 256 MB Infinity Cache
+
+
+def run_dq(prov, n_elems: int = 11008 * 4096) -> dict:
     """Standalone dequantization (the weight-upload warm-up path) of one
     Llama-2-7B FFN weight (11008 x 4096 elements) in every block format, to
-    f16 and f32, over `copies` distinct input/output buffer pairs per format
-    (each pair 115..205 MB, so consecutive launches do not hit in cache).
-    Achieved bandwidth counts the algorithmic bytes: blocks read + output
-    written."""
+    f16 and f32, over as many distinct input/output buffer pairs per format
+    as make >= 512 MB together (each pair 115..205 MB), so no launch finds
+    its bytes in the Infinity Cache.  Achieved bandwidth counts the
+    algorithmic bytes: blocks read + output written."""
     from neurofabric_amd import abi, synthetic as syn
     res = {}
     for fmt in DQ_FORMATS:
-        _, be = syn.KQ_GEOM[fmt]
+        bs, be = syn.KQ_GEOM[fmt]
         blocks = syn.kquant_blocks(fmt, n_elems // be, seed=len(res))
         qdt = getattr(abi, f"NF_DTYPE_{fmt.upper()}")
         for f16 in (True, False):
             st = Step(prov)
             odt = abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32
+            pair = blocks.nbytes + n_elems * (2 if f16 else 4)
+            copies = max(2, -(-ROTATE_BYTES // pair))
             for _ in range(copies):
                 w = prov.alloc_array(blocks, qdt)
                 o = prov.alloc(odt, n_elems * (2 if f16 else 4))
@@ -425,6 +477,7 @@ def run_dq(prov, n_elems: int = 11008 * 4096, copies: int = 2) -> dict:
             res[f"{fmt}_{'f16' if f16 else 'f32'}"] = {"GB_s": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
                                                        "us_per_launch": r["us_per_launch"],
                                                        "bytes_per_launch": st.bytes / copies,
+                                                       "rotated_MB": copies * pair / 1e6,
                                                        "kernel": sorted(st.kernels)[0]}
             log(f"[bench] dequant {fmt} {'f16' if f16 else 'f32'}: {gbs:.0f} GB/s, {r['us_per_launch']:.1f} us")
             st.release()
@@ -629,11 +682,15 @@ def main(argv=None) -> int:
     if not args.no_cpu:
         log("[bench] cpu baseline (1 thread) ...")
         cpu = cpu_baseline(1, args.cpu_seconds)
-        log(f"[bench] cpu 1 thread: {cpu['value']:.3f} GB/s over {cpu['seconds']:.1f} s")
+        log(f"[bench] cpu 1 thread: {cpu['value']:.3f} GB/s over {cpu['seconds']:.1f} s ({cpu['kind']})")
         ncores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
         allc = cpu_baseline(min(ncores, 64), min(args.cpu_seconds, 5.0))
         extra["cpu_all_cores"] = allc
         log(f"[bench] cpu {allc['cores']} threads: {allc['value']:.3f} GB/s")
+        if cpu.get("build") == "v3":
+            rel = cpu_baseline(1, min(args.cpu_seconds, 5.0), variant="release")
+            extra["cpu_release_flags_1_thread"] = rel
+            log(f"[bench] cpu 1 thread, reference Release flags: {rel['value']:.3f} GB/s")
 
     pmc = load_pmc_summary()
     traffic = None

@@ -397,19 +397,39 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
     }
     ps[wave][lane] = float4v{pw[0], pw[1], pw[2], pw[3]};
     __builtin_amdgcn_wave_barrier();
-    // keys past the wave's last query are no query's; keys between its
-    // queries carry weight 0 for the earlier ones (their value rows are
-    // multiplied by that 0, so a non-finite value there would reach the
-    // earlier queries as NaN; the per-query kernel never reads such rows)
+    // Keys past the wave's last query are no query's.  A key outside some
+    // query's range (a later token, or before its window) must not touch
+    // that query's sum at all, as in the per-query kernel, which never reads
+    // such a value row: a non-finite value times the weight 0 would be NaN.
+    // The range test is uniform over the wave, so keys inside every query's
+    // range (the common case) take the plain FMA loop.
     const int64_t wlast = (int64_t)(qok[kQW - 1] ? qpos[kQW - 1] : hi_blk);
     const int nk = (int)((wlast - t0 + 1) < kTile ? (wlast - t0 + 1) : kTile);
     for (int j = 0; j < nk; ++j) {
       const float4v pj = ps[wave][j];
+      const int64_t tj = t0 + j;
+      bool inr[kQW];
+      bool all = true;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float v = Vs[j * kMqDim + lane + 64 * r];
+      for (int i = 0; i < kQW; ++i) {
+        inr[i] = !qok[i] || (tj >= (int64_t)qlo[i] && tj <= (int64_t)qpos[i]);
+        all = all && inr[i];
+      }
+      if (all) {
 #pragma unroll
-        for (int i = 0; i < kQW; ++i) acc[i][r] += pj[i] * v;
+        for (int r = 0; r < R; ++r) {
+          const float v = Vs[j * kMqDim + lane + 64 * r];
+#pragma unroll
+          for (int i = 0; i < kQW; ++i) acc[i][r] += pj[i] * v;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float v = Vs[j * kMqDim + lane + 64 * r];
+#pragma unroll
+          for (int i = 0; i < kQW; ++i)
+            if (inr[i]) acc[i][r] += pj[i] * v;
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();

@@ -9,8 +9,11 @@
 //     on ONE in-order HIP stream under a mutex, so dependent ops dispatched
 //     from different engine threads execute in submission order — the
 //     engine treats "dispatch returned" as done (PipelineEngine.hpp:639-650);
-//   * cache_sync(INVALIDATE) blocks until the last dispatch that wrote the
-//     buffer has finished (the Metal fence contract, metal_provider.mm:2044-2062);
+//   * every launch records a completion event (a provider-owned ring), and
+//     each buffer it writes keeps that event, so map and
+//     cache_sync(INVALIDATE) block until the last dispatch that wrote the
+//     buffer has finished, not until the whole stream drains (the Metal
+//     fence contract, metal_provider.mm:2044-2062);
 //   * unknown ops return NF_ERROR_UNSUPPORTED_OP, bad arity or sizes
 //     NF_ERROR_INVALID_ARG, HIP failures NF_ERROR_DEVICE_LOST / _INTERNAL /
 //     _OUT_OF_MEMORY.  Nothing falls back to the CPU.
@@ -81,11 +84,24 @@ struct Buffer {
   std::mutex mu;  // guards the fields below
   void* host = nullptr;     // pinned staging
   uint64_t host_bytes = 0;  // size of the pinned block (may exceed alloc_bytes when pooled)
-  bool host_valid = false;  // staging mirrors device contents
+  // The staging copy mirrors the device contents as of write sequence
+  // host_seq (valid only while host_has).  It is current iff host_seq equals
+  // last_write_seq, which launches update under the provider lock in the same
+  // critical section that enqueues the write, so a map on another thread
+  // never mistakes a stale copy for a current one.
+  bool host_has = false;
+  uint64_t host_seq = 0;
   bool mapped = false;
   uint64_t map_seq = 0;     // last_write_seq when the mapping was (re)filled
   std::atomic<uint64_t> last_write_seq{0};
+  // Completion event of the last launch that wrote this buffer (provider
+  // lock): ring slot, and the write sequence that event covers.
+  int ev_slot = -1;
+  uint64_t ev_seq = 0;
+  std::atomic<bool> exported{false};  // a share token was handed out
 };
+
+inline bool host_current(const Buffer* b) { return b->host_has && b->host_seq == b->last_write_seq.load(); }
 
 struct TimingRec {
   char op[64];
@@ -95,6 +111,10 @@ struct TimingRec {
 };
 
 constexpr uint32_t kTimingRing = 1024;
+// Completion events, one recorded after each launch (outside graph capture)
+// and reused round-robin.  A reused slot was recorded by a later launch on
+// the same in-order stream, so waiting on it still covers every earlier write.
+constexpr int kEventRing = 256;
 
 struct Provider {
   std::mutex mu;  // init/shutdown and every launch
@@ -107,6 +127,12 @@ struct Provider {
   std::atomic<uint64_t> launch_groups{0};  // launches enqueued (a merged group counts once)
   Tuning tuning;
   Workspace ws;  // split-K partials and tile counters
+  hipEvent_t done_ev[kEventRing] = {};  // guarded by mu
+  int next_ev = 0;
+  // Device-to-host copies of map / cache_sync / nf_hip_buffer_read, issued
+  // after the host has waited for the buffer's last writer, so they do not
+  // queue behind unrelated work on the launch stream.
+  hipStream_t copy_stream = nullptr;
   // pinned staging blocks of released large mappings, by size
   std::mutex pool_mu;
   std::multimap<uint64_t, void*> pool;
@@ -139,10 +165,28 @@ nf_status drain(Provider* p) {
   return NF_OK;
 }
 
+// Block until the last launch that wrote `b` has finished: on that launch's
+// completion event when it has one, else by draining the stream.
 nf_status wait_for_writes(Buffer* b) {
   Provider* p = b->prov;
-  if (b->last_write_seq.load() <= p->done_seq.load()) return NF_OK;
-  return drain(p);
+  // Memory shared with another buffer handle (imported, or exported for
+  // import) may be written through that handle: drain.
+  if (!b->owns_dev || b->exported.load()) return drain(p);
+  const uint64_t target = b->last_write_seq.load();
+  if (target <= p->done_seq.load()) return NF_OK;
+  hipEvent_t ev = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (!p->initialized) return NF_OK;
+    if (b->ev_slot >= 0 && b->ev_seq >= target) ev = p->done_ev[b->ev_slot];
+  }
+  if (!ev) return drain(p);
+  hipError_t e = hipEventSynchronize(ev);
+  if (e != hipSuccess) return map_hip(e, "hipEventSynchronize");
+  uint64_t cur = p->done_seq.load();
+  while (cur < target && !p->done_seq.compare_exchange_weak(cur, target)) {
+  }
+  return NF_OK;
 }
 
 // Returns a pinned block to the pool, or frees it when the pool is full.
@@ -159,6 +203,14 @@ void staging_put(Provider* p, void* h, uint64_t bytes) {
   (void)hipHostFree(h);
 }
 
+void destroy_events(Provider* p) {
+  for (auto& ev : p->done_ev) {
+    if (ev) (void)hipEventDestroy(ev);
+    ev = nullptr;
+  }
+  p->next_ev = 0;
+}
+
 void staging_drop(Buffer* b) {
   if (!b->host) return;
   if (b->host_bytes >= kKeepStagingBelow && b->prov)
@@ -167,7 +219,7 @@ void staging_drop(Buffer* b) {
     (void)hipHostFree(b->host);
   b->host = nullptr;
   b->host_bytes = 0;
-  b->host_valid = false;
+  b->host_has = false;
 }
 
 void pool_release_all(Provider* p) {
@@ -189,7 +241,7 @@ nf_status ensure_staging(Buffer* b) {
       b->host_bytes = it->first;
       p->pool_bytes -= it->first;
       p->pool.erase(it);
-      b->host_valid = false;
+      b->host_has = false;
       return NF_OK;
     }
   }
@@ -198,22 +250,40 @@ nf_status ensure_staging(Buffer* b) {
   if (e != hipSuccess) return map_hip(e, "hipHostMalloc(staging)");
   b->host = h;
   b->host_bytes = b->alloc_bytes;
-  b->host_valid = false;
+  b->host_has = false;
   return NF_OK;
 }
 
-// Copy between staging and device on the provider stream, then wait.
-nf_status copy_sync(Buffer* b, bool to_host) {
+// Device-to-host copy of bytes [off, off + n) of `b`: waits for the
+// buffer's last writer, then copies on the copy stream and waits for that.
+nf_status read_device(Buffer* b, uint64_t off, void* host, uint64_t n) {
   Provider* p = b->prov;
-  if (b->bytes == 0) return NF_OK;
+  nf_status st = wait_for_writes(b);
+  if (st != NF_OK) return st;
   hipError_t e;
   {
     std::lock_guard<std::mutex> lk(p->mu);
     if (!p->initialized) return set_error(NF_ERROR_INVALID_ARG, "provider not initialised");
-    e = to_host ? hipMemcpyAsync(b->host, b->dev, b->bytes, hipMemcpyDeviceToHost, p->stream)
-                : hipMemcpyAsync(b->dev, b->host, b->bytes, hipMemcpyHostToDevice, p->stream);
+    e = hipMemcpyAsync(host, static_cast<const char*>(b->dev) + off, n, hipMemcpyDeviceToHost, p->copy_stream);
   }
-  if (e != hipSuccess) return map_hip(e, to_host ? "hipMemcpyAsync(D2H)" : "hipMemcpyAsync(H2D)");
+  if (e == hipSuccess) e = hipStreamSynchronize(p->copy_stream);
+  return e == hipSuccess ? NF_OK : map_hip(e, "hipMemcpyAsync(D2H)");
+}
+
+// Copy between staging and device, then wait.  Host-to-device copies go on
+// the launch stream (ordered after every dispatch already issued, which may
+// still read the old contents) and drain it.
+nf_status copy_sync(Buffer* b, bool to_host) {
+  Provider* p = b->prov;
+  if (b->bytes == 0) return NF_OK;
+  if (to_host) return read_device(b, 0, b->host, b->bytes);
+  hipError_t e;
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (!p->initialized) return set_error(NF_ERROR_INVALID_ARG, "provider not initialised");
+    e = hipMemcpyAsync(b->dev, b->host, b->bytes, hipMemcpyHostToDevice, p->stream);
+  }
+  if (e != hipSuccess) return map_hip(e, "hipMemcpyAsync(H2D)");
   return drain(p);
 }
 
@@ -245,12 +315,14 @@ nf_status buf_map(nf_buffer self, void** out_ptr) {
   if (b->mapped) return set_error(NF_ERROR_INVALID_ARG, "map: buffer already mapped");
   nf_status st = ensure_staging(b);
   if (st != NF_OK) return st;
-  if (!b->host_valid) {
+  const uint64_t ws = b->last_write_seq.load();
+  if (!host_current(b)) {
     st = copy_sync(b, /*to_host=*/true);  // ordered after every enqueued write
     if (st != NF_OK) return st;
-    b->host_valid = true;
+    b->host_has = true;
+    b->host_seq = ws;
   }
-  b->map_seq = b->last_write_seq.load();
+  b->map_seq = ws;
   b->mapped = true;
   *out_ptr = b->host;
   return NF_OK;
@@ -267,7 +339,8 @@ nf_status buf_unmap(nf_buffer self) {
   if (b->last_write_seq.load() == b->map_seq) {
     nf_status st = copy_sync(b, /*to_host=*/false);
     if (st != NF_OK) return st;
-    b->host_valid = true;
+    b->host_has = true;
+    b->host_seq = b->map_seq;
   }
   if (b->bytes >= kKeepStagingBelow) staging_drop(b);
   return NF_OK;
@@ -287,10 +360,12 @@ nf_status buf_cache_sync(nf_buffer self, nf_cache_op op, uint64_t, uint64_t) {
     if (st != NF_OK) return st;
     if (b->mapped) {
       // A live mapping sees the device's latest contents.
+      const uint64_t ws = b->last_write_seq.load();
       st = copy_sync(b, true);
       if (st != NF_OK) return st;
-      b->host_valid = true;
-      b->map_seq = b->last_write_seq.load();
+      b->host_has = true;
+      b->host_seq = ws;
+      b->map_seq = ws;
     }
   }
   return NF_OK;
@@ -304,6 +379,7 @@ nf_status buf_get_info(nf_buffer self, nf_buffer_info* info) {
   info->domain = NF_MEM_DOMAIN_DEVICE;
   info->offset_bytes = 0;
   info->share_token = reinterpret_cast<uint64_t>(b->dev);
+  b->exported.store(true);
   info->refcount = b->refs.load(std::memory_order_relaxed);
   return NF_OK;
 }
@@ -311,6 +387,7 @@ nf_status buf_get_info(nf_buffer self, nf_buffer_info* info) {
 nf_status buf_export(nf_buffer self, uint64_t* token, nf_mem_domain* domain) {
   if (!self || !token || !domain) return set_error(NF_ERROR_INVALID_ARG, "export: null argument");
   *token = reinterpret_cast<uint64_t>(as_buf(self)->dev);
+  as_buf(self)->exported.store(true);
   *domain = NF_MEM_DOMAIN_DEVICE;
   return NF_OK;
 }
@@ -367,10 +444,16 @@ nf_status hip_init(nf_provider self) {
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->ws.cnt), p->ws.cnt_len * sizeof(uint32_t));
   if (e == hipSuccess) e = hipMemsetAsync(p->ws.cnt, 0, p->ws.cnt_len * sizeof(uint32_t), p->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->copy_stream, hipStreamNonBlocking);
+  for (int i = 0; i < kEventRing && e == hipSuccess; ++i)
+    e = hipEventCreateWithFlags(&p->done_ev[i], hipEventDisableTiming);
   if (e != hipSuccess) {
     (void)hipFree(p->ws.part);
     (void)hipFree(p->ws.cnt);
     p->ws = Workspace{};
+    destroy_events(p);
+    if (p->copy_stream) (void)hipStreamDestroy(p->copy_stream);
+    p->copy_stream = nullptr;
     (void)hipStreamDestroy(p->stream);
     p->stream = nullptr;
     return map_hip(e, "init: workspace");
@@ -398,6 +481,9 @@ void hip_shutdown(nf_provider self) {
   (void)hipFree(p->ws.cnt);
   p->ws = Workspace{};
   pool_release_all(p);
+  destroy_events(p);
+  (void)hipStreamDestroy(p->copy_stream);
+  p->copy_stream = nullptr;
   (void)hipStreamDestroy(p->stream);
   p->stream = nullptr;
   p->initialized = false;
@@ -643,25 +729,29 @@ nf_status launch(Provider* p, const Prepared* prs, uint32_t n) {
       }
     }
     if (rec) (void)hipEventRecord(rec->stop, p->stream);
+    // The launch's completion event; none while the stream is being
+    // captured into a graph (the written buffers then fall back to a drain).
+    int slot = -1;
+    if (e == hipSuccess) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(p->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
+          hipEventRecord(p->done_ev[p->next_ev], p->stream) == hipSuccess) {
+        slot = p->next_ev;
+        p->next_ev = (p->next_ev + 1) % kEventRing;
+      }
+    }
+    const uint64_t last = p->issued_seq + n;
     for (uint32_t j = 0; j < n; ++j) {
       const uint64_t seq = ++p->issued_seq;
-      for (uint32_t i = 0; i < prs[j].n_out; ++i) prs[j].out[i]->last_write_seq.store(seq);
+      auto wrote = [&](Buffer* b) {
+        b->last_write_seq.store(seq);
+        b->ev_slot = slot;
+        b->ev_seq = last;
+      };
+      for (uint32_t i = 0; i < prs[j].n_out; ++i) wrote(prs[j].out[i]);
       for (uint32_t i = 0; i < prs[j].n_in; ++i)
-        if (prs[j].pl.writes_inputs & (1u << i)) prs[j].in[i]->last_write_seq.store(seq);
+        if (prs[j].pl.writes_inputs & (1u << i)) wrote(prs[j].in[i]);
     }
-  }
-  // Buffer flags are updated outside the provider lock (map takes the
-  // buffer lock first, then the provider lock).
-  for (uint32_t j = 0; j < n; ++j) {
-    for (uint32_t i = 0; i < prs[j].n_out; ++i) {
-      std::lock_guard<std::mutex> bl(prs[j].out[i]->mu);
-      prs[j].out[i]->host_valid = false;
-    }
-    for (uint32_t i = 0; i < prs[j].n_in; ++i)
-      if (prs[j].pl.writes_inputs & (1u << i)) {
-        std::lock_guard<std::mutex> bl(prs[j].in[i]->mu);
-        prs[j].in[i]->host_valid = false;
-      }
   }
   if (e != hipSuccess) return map_hip(e, (std::string("launch ") + prs[0].pl.kernel).c_str());
   return NF_OK;
@@ -1005,12 +1095,14 @@ NF_API nf_status nf_hip_get_stream(nf_provider self, void** stream) {
 NF_API nf_status nf_hip_buffer_device_ptr(nf_buffer buf, void** dev_ptr) {
   if (!buf || !dev_ptr) return NF_ERROR_INVALID_ARG;
   *dev_ptr = as_buf(buf)->dev;
+  as_buf(buf)->exported.store(true);  // may now be written outside the provider's launches
   return NF_OK;
 }
 
 // Copies between host memory of any kind (pageable, e.g. an mmap of a GGUF
-// file, or pinned) and a byte range of a buffer, ordered on the provider
-// stream after every dispatch already issued, and complete on return.
+// file, or pinned) and a byte range of a buffer, complete on return.  A
+// write is ordered on the provider stream after every dispatch already
+// issued; a read waits for the buffer's last writer.
 static nf_status buffer_copy(nf_buffer buf, uint64_t offset, void* host, uint64_t bytes, bool to_device) {
   if (!buf || (!host && bytes)) return set_error(NF_ERROR_INVALID_ARG, "buffer copy: null argument");
   Buffer* b = as_buf(buf);
@@ -1020,21 +1112,18 @@ static nf_status buffer_copy(nf_buffer buf, uint64_t offset, void* host, uint64_
   if (bytes == 0) return NF_OK;
   std::lock_guard<std::mutex> bl(b->mu);
   if (b->mapped) return set_error(NF_ERROR_INVALID_ARG, "buffer copy: buffer is mapped");
-  uint64_t seq = 0;
+  if (!to_device) return read_device(b, offset, host, bytes);
   hipError_t e;
   {
     std::lock_guard<std::mutex> lk(p->mu);
     if (!p->initialized) return set_error(NF_ERROR_INVALID_ARG, "provider not initialised");
-    char* dev = static_cast<char*>(b->dev) + offset;
-    e = to_device ? hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, p->stream)
-                  : hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, p->stream);
-    if (e == hipSuccess && to_device) seq = ++p->issued_seq;
+    e = hipMemcpyAsync(static_cast<char*>(b->dev) + offset, host, bytes, hipMemcpyHostToDevice, p->stream);
+    if (e == hipSuccess) {
+      b->last_write_seq.store(++p->issued_seq);
+      b->ev_slot = -1;  // written by a copy, not a launch: waiting on it drains
+    }
   }
-  if (e != hipSuccess) return map_hip(e, to_device ? "hipMemcpyAsync(write)" : "hipMemcpyAsync(read)");
-  if (to_device) {
-    b->last_write_seq.store(seq);
-    b->host_valid = false;
-  }
+  if (e != hipSuccess) return map_hip(e, "hipMemcpyAsync(write)");
   return drain(p);
 }
 

@@ -319,7 +319,7 @@ void nf_oracle_linear_f16(const uint16_t *A, const uint16_t *B, uint16_t *C, uin
 /* ---- fused dequant + linear --------------------------------------------- */
 
 typedef struct {
-    const void *A;
+    const float *A; /* f16 path: the fp16 activations widened exactly to fp32, once per call */
     const uint8_t *W;
     int qfmt;
     int f16;
@@ -340,30 +340,20 @@ static void dequant_row(const uint8_t *W, int qfmt, int f16, uint64_t n, uint32_
 static void *fused_worker(void *arg) {
     const fused_job *j = (const fused_job *)arg;
     float *row = (float *)malloc(sizeof(float) * (j->K ? j->K : 1));
-    float *arow = j->f16 ? (float *)malloc(sizeof(float) * (j->K ? j->K : 1)) : NULL;
-    if (!row || (j->f16 && !arow)) {
-        free(row);
-        free(arow);
-        return (void *)1;
-    }
+    if (!row) return (void *)1;
     for (uint32_t n = j->n0; n < j->n1; ++n) {
         dequant_row(j->W, j->qfmt, j->f16, n, j->K, row);
         for (uint32_t m = 0; m < j->M; ++m) {
+            const float *a = j->A + (uint64_t)m * j->K;
             float acc = 0.0f;
-            if (j->f16) {
-                const uint16_t *a = (const uint16_t *)j->A + (uint64_t)m * j->K;
-                for (uint32_t k = 0; k < j->K; ++k) arow[k] = nf_oracle_f16_to_f32(a[k]);
-                for (uint32_t k = 0; k < j->K; ++k) acc += arow[k] * row[k];
+            for (uint32_t k = 0; k < j->K; ++k) acc += a[k] * row[k];
+            if (j->f16)
                 ((uint16_t *)j->C)[(uint64_t)m * j->N + n] = nf_oracle_f32_to_f16_rne(acc);
-            } else {
-                const float *a = (const float *)j->A + (uint64_t)m * j->K;
-                for (uint32_t k = 0; k < j->K; ++k) acc += a[k] * row[k];
+            else
                 ((float *)j->C)[(uint64_t)m * j->N + n] = acc;
-            }
         }
     }
     free(row);
-    free(arow);
     return NULL;
 }
 
@@ -374,12 +364,20 @@ static void fused_run(const void *A, const uint8_t *W, int qfmt, int f16, void *
     if (threads < 1) threads = 1;
     if (threads > n1 - n0) threads = n1 - n0;
     if (threads > 256) threads = 256;
+    /* fp16 activations widened once (exact), shared by every worker */
+    float *a32 = NULL;
+    if (f16) {
+        const uint64_t n = (uint64_t)M * K;
+        a32 = (float *)malloc(sizeof(float) * (n ? n : 1));
+        if (!a32) return;
+        for (uint64_t i = 0; i < n; ++i) a32[i] = nf_oracle_f16_to_f32(((const uint16_t *)A)[i]);
+    }
     fused_job jobs[256];
     pthread_t tids[256];
     const uint32_t span = n1 - n0;
     for (uint32_t t = 0; t < threads; ++t) {
         fused_job *j = &jobs[t];
-        j->A = A;
+        j->A = f16 ? a32 : (const float *)A;
         j->W = W;
         j->qfmt = qfmt;
         j->f16 = f16;
@@ -392,10 +390,11 @@ static void fused_run(const void *A, const uint8_t *W, int qfmt, int f16, void *
     }
     if (threads == 1) {
         fused_worker(&jobs[0]);
-        return;
+    } else {
+        for (uint32_t t = 0; t < threads; ++t) pthread_create(&tids[t], NULL, fused_worker, &jobs[t]);
+        for (uint32_t t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
     }
-    for (uint32_t t = 0; t < threads; ++t) pthread_create(&tids[t], NULL, fused_worker, &jobs[t]);
-    for (uint32_t t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
+    free(a32);
 }
 
 void nf_oracle_fused_f32(const float *A, const uint8_t *W, int qfmt, float *C, uint32_t M,

@@ -193,9 +193,14 @@ def test_embedding_lookup(provider, dim):
     o.release()
 
 
-@pytest.mark.parametrize("seq,heads,dim,step", [(5, 4, 64, 0), (3, 8, 128, 100), (1, 32, 64, 17)])
-def test_rope_batch_and_rope(provider, seq, heads, dim, step):
-    x = _rng(seq).standard_normal(seq * heads * dim).astype(np.float32)
+@pytest.mark.parametrize("seq,heads,dim,step,cut", [(5, 4, 64, 0, 0), (3, 8, 128, 100, 0), (1, 32, 64, 17, 0),
+                                                   (4, 6, 64, 3, 0), (3, 12, 128, 9, 0), (5, 7, 32, 1, 0),
+                                                   (3, 12, 64, 2, 5 * 64), (4, 14, 32, 0, 3 * 32)])
+def test_rope_batch_and_rope(provider, seq, heads, dim, step, cut):
+    """Head counts with and without a divisor <= 8 (the kernel applies one
+    angle to a group of heads of a token), and outputs whose length ends
+    inside a token (`cut` elements, whole heads, short of the last one)."""
+    x = _rng(seq).standard_normal(seq * heads * dim - cut).astype(np.float32)
     pc = push_constants(n_heads=heads, head_dim=dim, theta=10000.0, step_idx=step)
     # The angle pos * theta^(-2p/d) is formed in fp32 by both sides with powf
     # implementations that may differ by an ulp, so the rotation can differ
@@ -318,6 +323,65 @@ def test_attention(provider, op, f16, kw):
     if caches is not None:
         gk, gv, wk, wv = caches
         assert np.array_equal(gk, wk) and np.array_equal(gv, wv), "cache append"
+
+
+@pytest.mark.parametrize("op,kw,bad,f16", [
+    ("causal_attention", dict(H=4, KV=4, D=64, S=50, step=0, max_seq=0), 40, False),
+    ("flash_attention_cached", dict(H=4, KV=4, D=128, S=130, step=0, max_seq=160, window=40), 10, False),
+    ("flash_attention_cached", dict(H=4, KV=4, D=128, S=130, step=0, max_seq=160, window=40), 10, True),
+    ("flash_attention_gqa", dict(H=8, KV=2, D=64, S=70, step=0, max_seq=80), 33, False),
+    ("flash_attention_gqa", dict(H=8, KV=2, D=64, S=70, step=0, max_seq=80), 33, True)],
+    ids=["causal-f32", "cached-window-f32", "cached-window-f16", "gqa-f32", "gqa-f16"])
+def test_attention_prefill_nonfinite_value_row(provider, op, kw, bad, f16):
+    """An infinite value in the V row of token `bad` reaches only the queries
+    whose key range holds that token (the per-query reference kernel never
+    reads a row outside the range): every query the oracle keeps finite is
+    finite on the GPU too and matches it."""
+    H, KV, D, S, max_seq, window = kw["H"], kw["KV"], kw["D"], kw["S"], kw["max_seq"], kw.get("window", 0)
+    r = _rng(bad)
+    et, edt = (np.uint16, F16) if f16 else (np.float32, F32)
+    inf = np.array([np.inf], np.float16).view(np.uint16)[0] if f16 else np.float32(np.inf)
+
+    def rnd(n):
+        x = r.standard_normal(n).astype(np.float32)
+        return x.astype(np.float16).view(np.uint16) if f16 else x
+
+    mode = orc.ATTN_VARIANT[op][0]
+    prm = dict(n_heads=H, n_kv=KV, head_dim=D, seq_len=S, step=0, max_seq=max_seq, window=window)
+    pc = push_constants(seq_len=S, n_heads=H, head_dim=D, M=KV if KV != H else 0, step_idx=0,
+                        max_seq_len=max_seq, window_size=window)
+    if mode == 0:  # Q, K, V, out [n_heads, seq, dim]
+        q, k, v = rnd(H * S * D), rnd(H * S * D), rnd(H * S * D)
+        v.reshape(H, S, D)[:, bad, 3] = inf
+        want = orc.attention(op, prm, q, k=k.copy(), v=v.copy(), out=np.zeros(q.size, et), f16=f16)
+        (o,) = _run(provider, op, [q, k, v], [(edt, q.size * q.itemsize)], pc)
+        got = _read(o, et)
+        o.release()
+        qrows = lambda a: a.reshape(H, S, D).transpose(1, 0, 2)  # noqa: E731
+    else:
+        ck, cv = rnd(KV * max_seq * D), rnd(KV * max_seq * D)
+        kn, vn, q = rnd(S * KV * D), rnd(S * KV * D), rnd(S * H * D)
+        if mode == 1:  # K_new / V_new [seq, n_kv, dim], Q / out [seq, n_heads, dim]
+            vn.reshape(S, KV, D)[bad, :, 3] = inf
+            qrows = lambda a: a.reshape(S, H, D)  # noqa: E731
+        else:  # [n_kv, seq, dim], Q / out [n_heads, seq, dim]
+            vn.reshape(KV, S, D)[:, bad, 3] = inf
+            qrows = lambda a: a.reshape(H, S, D).transpose(1, 0, 2)  # noqa: E731
+        want = orc.attention(op, prm, q, kn, vn, ck.copy(), cv.copy(), out=np.zeros(q.size, et), f16=f16)
+        bk, bv = provider.alloc_array(ck, edt), provider.alloc_array(cv, edt)
+        (o,) = _run(provider, op, [q, kn, vn, bk, bv], [(edt, q.size * q.itemsize)], pc)
+        got = _read(o, et)
+        for b in (o, bk, bv):
+            b.release()
+    gf = qrows(got.view(np.float16).astype(np.float32) if f16 else got)
+    wf = qrows(want.view(np.float16).astype(np.float32) if f16 else want)
+    clean = np.isfinite(wf).all(axis=(1, 2))
+    assert clean[:bad].all() and not clean.all(), "the case must have clean and affected queries"
+    assert np.isfinite(gf[clean]).all(), f"non-finite output in queries {np.flatnonzero(~np.isfinite(gf).all(axis=(1, 2)) & clean)}"
+    if f16:
+        assert _ulp16_ok(qrows(got)[clean], qrows(want)[clean], ulps=2)
+    else:
+        assert np.max(np.abs(gf[clean] - wf[clean])) <= 2e-5 * np.max(np.abs(wf[clean]))
 
 
 def test_attention_decode_past_cache_is_noop(provider):
