@@ -166,8 +166,10 @@ NF_API nf_status nf_hip_buffer_device_ptr(nf_buffer buf, void **dev_ptr);
 
 /* Copy `bytes` bytes between host memory of any kind (pageable, such as an
  * mmap of a GGUF file, or pinned) and the byte range [offset, offset+bytes)
- * of a buffer.  Ordered on the provider stream after every dispatch already
- * issued; complete on return.  NF_ERROR_INVALID_ARG for a range outside the
+ * of a buffer; complete on return.  A write is ordered on the provider
+ * stream after every dispatch already issued; a read waits for the last
+ * dispatch that wrote the buffer (every dispatch for a buffer whose device
+ * address was handed out by export, get_info or nf_hip_buffer_device_ptr).  NF_ERROR_INVALID_ARG for a range outside the
  * buffer or a mapped buffer.  No counterpart in the reference's ABI: it is
  * the one-copy form of the weight upload the reference's model layer does
  * with map + memcpy + unmap (model/model/llama_dag_builder.hpp:146-156,
@@ -185,6 +187,27 @@ NF_API void nf_hip_release_staging(nf_provider self);
 
 /* Last error text recorded by the provider (thread-local, never NULL). */
 NF_API const char *nf_hip_last_error(void);
+
+/* Fused dequant + linear that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same computation and kernel choice as dispatch() of
+ * dequant_q4_0_linear[_f16] / dequant_q8_0_linear[_f16] (wtype Q4_0 or
+ * Q8_0; f16 = f16 activations and output, else f32), on caller-owned device
+ * pointers A [M,K], W [N,K] (blocks along K) and C [M,N], enqueued on
+ * `stream` (a hipStream_t; NULL = the null stream); needs no init.
+ * Split-K partials and tile counters come from a static device array of the
+ * library (4 MiB of partial tiles plus 4096 counters, held on every GPU the
+ * library runs on until the process ends), not from the provider workspace:
+ * a shape whose K split would need more partial tiles than that runs with
+ * fewer splits, so no size is refused for scratch and results agree with
+ * dispatch() within the fp32 accumulation tolerance.  Calls on one GPU share
+ * that array: calls that overlap in time on one GPU (different streams or
+ * threads) race; calls in order on one stream do not.  Returns
+ * NF_ERROR_INVALID_ARG for a bad dtype, null operand, zero size or a shape
+ * dispatch() would reject. */
+NF_API nf_status nf_hip_fused_linear_noalloc(nf_dtype wtype, const void *A, const void *W, void *C, uint32_t M,
+                                             uint32_t N, uint32_t K, bool f16, void *stream);
 
 #ifdef __cplusplus
 }

@@ -64,17 +64,22 @@ def _obj(src: Path) -> Path:
     return BUILD / (src.stem + ("_hip" if src.suffix == ".hip" else "_cxx") + ".o")
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every source and link the provider library; returns its path."""
+def build(jobs: int | None = None, verbose: bool = False, only: list[str] | None = None) -> Path:
+    """Compile every source (or, with `only`, the sources whose file names
+    are listed, reusing the other objects) and link the provider library;
+    returns its path."""
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     BUILD.mkdir(exist_ok=True)
     LIBDIR.mkdir(exist_ok=True)
     cmds = []
+    pick = (lambda src: True) if not only else (lambda src: src.name in only or not _obj(src).exists())
     for src in HIP_SOURCES:
-        cmds.append([HIPCC, *HIP_FLAGS, *COMMON_FLAGS, "-c", str(src), "-o", str(_obj(src))])
+        if pick(src):
+            cmds.append([HIPCC, *HIP_FLAGS, *COMMON_FLAGS, "-c", str(src), "-o", str(_obj(src))])
     for src in CXX_SOURCES:
-        cmds.append(["g++", *COMMON_FLAGS, "-Wall", "-c", str(src), "-o", str(_obj(src))])
+        if pick(src):
+            cmds.append(["g++", *COMMON_FLAGS, "-Wall", "-c", str(src), "-o", str(_obj(src))])
     jobs = jobs or min(8, os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         for fut in [ex.submit(_run, c) for c in cmds]:
@@ -103,6 +108,8 @@ def main(argv=None) -> int:
     ap.add_argument("--check", action="store_true")
     ap.add_argument("--clean", action="store_true")
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("--only", nargs="+", default=None, metavar="FILE",
+                    help="recompile only these source files (e.g. provider.hip), then link")
     a = ap.parse_args(argv)
     if a.clean:
         clean()
@@ -110,7 +117,7 @@ def main(argv=None) -> int:
     if a.check:
         print(LIB if LIB.exists() else "not built")
         return 0 if LIB.exists() else 1
-    build(a.j, verbose=True)
+    build(a.j, verbose=True, only=a.only)
     return 0
 
 

@@ -1143,3 +1143,110 @@ NF_API void nf_hip_release_staging(nf_provider self) {
 NF_API const char* nf_hip_last_error(void) { return t_last_error.c_str(); }
 
 }  // extern "C"
+
+// ---- fused linear that allocates nothing -------------------------------------
+//
+// nf_hip_fused_linear_noalloc runs the fused dequant + linear of dispatch()
+// on caller-owned device pointers and a caller's stream.  The split-K partial
+// tiles and tile counters its kernels need live in `scratch`, a file-scope
+// device array (each GPU the library runs on holds its own copy until the
+// process ends), instead of the provider workspace, so the call makes no
+// allocation and needs no provider init.
+namespace nfhip {
+namespace {
+
+constexpr size_t kScratchPartFloats = (size_t)1 << 20;  // 4 MiB of fp32 partial tiles
+constexpr uint32_t kScratchCounters = 4096;              // per-tile arrival counters
+constexpr size_t kScratchWords = kScratchPartFloats + kScratchCounters;
+
+static __device__ __align__(256) uint32_t scratch[kScratchWords];
+
+// Counters start at zero: the array is zero-initialised when the code object
+// loads, cleared again here at set-up, and every split-K launch leaves each
+// counter it used back at zero.
+__global__ void scratch_clear_kernel(uint32_t* p, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint32_t* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// Device address of this device's `scratch`, looked up (and its counters
+// cleared on `s`) the first time the device is used.
+nf_status scratch_for_current_device(hipStream_t s, uint32_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return map_hip(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return set_error(NF_ERROR_INVALID_ARG, "noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    uint32_t* ptr = nullptr;
+    e = hipGetSymbolAddress(reinterpret_cast<void**>(&ptr), HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return map_hip(e, "hipGetSymbolAddress(scratch)");
+    scratch_clear_kernel<<<(kScratchCounters + 255) / 256, 256, 0, s>>>(ptr + kScratchPartFloats, kScratchCounters);
+    e = hipGetLastError();
+    if (e != hipSuccess) return map_hip(e, "noalloc: scratch clear");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return NF_OK;
+}
+
+}  // namespace
+}  // namespace nfhip
+
+extern "C" {
+
+NF_API nf_status nf_hip_fused_linear_noalloc(nf_dtype wtype, const void* A, const void* W, void* C, uint32_t M,
+                                             uint32_t N, uint32_t K, bool f16, void* stream) {
+  if (wtype != NF_DTYPE_Q4_0 && wtype != NF_DTYPE_Q8_0)
+    return set_error(NF_ERROR_INVALID_ARG, "noalloc: weight dtype must be Q4_0 or Q8_0");
+  if (!A || !W || !C) return set_error(NF_ERROR_INVALID_ARG, "noalloc: null operand");
+  if (M == 0 || N == 0 || K == 0) return set_error(NF_ERROR_INVALID_ARG, "noalloc: M, N and K must be non-zero");
+  const char* op = wtype == NF_DTYPE_Q4_0 ? (f16 ? "dequant_q4_0_linear_f16" : "dequant_q4_0_linear")
+                                          : (f16 ? "dequant_q8_0_linear_f16" : "dequant_q8_0_linear");
+  // Descriptors sized exactly for M, N, K, so make_plan validates and plans
+  // the call as dispatch() would plan buffers of those sizes.
+  const uint64_t elt = f16 ? 2 : 4, bb = wtype == NF_DTYPE_Q4_0 ? 18 : 34;
+  const uint64_t blocks = (K % 32 == 0) ? (uint64_t)N * (K / 32) : ((uint64_t)N * K + 31) / 32;
+  nf_tensor_desc da{}, dw{}, dc{};
+  da.dtype = dc.dtype = f16 ? NF_DTYPE_F16 : NF_DTYPE_F32;
+  dw.dtype = wtype;
+  da.ndim = dw.ndim = dc.ndim = 1;
+  da.size_bytes = da.shape[0] = (uint64_t)M * K * elt;
+  dw.size_bytes = dw.shape[0] = blocks * bb;
+  dc.size_bytes = dc.shape[0] = (uint64_t)M * N * elt;
+  const nf_tensor_desc* ins[2] = {&da, &dw};
+  const nf_tensor_desc* outs[1] = {&dc};
+  nf_push_constants pc{};
+  pc.M = M;
+  pc.N = N;
+  pc.K = K;
+  Plan pl;
+  std::string why;
+  nf_status st = make_plan(op, ins, 2, outs, 1, reinterpret_cast<const uint8_t*>(&pc), sizeof(pc), g_prov.tuning, &pl,
+                           &why);
+  if (st != NF_OK) return set_error(st, std::string("noalloc: ") + why);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* ptr = nullptr;
+  st = scratch_for_current_device(s, &ptr);
+  if (st != NF_OK) return st;
+  Workspace ws;
+  ws.part = reinterpret_cast<float*>(ptr);
+  ws.part_floats = kScratchPartFloats;
+  ws.cnt = ptr + kScratchPartFloats;
+  ws.cnt_len = kScratchCounters;
+  // Operand views for run_plan, which reads only their device addresses.
+  Buffer ba, bw, bc;
+  ba.dev = const_cast<void*>(A);
+  bw.dev = const_cast<void*>(W);
+  bc.dev = C;
+  Buffer* in[2] = {&ba, &bw};
+  Buffer* out[1] = {&bc};
+  const hipError_t e = run_plan(pl, in, out, g_prov.tuning.gemm_tile, ws, s);
+  return e == hipSuccess ? NF_OK : map_hip(e, (std::string("noalloc launch ") + pl.kernel).c_str());
+}
+
+}  // extern "C"
