@@ -2,7 +2,7 @@
 """bench.py — throughput of the Q4_0/Q8_0 fused dequant+matmul path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode graph|eager] [--m M]
-                    [--no-extra] [--no-cpu] [--sweep]
+                    [--no-extra] [--no-cpu]
 
 Headline workload: one TinyLlama-1.1B decode step
 = the 155 Q4_0 projections of 22 layers + lm_head, f32 activations, batch M
@@ -27,9 +27,10 @@ resident in HBM before timing starts; the 582 MB of weights per step exceed
 
 Extras in the same JSON line: decode steps at M=4 and 16, configs[0] (one
 5632x2048 GEMV over 80 rotated weight copies), a Llama-3-8B Q8_0 decode step
-(configs[3], 32 layers + lm_head) at M=1/16/64, Llama-2-7B Q4_0 prefill GEMMs
-(configs[2]) in TFLOP/s, and with --sweep the configs[4] GEMV-vs-MFMA sweep
-over M = 1..256 on the 28672x8192 gate projection.
+(configs[3], 32 layers + lm_head) at M=1/16/64, a Llama-2-7B Q4_0 decode step
+at M=1 (north_star's "Llama-7B shapes"), Llama-2-7B Q4_0 prefill GEMMs
+(configs[2]) in TFLOP/s, and the configs[4] GEMV / small-batch / tiled-GEMM
+crossover sweep over M = 1..256 on both 70B FFN shapes.
 
 Modes: `graph` captures the step's dispatches (one nf_hip_run_tasks call)
 into a HIP graph and replays it; `eager` calls nf_hip_run_tasks every step.
@@ -69,9 +70,8 @@ def parse(argv=None):
     ap.add_argument("--roof-steps", type=int, default=5, help="eager steps timed per dispatch (<= 6)")
     ap.add_argument("--no-extra", action="store_true", help="only the headline decode step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--sweep", action="store_true", help="configs[4] GEMV/MFMA crossover sweep")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
-    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "dq", "up", "layer"], default=None,
+    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "c7b", "dq", "up", "layer"], default=None,
                     help="run one configs[i] section alone and print its JSON (profiling aid)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 4 device-to-device copies of BYTES (reference for HBM byte counters)")
@@ -301,14 +301,11 @@ def _ref_cpu(variant: str):
     return L
 
 
-def cpu_baseline(threads: int, seconds: float, variant: str = "v3") -> dict:
+def cpu_baseline(threads: int, seconds: float, variant: str = "release") -> dict:
     """configs[1] decode steps (155 Q4_0 linears at M=1) on the host cores,
     repeated for about `seconds`; GB/s of algorithmic bytes."""
     from neurofabric_amd import synthetic as syn
     ref = _ref_cpu(variant)
-    if ref is None and variant == "v3":
-        variant = "release"
-        ref = _ref_cpu(variant)
     shapes = syn.tinyllama_step_shapes()
     cache = {}
     for _, N, K in shapes:
@@ -359,37 +356,82 @@ def llama3_q8_step_shapes(layers: int = 32):
     return out
 
 
-def crossover_sweep(prov, N=28672, K=8192, Ms=(1, 2, 3, 4, 8, 16, 32, 64, 128, 256)) -> dict:
-    """the gate projection through every kernel family at each M
-    (f16 activations), by pinning the switch points: the VALU GEMV, the
-    small-batch MFMA kernel (M <= 64 per launch) and the tiled MFMA GEMM."""
+def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8, 16, 32, 64, 128, 256),
+                    copies: int = 4) -> dict:
+    """the Llama-70B FFN gate/up (28672x8192) and down
+    (8192x28672) Q4_0 projections, f16 activations, through every kernel
+    family that serves each M (switch points pinned): the VALU GEMV (while
+    its activation stage fits in LDS), the small-batch MFMA kernel (M <= 64,
+    one launch) and the tiled MFMA GEMM.  Each measurement replays (graph)
+    `copies` launches over distinct copies of the weights (4 x 132 MB, twice
+    the Infinity Cache), 5 times; the weights are uploaded once per shape."""
+    from neurofabric_amd import abi, synthetic as syn
     g32, g16 = prov.get_gemv_max_m()
     sk16 = prov.get_skinny_max_m()
     pins = {"gemv": (1 << 30, 1 << 30), "skinny": (0, 1 << 30), "tiled": (0, 0)}
-    rows = []
+    family = {"gemv": "gemv_", "skinny": "skinny_mfma_", "tiled": "gemm_mfma_"}
+    out = {}
     try:
-        for M in Ms:
-            row = {"M": M}
-            for path, (gmax, smax) in pins.items():
-                if path == "skinny" and M > 64:
-                    continue
-                prov.set_gemv_max_m(g32, gmax)
-                prov.set_skinny_max_m(smax)
-                st = rotated_linear(prov, "q4_0", M, N, K, True, 4)
-                r = time_step(prov, st, 5, 1, "eager")
-                us = r["us_per_launch"]
-                row[path] = {"us": us, "GB_s": st.bytes / len(st.tasks) / (us * 1e-6) / 1e9,
-                             "TFLOP_s": st.flops / len(st.tasks) / (us * 1e-6) / 1e12,
-                             "kernels": sorted(st.kernels)}
-                st.release()
-            row["fastest"] = min((k for k in pins if k in row), key=lambda k: row[k]["us"])
-            rows.append(row)
-            log(f"[bench] sweep M={M}: " + ", ".join(f"{k} {row[k]['us']:.1f} us" for k in pins if k in row))
+        for (N, K) in shapes:
+            W = syn.weights("q4_0", N, K, seed=N + K)
+            ws = [prov.alloc_array(W, abi.NF_DTYPE_Q4_0) for _ in range(copies)]
+            rows = []
+            for M in Ms:
+                a = prov.alloc_array(syn.activations(M, K, seed=M, dtype=np.float16), abi.NF_DTYPE_F16)
+                c = prov.alloc(abi.NF_DTYPE_F16, M * N * 2)
+                row = {"M": M}
+                for path, (gmax, smax) in pins.items():
+                    prov.set_gemv_max_m(g32, gmax)
+                    prov.set_skinny_max_m(smax)
+                    st = Step(prov)
+                    for w in ws:
+                        st.add("dequant_q4_0_linear_f16", [a, w], [c], M, N, K)
+                    st.finish()
+                    kern = sorted(st.kernels)[0]
+                    if not kern.startswith(family[path]) or (path == "skinny" and M > 64):
+                        continue  # this family does not serve M here
+                    r = time_step(prov, st, 5, 2, "graph")
+                    us = r["us_per_launch"]
+                    row[path] = {"us": us, "GB_s": st.bytes / copies / (us * 1e-6) / 1e9,
+                                 "TFLOP_s": st.flops / copies / (us * 1e-6) / 1e12, "kernel": kern}
+                a.release()
+                c.release()
+                fams = [k for k in pins if k in row]
+                row["fastest"] = min(fams, key=lambda k: row[k]["us"])
+                rows.append(row)
+                log(f"[bench] C4 {N}x{K} M={M}: " + ", ".join(f"{k} {row[k]['us']:.1f} us" for k in fams))
+            for w in ws:
+                w.release()
+            out[f"{N}x{K}"] = {"rows": rows, "fastest_by_M": {r["M"]: r["fastest"] for r in rows}}
     finally:
         prov.set_gemv_max_m(g32, g16)
         prov.set_skinny_max_m(sk16)
-    return {"shape": f"{N}x{K} Q4_0, f16 activations", "rows": rows,
-            "fastest_by_M": {r["M"]: r["fastest"] for r in rows}}
+    # The switch points these measurements imply beside the provider's
+    # defaults: the largest M at which the family is the fastest on every
+    # shape it serves (the GEMV does not serve the 28672-long rows beyond
+    # M = 2: its activation stage would not fit in LDS).
+    def last_m(fam):
+        ms = [m for m in Ms if any(fam in r for k in out for r in out[k]["rows"] if r["M"] == m) and
+              all(r["fastest"] == fam for k in out for r in out[k]["rows"] if r["M"] == m and fam in r)]
+        return max(ms) if ms else 0
+    out["switch_points"] = {"measured": {"gemv_max_m_f16": last_m("gemv"), "skinny_max_m_f16": last_m("skinny")},
+                            "defaults": {"gemv_max_m_f16": g16, "skinny_max_m_f16": sk16}}
+    out["activations"] = "f16 N(0,1); weights Q4_0 per configs[0] statistics"
+    return out
+
+
+def run_step(prov, shapes, fmt, M, steps, warmup, mode) -> dict:
+    """A whole decode step over a model's projections (model_step dataflow)."""
+    ws = WeightSet(prov, shapes, fmt)
+    st = model_step(prov, ws, M)
+    r = time_step(prov, st, steps, warmup, mode)
+    res = {"GB_s": st.bytes / (r["ms_per_step"] * 1e-3) / 1e9, "us_per_step": r["ms_per_step"] * 1e3,
+           "frac_of_hbm_peak": st.bytes / (r["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
+           "tokens_per_s": M / (r["ms_per_step"] * 1e-3), "dispatches": len(st.tasks), "launches": r["launches"],
+           "weight_GB_per_step": st.weight_bytes / 1e9, "kernels": sorted(st.kernels)}
+    st.release()
+    ws.release()
+    return res
 
 
 def run_c0(prov, mode: str) -> dict:
@@ -620,6 +662,7 @@ def main(argv=None) -> int:
     if args.only:
         sections = {"c0": lambda: run_c0(prov, args.mode), "c2": lambda: run_c2(prov),
                     "c3": lambda: run_c3(prov, args.mode), "c4": lambda: crossover_sweep(prov),
+                    "c7b": lambda: run_step(prov, syn.llama2_7b_step_shapes(), "q4_0", 1, 10, 2, args.mode),
                     "dq": lambda: run_dq(prov), "up": lambda: run_upload(prov),
                     "layer": lambda: run_layer(prov)}
         print(json.dumps({args.only: sections[args.only]()}), flush=True)
@@ -670,13 +713,14 @@ def main(argv=None) -> int:
     tiny.release()
     if not args.no_extra:
         extra["c0_gemv_5632x2048"] = run_c0(prov, args.mode)
+        extra["llama2_7b_q4_0_decode_m1"] = run_step(prov, syn.llama2_7b_step_shapes(), "q4_0", 1, 10, 2, args.mode)
+        log(f"[bench] Llama-2-7B Q4_0 decode step M=1: {extra['llama2_7b_q4_0_decode_m1']}")
         extra["c3_llama3_8b_q8_0_decode"] = run_c3(prov, args.mode)
         extra["c2_prefill_f16"] = run_c2(prov)
+        extra["c4_crossover"] = crossover_sweep(prov)
         extra["dequant_7b_ffn_weight"] = run_dq(prov)
         extra["weight_upload_512MiB"] = run_upload(prov)
         extra["layer_ops"] = run_layer(prov)
-    if args.sweep:
-        extra["c4_crossover"] = crossover_sweep(prov)
 
     cpu = None
     if not args.no_cpu:
@@ -687,10 +731,10 @@ def main(argv=None) -> int:
         allc = cpu_baseline(min(ncores, 64), min(args.cpu_seconds, 5.0))
         extra["cpu_all_cores"] = allc
         log(f"[bench] cpu {allc['cores']} threads: {allc['value']:.3f} GB/s")
-        if cpu.get("build") == "v3":
-            rel = cpu_baseline(1, min(args.cpu_seconds, 5.0), variant="release")
-            extra["cpu_release_flags_1_thread"] = rel
-            log(f"[bench] cpu 1 thread, reference Release flags: {rel['value']:.3f} GB/s")
+        if _ref_cpu("v3") is not None:
+            v3 = cpu_baseline(1, min(args.cpu_seconds, 5.0), variant="v3")
+            extra["cpu_x86_64_v3_1_thread"] = v3
+            log(f"[bench] cpu 1 thread, -march=x86-64-v3: {v3['value']:.3f} GB/s")
 
     pmc = load_pmc_summary()
     traffic = None

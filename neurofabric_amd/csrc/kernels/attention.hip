@@ -401,34 +401,36 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
     // query's range (a later token, or before its window) must not touch
     // that query's sum at all, as in the per-query kernel, which never reads
     // such a value row: a non-finite value times the weight 0 would be NaN.
-    // The range test is uniform over the wave, so keys inside every query's
-    // range (the common case) take the plain FMA loop.
+    // Tiles whose keys all lie inside every live query's range (all but the
+    // tiles at the diagonal and at a window edge) take the plain FMA loop;
+    // the others test each key against each query (the test is uniform over
+    // the wave).
     const int64_t wlast = (int64_t)(qok[kQW - 1] ? qpos[kQW - 1] : hi_blk);
     const int nk = (int)((wlast - t0 + 1) < kTile ? (wlast - t0 + 1) : kTile);
-    for (int j = 0; j < nk; ++j) {
-      const float4v pj = ps[wave][j];
-      const int64_t tj = t0 + j;
-      bool inr[kQW];
-      bool all = true;
+    bool interior = true;
 #pragma unroll
-      for (int i = 0; i < kQW; ++i) {
-        inr[i] = !qok[i] || (tj >= (int64_t)qlo[i] && tj <= (int64_t)qpos[i]);
-        all = all && inr[i];
-      }
-      if (all) {
+    for (int i = 0; i < kQW; ++i)
+      interior = interior && (!qok[i] || (t0 >= (int64_t)qlo[i] && t0 + nk - 1 <= (int64_t)qpos[i]));
+    if (interior) {
+      for (int j = 0; j < nk; ++j) {
+        const float4v pj = ps[wave][j];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const float v = Vs[j * kMqDim + lane + 64 * r];
 #pragma unroll
           for (int i = 0; i < kQW; ++i) acc[i][r] += pj[i] * v;
         }
-      } else {
+      }
+    } else {
+      for (int j = 0; j < nk; ++j) {
+        const float4v pj = ps[wave][j];
+        const int64_t tj = t0 + j;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const float v = Vs[j * kMqDim + lane + 64 * r];
 #pragma unroll
           for (int i = 0; i < kQW; ++i)
-            if (inr[i]) acc[i][r] += pj[i] * v;
+            if (qok[i] && tj >= (int64_t)qlo[i] && tj <= (int64_t)qpos[i]) acc[i][r] += pj[i] * v;
         }
       }
     }

@@ -74,14 +74,17 @@ struct LayerParams {
 // while M <= gemv_max_m (and its activation stage fits in LDS), the
 // small-batch MFMA kernel while M <= skinny_max_m (the f32 path stays there
 // for every larger M, 32 rows per launch), the tiled MFMA GEMM above (f16).
-// Defaults from the measured sweep on MI355X (28672x8192 Q4_0): the GEMV
-// wins or ties up to M = 4, the small-batch kernel from M = 8; for f16 it
-// still beats the tiled GEMM at M = 32 (91 vs 95 us) and loses at M = 64
-// (177 vs 96 us).
+// Defaults from the measured crossover sweep on MI355X (bench.py's configs[4]
+// section: 28672x8192 and 8192x28672 Q4_0, f16 activations, graph replay
+// over 4 weight copies): the GEMV is fastest up to M = 4 wherever its
+// activation stage fits (M = 4 at 28672x8192: 51.2 vs 53.0 us for the
+// small-batch kernel), the small-batch kernel up to M = 16 (64.5 vs 88.8 us
+// and 94.3 vs 97.7 us), the tiled GEMM from M = 32 (88.6 vs 89.3 us and
+// 95.8 vs 144.0 us).
 struct Tuning {
   uint32_t gemv_max_m_f32 = 4;
   uint32_t gemv_max_m_f16 = 4;
-  uint32_t skinny_max_m_f16 = 32;
+  uint32_t skinny_max_m_f16 = 16;
   // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernel
   // (default, measured fastest), 0..6 = one of the LDS-staged tile shapes.
   int32_t gemm_tile = -1;

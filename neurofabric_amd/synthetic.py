@@ -133,6 +133,13 @@ TINYLLAMA_LM_HEAD = ("lm_head", 32000, 2048)
 LLAMA2_7B_PREFILL = [("qkvo_proj", 4096, 4096), ("gate_up_proj", 11008, 4096),
                      ("down_proj", 4096, 11008)]
 
+# Llama-2-7B decode projections (north_star's "Llama-7B shapes"): 32 layers.
+LLAMA2_7B_LAYER = [("q_proj", 4096, 4096), ("k_proj", 4096, 4096), ("v_proj", 4096, 4096),
+                   ("o_proj", 4096, 4096), ("gate_proj", 11008, 4096), ("up_proj", 11008, 4096),
+                   ("down_proj", 4096, 11008)]
+LLAMA2_7B_LAYERS = 32
+LLAMA2_7B_LM_HEAD = ("lm_head", 32000, 4096)
+
 LLAMA3_8B_Q8 = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096),
                 ("o_proj", 4096, 4096), ("gate_proj", 14336, 4096), ("up_proj", 14336, 4096),
                 ("down_proj", 4096, 14336), ("lm_head", 128256, 4096)]
@@ -147,4 +154,14 @@ def tinyllama_step_shapes():
         for name, n, k in TINYLLAMA_LAYER:
             out.append((f"l{layer}.{name}", n, k))
     out.append(TINYLLAMA_LM_HEAD)
+    return out
+
+
+def llama2_7b_step_shapes():
+    """The 225 projections of one Llama-2-7B decode step, in order."""
+    out = []
+    for layer in range(LLAMA2_7B_LAYERS):
+        for name, n, k in LLAMA2_7B_LAYER:
+            out.append((f"l{layer}.{name}", n, k))
+    out.append(LLAMA2_7B_LM_HEAD)
     return out

@@ -102,3 +102,67 @@ def test_run_tasks_keeps_hazards_apart(provider, oracle_mod):
     finally:
         for b in (a, w1, w2, c):
             b.release()
+
+
+def test_run_tasks_weight_written_mid_list(provider, oracle_mod):
+    """A task in the middle of a batch overwrites the weight buffer a later
+    GEMV reads (embedding_lookup copying new Q4_0 bytes into it, bit for
+    bit); the later GEMV must use the new bytes, also when the list is run
+    twice in one call (repeat=2)."""
+    from neurofabric_amd.plugin import push_constants
+    M, N, K = 1, 300, 512
+    A = syn.activations(M, K, seed=5)
+    W1, W2_old, W2_new = (syn.q4_0_weights(N, K, seed=s) for s in (6, 7, 8))
+    assert W2_new.nbytes % 4 == 0
+    dim = W2_new.nbytes // 4
+    a = provider.alloc_array(A, abi.NF_DTYPE_F32)
+    w1 = provider.alloc_array(W1, abi.NF_DTYPE_Q4_0)
+    w2 = provider.alloc_array(W2_old.view(np.float32), abi.NF_DTYPE_F32)
+    table = provider.alloc_array(W2_new.view(np.float32), abi.NF_DTYPE_F32)
+    ids = provider.alloc_array(np.zeros(1, np.int32), abi.NF_DTYPE_I32)
+    c1 = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    c2 = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    try:
+        arr = _array([provider.task("dequant_q4_0_linear", [a, w1], [c1], M, N, K),
+                      provider.task("embedding_lookup", [table, ids], [w2], pc=push_constants(seq_len=1, head_dim=dim)),
+                      provider.task("dequant_q4_0_linear", [a, w2], [c2], M, N, K)])
+        provider.run_tasks(arr, 2)
+        provider.synchronize()
+        assert np.array_equal(w2.download(np.uint8), W2_new)
+        assert_close(c1.download(np.float32).reshape(M, N), oracle_mod.fused(A, W1, "q4_0", M, N, K), what="first")
+        assert_close(c2.download(np.float32).reshape(M, N), oracle_mod.fused(A, W2_new, "q4_0", M, N, K),
+                     what="after the write")
+    finally:
+        for b in (a, w1, w2, table, ids, c1, c2):
+            b.release()
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_run_tasks_chain_bit_identical(provider, fmt):
+    """Twelve decode GEMVs with distinct weights and shapes, the adjacent
+    same-input ones merged, through nf_hip_run_tasks three times in one
+    call, then one dispatch each: bit-identical outputs."""
+    M, K = 1, 2048
+    A = syn.activations(M, K, seed=9)
+    a = provider.alloc_array(A, abi.NF_DTYPE_F32)
+    shapes = [2048, 256, 256, 2048, 5632, 5632, 2048, 1024, 4096, 300, 64, 8192]
+    bufs, tasks, outs = [a], [], []
+    op = f"dequant_{fmt}_linear"
+    for i, N in enumerate(shapes):
+        w = provider.alloc_array(syn.weights(fmt, N, K, seed=20 + i), QDT[fmt])
+        c = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+        bufs += [w, c]
+        outs.append((w, c, N))
+        tasks.append(provider.task(op, [a, w], [c], M, N, K))
+    try:
+        provider.run_tasks(_array(tasks), 3)
+        provider.synchronize()
+        got = [c.download(np.float32).copy() for (_, c, _) in outs]
+        for (w, c, N) in outs:
+            provider.dispatch(op, [a, w], [c], M, N, K)
+        provider.synchronize()
+        for i, (_, c, _) in enumerate(outs):
+            assert np.array_equal(got[i].view(np.uint32), c.download(np.float32).view(np.uint32)), i
+    finally:
+        for b in bufs:
+            b.release()

@@ -280,14 +280,16 @@ def test_crossover_setter_roundtrip():
 
 
 def test_default_switch_points(lib):
-    """Defaults from the measured sweep: GEMV for M <= 4 while its activation
-    stage fits in 120 KB of LDS, the small-batch MFMA kernel up to 32 rows,
-    the tiled GEMM beyond (f16)."""
+    """Defaults from the measured configs[4] sweep: GEMV for M <= 4 while
+    its activation stage fits in 120 KB of LDS, the small-batch MFMA kernel
+    up to 16 rows, the tiled GEMM beyond (f16)."""
     f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
     assert _fused(lib, 4, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"   # 4 x 8192 x 2 B = 64 KB
+    assert _fused(lib, 4, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"  # 4 x 28672 x 2 B > 120 KB
     assert _fused(lib, 5, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
-    assert _fused(lib, 32, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
-    assert _fused(lib, 33, 28672, 8192, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
+    assert _fused(lib, 16, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
+    assert _fused(lib, 17, 28672, 8192, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
+    assert _fused(lib, 32, 8192, 28672, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
     assert _fused(lib, 4, 4096, 4096)["kernel"] == "gemv_q4_0_f32"
     assert _fused(lib, 2, 28672, 8192)["kernel"] == "gemv_q4_0_f32"           # 2 x 8192 x 4 B + sums
     assert _fused(lib, 3, 28672, 8192)["kernel"] == "skinny_mfma_q4_0_f32"    # 4 x 8192 x 4 B > 120 KB
