@@ -40,7 +40,7 @@ HIP_SOURCES = [
     CSRC / "kernels" / "layer.hip",
     CSRC / "kernels" / "attention.hip",
 ]
-CXX_SOURCES = [CSRC / "plan.cpp", CSRC / "plan_layer.cpp"]
+CXX_SOURCES = [CSRC / "plan.cpp", CSRC / "plan_layer.cpp", CSRC / "model_ops.cpp"]
 
 COMMON_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-fvisibility=hidden",
                 f"-I{REPO / 'include'}", f"-I{CSRC}"]

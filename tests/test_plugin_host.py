@@ -316,3 +316,40 @@ def test_every_reference_op_name_is_served(lib, op):
     with pytest.raises(NfError) as e:
         plan(lib, op, [], [])
     assert e.value.status == abi.NF_ERROR_INVALID_ARG, op
+
+
+def test_model_layer_op_selection(lib):
+    """nf_hip_model.h: the op a model layer emits per projection weight dtype.
+    Q4_0 and Q8_0 (and so a Q4_0 / Q8_0 output projection) run fused; dense
+    weights run `linear`; the other block formats need a warm-up dequant and
+    then run `linear` (quant_registry.hpp:50-88; llama_dag_builder.hpp:
+    1025-1039, 1411-1422).  Every name it returns is one the provider serves."""
+    import ctypes as C
+    for fn in ("nf_hip_fused_linear_op_name", "nf_hip_projection_op_name", "nf_hip_dequant_op_name"):
+        getattr(lib, fn).argtypes = [C.c_uint32, C.c_bool]
+        getattr(lib, fn).restype = C.c_char_p
+    lib.nf_hip_projection_needs_dequant.argtypes = [C.c_uint32]
+    lib.nf_hip_projection_needs_dequant.restype = C.c_bool
+    fused, proj, deq = lib.nf_hip_fused_linear_op_name, lib.nf_hip_projection_op_name, lib.nf_hip_dequant_op_name
+    assert fused(abi.NF_DTYPE_Q4_0, False) == b"dequant_q4_0_linear"
+    assert fused(abi.NF_DTYPE_Q4_0, True) == b"dequant_q4_0_linear_f16"
+    assert fused(abi.NF_DTYPE_Q8_0, False) == b"dequant_q8_0_linear"
+    assert fused(abi.NF_DTYPE_Q8_0, True) == b"dequant_q8_0_linear_f16"
+    names = ["q4_0", "q8_0", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q4_k", "q5_k", "q6_k"]
+    for f16 in (False, True):
+        for dt in (abi.NF_DTYPE_F32, abi.NF_DTYPE_F16):
+            assert fused(dt, f16) is None and proj(dt, f16) == b"linear" and deq(dt, f16) is None
+            assert not lib.nf_hip_projection_needs_dequant(dt)
+        for name in names:
+            dt = getattr(abi, f"NF_DTYPE_{name.upper()}")
+            want_deq = f"dequant_{name}" + ("_f16" if f16 else "")
+            assert deq(dt, f16) == want_deq.encode()
+            if name in ("q4_0", "q8_0"):
+                assert proj(dt, f16) == fused(dt, f16) and not lib.nf_hip_projection_needs_dequant(dt)
+            else:
+                assert fused(dt, f16) is None and proj(dt, f16) == b"linear"
+                assert lib.nf_hip_projection_needs_dequant(dt)
+            for op in {proj(dt, f16), deq(dt, f16)}:
+                with pytest.raises(NfError) as e:  # served: the planner answers arity, not unsupported
+                    plan(lib, op.decode(), [], [])
+                assert e.value.status == abi.NF_ERROR_INVALID_ARG, op
