@@ -122,10 +122,14 @@ NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path);
 NF_API uint32_t nf_hip_get_skinny_max_m(void);
 
 /* Kernel of the fused f16 GEMM path (M above the small-batch range): -1
- * (default) = the kernel that dequantizes weights in registers, measured
- * fastest on MI355X; 0..6 = the kernel that dequantizes weight tiles into
- * LDS, tile shape 256x256, 256x128, 128x128, 256x128 with 4 waves,
- * 256x128 with 4 waves and 3 stages, 128x128 with 3 stages, 128x256.
+ * (default) = the kernels that dequantize weights in registers, measured
+ * fastest on MI355X (two waves per SIMD for Q4_0 with K % 128 == 0 and
+ * M >= 1024, one wave per SIMD otherwise); 0..6 = the kernel that
+ * dequantizes weight tiles into LDS, tile shape 256x256, 256x128, 128x128,
+ * 256x128 with 4 waves, 256x128 with 4 waves and 3 stages, 128x128 with 3
+ * stages, 128x256; 7 = the register-dequantizing kernel with one wave per
+ * SIMD for every shape; 8 = the two-wave kernel wherever it applies (Q4_0,
+ * K % 128 == 0), else as 7.
  * Other values mean -1.  Environment override NF_HIP_GEMM_TILE (the shape
  * name or number) is read at nf_plugin_register.  No counterpart in the
  * reference (its Metal provider has one fused GEMM kernel); this is

@@ -958,6 +958,338 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_wq_kernel(const half_t* __res
 }
 
 // ---------------------------------------------------------------------------
+// two waves per SIMD: gemm_wq2_kernel
+//
+// The register-dequantizing design of gemm_wq_kernel (weights straight from
+// global memory into registers, dequantized there; A through LDS; TM x 2
+// v_mfma_f32_32x32x16_f16 tiles per wave, the same K permutation and output
+// layout) with two waves on every SIMD (TM = 4, NW = 4: 8 waves, at most 256
+// registers each, 128 of them the accumulators), so that one wave's
+// load-issue stalls, LDS waits and dequantization VALU run in the shadow of
+// the other wave's MFMAs.  The workgroup's 2*NW waves form two K-groups of
+// NW: group g takes the second half (g = 1) or the first half of the
+// workgroup's K steps for the same 32*TM x 64*NW output tile, with its own
+// two-stage A buffer in LDS.  To fit the register budget:
+//   * A streams global -> LDS with direct-to-LDS loads (no registers), one
+//     step ahead;
+//   * the weights are loaded two steps ahead into two register sets and
+//     dequantized one MFMA slice (8 halves per fragment) ahead, not a whole
+//     step ahead.
+// The end-of-step barrier waits for the A loads only (vmcnt = the weight
+// loads issued after them), through the s_waitcnt intrinsic so the
+// compiler's own wait insertion sees it and does not add a vmcnt(0).
+// After the K loop group 1's accumulators are added to group 0's through
+// LDS, element by element in that order (deterministic), and group 0 stores
+// the tile or, with K split across workgroups as well, parks it for the
+// fix-up of gemm_wq_kernel.  (TM = 8 with one wave per SIMD, 256-row waves
+// that halve the dequantization per MFMA, measured slower: 693 against 816
+// TFLOP/s at 4096 x 4096, M = 2048.)
+
+// Elements 8kk..8kk+7 of the lane's block as 4 dwords of fp16 (the
+// dequant_*_f16 bits): Q4_0 low nibbles of code dwords 2(kk&1), 2(kk&1)+1
+// for kk < 2, high nibbles for kk >= 2; Q8_0 code dwords 2kk, 2kk+1.
+template <class QF>
+__device__ __forceinline__ u32x4 dequant_slice(const uint32_t (&w)[WBlk<QF>::kDwords], uint32_t sel, half2v d2,
+                                               int kk) {
+  u32x4 o;
+  if constexpr (std::is_same<QF, Q4_0>::value) {
+    const half2v off = {(half_t)-1032.f, (half_t)-1032.f};
+    const int t0 = 2 * (kk & 1);
+    const uint32_t qa = __builtin_amdgcn_perm(w[t0 + 1], w[t0], sel);
+    const uint32_t qb = __builtin_amdgcn_perm(w[t0 + 2], w[t0 + 1], sel);
+    const uint32_t xa = (kk >> 1) ? (qa >> 4) & 0x0F0F0F0Fu : qa & 0x0F0F0F0Fu;
+    const uint32_t xb = (kk >> 1) ? (qb >> 4) & 0x0F0F0F0Fu : qb & 0x0F0F0F0Fu;
+    o.x = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, xa, 0x04010400u)) + off) * d2);
+    o.y = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, xa, 0x04030402u)) + off) * d2);
+    o.z = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, xb, 0x04010400u)) + off) * d2);
+    o.w = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, xb, 0x04030402u)) + off) * d2);
+  } else {
+    const half2v off = {(half_t)-1152.f, (half_t)-1152.f};
+    const uint32_t ua = __builtin_amdgcn_perm(w[2 * kk + 1], w[2 * kk], sel) ^ 0x80808080u;
+    const uint32_t ub = __builtin_amdgcn_perm(w[2 * kk + 2], w[2 * kk + 1], sel) ^ 0x80808080u;
+    o.x = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, ua, 0x04010400u)) + off) * d2);
+    o.y = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, ua, 0x04030402u)) + off) * d2);
+    o.z = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, ub, 0x04010400u)) + off) * d2);
+    o.w = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, ub, 0x04030402u)) + off) * d2);
+  }
+  return o;
+}
+
+template <class QF, int TM, int NW, bool SPLIT>
+__global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __restrict__ A,
+                                                              const uint8_t* __restrict__ W, half_t* __restrict__ C,
+                                                              int M, int N, int K, float* __restrict__ ws_part,
+                                                              uint32_t* __restrict__ ws_cnt) {
+  constexpr int TN = 2, BM = 32 * TM, BN = 32 * TN * NW, NT0 = 64 * NW;
+  constexpr int STAGE = BM * 64;     // halves per LDS stage
+  constexpr int A_DMA = BM / 8 / NW;  // direct-to-LDS loads (8 rows each) per wave per step
+  static_assert(BM % (8 * NW) == 0 && A_DMA % 2 == 0, "A rows per wave");
+  constexpr int WD = WBlk<QF>::kDwords;
+  extern __shared__ __attribute__((aligned(16))) half_t lds[];  // [group][2][BM][64]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int grp = wave / NW, wv = wave % NW;
+  const int r32 = lane & 31, kb = lane >> 5;
+  int tm, tn;
+  xcd_tile(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN, wn = wv * 32 * TN;
+  // K steps: the KG workgroups of a tile take ranges of whole step pairs;
+  // the two groups of a workgroup split its range in halves.
+  const int KG = SPLIT ? (int)gridDim.y : 1, kg = SPLIT ? (int)blockIdx.y : 0;
+  const int np_all = K / (2 * kBK);
+  const int p_first = (int)((long)np_all * kg / KG);
+  const int nk = (int)((long)np_all * (kg + 1) / KG) - p_first;  // steps per group
+  const int k0 = 2 * p_first + grp * nk;                            // this group's first step
+
+  // A: load i of a lane fills row (wv*A_DMA + i)*8 + l/8 of the stage, slot
+  // l%8, with the global chunk the swizzle places in that slot.  Rows past M
+  // read row M-1 (their outputs are never stored).
+  const half_t* asrc[A_DMA];
+#pragma unroll
+  for (int i = 0; i < A_DMA; ++i) {
+    const int r = (wv * A_DMA + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int gr = m0 + r < M ? m0 + r : M - 1;
+    asrc[i] = A + (size_t)gr * K + (size_t)k0 * kBK + c * 8;
+  }
+  const size_t row_bytes = (size_t)(K / 64) * GPair<QF>::kBytes;
+  const uint32_t w_sel = kb ? 0x07060504u : 0x05040302u, w_sh = kb ? 16u : 0u;
+  const uint8_t* wsrc[TN];
+  bool w_valid[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn + 32 * j + r32;
+    w_valid[j] = n < N;
+    wsrc[j] = W + (size_t)(w_valid[j] ? n : 0) * row_bytes + (size_t)k0 * GPair<QF>::kBytes + kb * 4 * WBlk<QF>::kStride;
+  }
+  half_t* my_lds = lds + (size_t)grp * 2 * STAGE;
+
+  uint32_t wr[2][TN][WD];
+  auto load_w = [&](int ks, int set) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) load_wblk<QF>(wsrc[j] + (size_t)ks * GPair<QF>::kBytes, wr[set][j]);
+  };
+  auto dma_a = [&](int ks, int stage) {
+    half_t* dst = my_lds + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) lds_dma16(asrc[i] + (size_t)ks * kBK, dst + (wv * A_DMA + i) * 8 * 64);
+  };
+  half2v dsc[2][TN];  // fp16 scales of the two register sets' blocks
+  auto scales = [&](int set) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      uint32_t db = (wr[set][j][0] >> w_sh) & 0xFFFFu;
+      db = w_valid[j] ? db : 0u;
+      dsc[set][j] = h2_of(db | (db << 16));
+    }
+  };
+  u32x4 bw[2][TN];
+  auto dequant = [&](int set, int kk, int buf) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bw[buf][j] = dequant_slice<QF>(wr[set][j], w_sel, dsc[set][j], kk);
+  };
+  half8 af[2][TM];
+  auto read_a = [&](int stage, int kk, int buf) {
+    const half_t* As = my_lds + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      af[buf][i] = *reinterpret_cast<const half8*>(As + tile_off(32 * i + r32, 4 * kb + kk));
+  };
+  float16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
+  auto mfma = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, bw[buf][j]), af[buf][i],
+                                                           acc[i][j], 0, 0, 0);
+  };
+  // End-of-step barrier: this wave's LDS reads and its A loads for the next
+  // step must be complete; the weight loads issued during the step for the
+  // step after next (kInFlight instructions, issued after the A loads) may
+  // stay in flight.
+  constexpr int kInFlight = TN * WBlk<QF>::kLoads;
+  // (The wait is the intrinsic, not inline asm, so the compiler's own wait
+  // insertion knows the older loads have landed and adds no vmcnt(0).)
+  static_assert(kInFlight < 16, "vmcnt field");
+  auto step_barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0070 | kInFlight);  // vmcnt(kInFlight) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: A of step 0 into stage 0; weights of steps 0 and 1 (past the
+  // last step: its loads again, never used) into register sets 0 and 1.
+  dma_a(0, 0);
+  load_w(0, 0);
+  load_w(nk > 1 ? 1 : 0, 1);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  scales(0);
+  read_a(0, 0, 0);
+  dequant(0, 0, 0);
+
+  // Step s (weight register set and LDS stage u = s & 1):
+  //   A of step s+1 streams into stage u^1 (read last in step s-1, released
+  //   by that step's barrier);
+  //   slice kk: read A of slice kk+1 and dequantize its weights, then the
+  //   MFMAs of slice kk;
+  //   the weights of step s+2 are loaded into set u once its last slice is
+  //   dequantized (before the last slice's MFMAs);
+  //   barrier; then slice 0 of step s+1 read and dequantized.
+  auto step = [&](auto uc, int s) {
+    constexpr int u = decltype(uc)::value;
+    dma_a(s + 1 < nk ? s + 1 : nk - 1, u ^ 1);  // past the last step: an unused reload
+    // The weight loads below must issue after these (the barrier's vmcnt
+    // counts them as the only loads younger than the A loads).
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk < 3) {
+        read_a(u, kk + 1, (kk + 1) & 1);
+        dequant(u, kk + 1, (kk + 1) & 1);
+      } else {
+        load_w(s + 2 < nk ? s + 2 : nk - 1, u);
+      }
+      mfma(kk & 1);
+    }
+    step_barrier();
+    if (s + 1 < nk) {
+      scales(u ^ 1);
+      read_a(u ^ 1, 0, 0);
+      dequant(u ^ 1, 0, 0);
+    }
+  };
+  int s = 0;
+  for (; s + 2 <= nk; s += 2) {
+    step(std::integral_constant<int, 0>{}, s);
+    step(std::integral_constant<int, 1>{}, s + 1);
+  }
+  if (s < nk) step(std::integral_constant<int, 0>{}, s);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // Group 1 hands its sums to group 0 through LDS (the stages are free now),
+  // RT tiles of TM at a time: value (i, j, r) of thread t at float index
+  // ((i' * TN + j) * 16 + r) * NT0 + t (i' = i - round * RT), conflict-free.
+  constexpr int RT = (4 * STAGE * 2) / (TN * 16 * NT0 * 4);  // tiles of TM per round that fit the stages
+  static_assert(RT >= 1 && TM % RT == 0, "reduction rounds");
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int rd = 0; rd < TM / RT; ++rd) {
+    if (grp == 1) {
+#pragma unroll
+      for (int ii = 0; ii < RT; ++ii)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            red[((ii * TN + j) * 16 + r) * NT0 + (tid - NT0)] = acc[rd * RT + ii][j][r];
+    }
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+      for (int ii = 0; ii < RT; ++ii)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[rd * RT + ii][j][r] += red[((ii * TN + j) * 16 + r) * NT0 + tid];
+    }
+    __syncthreads();
+  }
+
+  auto store = [&]() {
+    const bool vec = (N & 3) == 0 && ((uintptr_t)C & 7) == 0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int gm = m0 + 32 * i + r32;
+      if (gm >= M) continue;
+      half_t* crow = C + (size_t)gm * N;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int gn = n0 + wn + 32 * j + 8 * q + 4 * kb;
+          const half_t h0 = (half_t)acc[i][j][4 * q + 0], h1 = (half_t)acc[i][j][4 * q + 1];
+          const half_t h2 = (half_t)acc[i][j][4 * q + 2], h3 = (half_t)acc[i][j][4 * q + 3];
+          if (vec && gn + 3 < N) {
+            typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<half4v*>(crow + gn) = half4v{h0, h1, h2, h3};
+          } else {
+            if (gn + 0 < N) crow[gn + 0] = h0;
+            if (gn + 1 < N) crow[gn + 1] = h1;
+            if (gn + 2 < N) crow[gn + 2] = h2;
+            if (gn + 3 < N) crow[gn + 3] = h3;
+          }
+        }
+    }
+  };
+  if constexpr (!SPLIT) {
+    if (grp == 0) store();
+    return;
+  }
+  // K split across workgroups: group 0 parks its tile and the last
+  // workgroup of the tile adds the KG partial tiles in order (the fix-up of
+  // gemm_wq_kernel, with group 0's 256 threads).
+  const int tile = blockIdx.x;
+  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
+  if (grp == 0) {
+    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          mine[((i * TN + j) * 4 + q) * NT0 + tid] =
+              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ uint32_t is_last;
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == (uint32_t)(KG - 1);
+  }
+  __syncthreads();
+  if (!is_last || grp != 0) return;
+  constexpr int kMaxKG = 8;
+  // One 16-byte group of each partial tile at a time (registers: the
+  // accumulators already use half of them).
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float4v part[kMaxKG];
+#pragma unroll
+        for (int g = 0; g < kMaxKG; ++g)
+          if (g < KG && g != kg) part[g] = tile_ws[(size_t)g * (BM * BN / 4) + ((i * TN + j) * 4 + q) * NT0 + tid];
+        float4v sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < kMaxKG; ++g) {
+          if (g >= KG) break;
+          sum += g == kg ? float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]}
+                         : part[g];
+        }
+        acc[i][j][4 * q + 0] = sum[0];
+        acc[i][j][4 * q + 1] = sum[1];
+        acc[i][j][4 * q + 2] = sum[2];
+        acc[i][j][4 * q + 3] = sum[3];
+      }
+  store();
+  if (tid == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // small-tile kernel (any K % 32 == 0)
 
 constexpr int kTile = 64;
@@ -1147,6 +1479,50 @@ hipError_t gemm_wq_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_t
   return hipGetLastError();
 }
 
+// gemm_wq2_kernel: K in whole step pairs (K % 128 == 0).  K is split over
+// kg = 1, 2, 4, 8 workgroups per tile like gemm_wq_launch (one workgroup per
+// CU; the smallest kg minimizing rounds x step pairs per workgroup, at least
+// 8 pairs per part, bounded by the workspace).
+template <class QF, int TM, int NW>
+hipError_t gemm_wq2_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_t M, uint32_t N, uint32_t K,
+                           const nfhip::Workspace& ws, hipStream_t s) {
+  constexpr int BM = 32 * TM, BN = 64 * NW;
+  const long tiles = (long)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
+  if (tiles > (1L << 31) - 1 || K % 128 != 0) return hipErrorInvalidConfiguration;
+  const int np = (int)(K / 128);
+  static const int kg_max = [] {
+    const char* e = std::getenv("NF_HIP_GEMM_SPLITK_MAX");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 ? v : 8;
+  }();
+  constexpr long kCUs = 256;
+  int kg = 1;
+  long best = ((tiles + kCUs - 1) / kCUs) * np;
+  for (int g = 2; g <= kg_max && g <= 8 && np / g >= 8 && tiles <= (long)ws.cnt_len &&
+                  (size_t)tiles * g * BM * BN <= ws.part_floats;
+       g *= 2) {
+    const long cost = ((tiles * g + kCUs - 1) / kCUs) * ((np + g - 1) / g);
+    if (cost < best) best = cost, kg = g;
+  }
+  const size_t lds = (size_t)4 * BM * 64 * sizeof(half_t);
+  if (kg == 1) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_wq2_kernel<QF, TM, NW, false>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)lds);
+    if (attr != hipSuccess) return attr;
+    gemm_wq2_kernel<QF, TM, NW, false><<<dim3((unsigned)tiles), dim3(128 * NW), lds, s>>>(a, w, c, M, N, K, ws.part,
+                                                                                        ws.cnt);
+  } else {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_wq2_kernel<QF, TM, NW, true>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)lds);
+    if (attr != hipSuccess) return attr;
+    gemm_wq2_kernel<QF, TM, NW, true><<<dim3((unsigned)tiles, (unsigned)kg), dim3(128 * NW), lds, s>>>(
+        a, w, c, M, N, K, ws.part, ws.cnt);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace nfk
 
 namespace nfhip {
@@ -1184,9 +1560,18 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
   nfk::half_t* c = static_cast<nfk::half_t*>(C);
   const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
   if (K % 64 == 0 && aligned) {
-    // Default: the register-dequantizing kernel (measured faster than the
-    // LDS-staged tiles at every prefill shape with M > 64); tile 0..6 selects
-    // one of the LDS-staged tile shapes instead.
+    // Default: the register-dequantizing kernels (measured faster than the
+    // LDS-staged tiles at every prefill shape with M > 64): two waves per
+    // SIMD (gemm_wq2_kernel) for Q4_0 with K % 128 == 0 and M >= 1024, where
+    // it measured faster (816 / 747 / 859 against 785 / 735 / 804 TFLOP/s on
+    // the three Llama-2-7B projection shapes at M = 2048), else one wave per
+    // SIMD (gemm_wq_kernel; also Q8_0, whose weight window does not fit the
+    // two-wave register budget).  Tile 7 forces the one-wave kernel, tile 8
+    // the two-wave kernel wherever it applies; 0..6 select one of the
+    // LDS-staged tile shapes.
+    const bool wq2_fits = q == QFmt::Q4_0 && K % 128 == 0;
+    if ((tile == 8 && wq2_fits) || (tile < 0 && wq2_fits && M >= 1024))
+      return nfk::gemm_wq2_launch<nfk::Q4_0, 4, 4>(a, w, c, M, N, K, ws, s);
     if (tile < 0 || tile > 6)
       return (q == QFmt::Q4_0) ? nfk::gemm_wq_launch<nfk::Q4_0, 4, 2, 4, 4>(a, w, c, M, N, K, ws, s)
                                : nfk::gemm_wq_launch<nfk::Q8_0, 4, 2, 4, 4>(a, w, c, M, N, K, ws, s);

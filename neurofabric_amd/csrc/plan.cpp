@@ -224,10 +224,10 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
 int gemm_tile_from_name(const char* name) {
   if (!name) return -1;
   static const char* const kNames[] = {"256x256", "256x128", "128x128", "256x128w4",
-                                       "256x128w4s3", "128x128s3", "128x256"};
-  for (int i = 0; i < 7; ++i)
+                                       "256x128w4s3", "128x128s3", "128x256", "wq1", "wq2"};
+  for (int i = 0; i < 9; ++i)
     if (std::strcmp(name, kNames[i]) == 0) return i;
-  if (name[0] >= '0' && name[0] <= '6' && name[1] == '\0') return name[0] - '0';
+  if (name[0] >= '0' && name[0] <= '8' && name[1] == '\0') return name[0] - '0';
   return -1;
 }
 

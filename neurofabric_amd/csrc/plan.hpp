@@ -85,14 +85,17 @@ struct Tuning {
   uint32_t gemv_max_m_f32 = 4;
   uint32_t gemv_max_m_f16 = 4;
   uint32_t skinny_max_m_f16 = 16;
-  // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernel
-  // (default, measured fastest), 0..6 = one of the LDS-staged tile shapes.
+  // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernels
+  // (default: two waves per SIMD where it applies and measured faster),
+  // 0..6 = one of the LDS-staged tile shapes, 7 = the register-dequantizing
+  // kernel with one wave per SIMD, 8 = the two-wave kernel wherever it
+  // applies (Q4_0, K % 128 == 0).
   int32_t gemm_tile = -1;
 };
 
 // "256x256" -> 0, "256x128" -> 1, "128x128" -> 2, "256x128w4" -> 3,
-// "256x128w4s3" -> 4, "128x128s3" -> 5, "128x256" -> 6, or the number 0..6;
-// anything else (including null) -> -1.
+// "256x128w4s3" -> 4, "128x128s3" -> 5, "128x256" -> 6, "wq1" -> 7,
+// "wq2" -> 8, or the number 0..8; anything else (including null) -> -1.
 int gemm_tile_from_name(const char* name);
 
 struct Plan {

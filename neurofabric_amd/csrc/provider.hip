@@ -1009,7 +1009,7 @@ NF_API uint32_t nf_hip_get_skinny_max_m(void) { return g_prov.tuning.skinny_max_
 
 NF_API void nf_hip_set_gemm_tile(int32_t tile) {
   std::lock_guard<std::mutex> lk(g_prov.mu);
-  g_prov.tuning.gemm_tile = (tile >= 0 && tile <= 6) ? tile : -1;
+  g_prov.tuning.gemm_tile = (tile >= 0 && tile <= 8) ? tile : -1;
 }
 
 NF_API int32_t nf_hip_get_gemm_tile(void) { return g_prov.tuning.gemm_tile; }

@@ -340,7 +340,9 @@ class Provider:
         return int(self.lib.nf_hip_launch_count(self.handle))
 
     def set_gemm_tile(self, tile: int) -> None:
-        """-1: register-dequantizing GEMM kernel (default); 0..6: LDS-staged tile shapes."""
+        """-1: register-dequantizing GEMM kernels (default); 0..6: LDS-staged tile
+        shapes; 7: the register-dequantizing kernel with one wave per SIMD;
+        8: the two-wave-per-SIMD kernel wherever it applies (Q4_0, K % 128 == 0)."""
         self.lib.nf_hip_set_gemm_tile(tile)
 
     def get_gemm_tile(self) -> int:

@@ -167,17 +167,21 @@ def test_gemv_large_activation_staging(provider, oracle_mod, fmt, f16, shape):
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("tile", [-1, 8], ids=["default", "wq2"])
 @pytest.mark.parametrize("shape", [(200, 520, 8192), (130, 300, 16384), (512, 4096, 11008)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_tiled_gemm_split_k(provider, oracle_mod, fmt, shape):
+def test_tiled_gemm_split_k(provider, oracle_mod, fmt, tile, shape):
     """Tiled MFMA GEMM with fewer tiles than CUs and long K: K is split over
     2-4 workgroups per tile and the last one adds the partial tiles.  Two
-    calls in a row: the per-tile counters must be back at zero after each."""
+    calls in a row: the per-tile counters must be back at zero after each.
+    Tile 8 forces the two-waves-per-SIMD kernel (Q4_0; Q8_0 falls back to
+    the one-wave kernel), which the default picks only from M = 1024."""
     M, N, K = shape
     W = syn.weights(fmt, N, K, seed=N + 1)
-    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m(), provider.get_gemm_tile())
     try:
         _force_path(provider, "tiled", True)
+        provider.set_gemm_tile(tile)
         for rep in range(2):
             A = syn.activations(M, K, seed=K + rep, dtype=np.float16)
             cols = (0, N) if N <= 520 else (N - 256, N)
@@ -188,17 +192,24 @@ def test_tiled_gemm_split_k(provider, oracle_mod, fmt, shape):
     finally:
         provider.set_gemv_max_m(*old[0])
         provider.set_skinny_max_m(old[1])
+        provider.set_gemm_tile(old[2])
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 5], ids=lambda t: "regdq" if t < 0 else f"lds{t}")
-@pytest.mark.parametrize("shape", [(129, 260, 64), (257, 514, 192), (130, 302, 320), (200, 777, 448)],
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 5, 7, 8],
+                         ids=lambda t: "regdq" if t < 0 else f"lds{t}" if t < 7 else f"wq{t - 6}")
+@pytest.mark.parametrize("shape", [(129, 260, 64), (257, 514, 192), (130, 302, 320), (200, 777, 448),
+                                   (129, 260, 128), (257, 514, 384), (130, 302, 640), (200, 777, 896)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_gemm_kernels_edges(provider, oracle_mod, fmt, tile, shape):
-    """Both f16 GEMM kernels (weights dequantized in registers: tile -1; into
-    LDS: tiles 0..6) against the oracle on ragged shapes: M and N past a tile
-    edge, N % 4 != 0 (element-wise stores), and 1, 3, 5 and 7 K steps, i.e.
-    fewer steps than the prefetch depth and every loop remainder."""
+    """Every f16 GEMM kernel (weights dequantized in registers: tile -1 the
+    default pick, tile 7 the one-wave kernel, tile 8 the two-waves-per-SIMD
+    kernel for Q4_0 with K % 128 == 0; into LDS: tiles 0..6) against the
+    oracle on ragged
+    shapes: M and N past a tile edge, N % 4 != 0 (element-wise stores), and
+    1, 3, 5, 7 K steps, or 1, 3, 5, 7 step pairs per K-group (K = 128 ..
+    896), i.e. fewer steps than the prefetch depth and every loop
+    remainder."""
     M, N, K = shape
     W = syn.weights(fmt, N, K, seed=N + K)
     A = syn.activations(M, K, seed=M + K, dtype=np.float16)
