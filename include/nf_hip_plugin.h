@@ -111,15 +111,21 @@ NF_API nf_status nf_hip_plan_dispatch(const char *op_name,
 
 /* Batch-size switch points between the kernel families of the fused ops:
  * the VALU decode GEMV while M <= gemv_max_m, the small-batch MFMA kernel
- * above it (up to skinny_max_m for f16 activations; f32 activations stay on
- * it for every M, 64 rows per launch), the LDS-tiled MFMA GEMM beyond
- * (f16).  Defaults come from measurement; environment overrides
- * NF_HIP_GEMV_MAX_M_F32, NF_HIP_GEMV_MAX_M_F16 and NF_HIP_SKINNY_MAX_M_F16
- * are read at nf_plugin_register. */
+ * above it up to skinny_max_m (at most 32 f32 / 64 f16 activation rows per
+ * launch), the tiled MFMA GEMM beyond (f16 activations: fp16 MFMA; f32
+ * activations: exact bf16 pieces on bf16 MFMA, K % 64 == 0).  f16 and f32
+ * activations each have their own switch points.  Defaults come from
+ * measurement; environment overrides NF_HIP_GEMV_MAX_M_F32,
+ * NF_HIP_GEMV_MAX_M_F16, NF_HIP_SKINNY_MAX_M_F16 and NF_HIP_SKINNY_MAX_M_F32
+ * are read at nf_plugin_register.  No counterpart in the reference: its
+ * Metal provider runs one kernel for every M (metal_provider.mm:3009-3019,
+ * the simdgroup variant disabled). */
 NF_API void nf_hip_set_gemv_max_m(uint32_t f32_path, uint32_t f16_path);
 NF_API void nf_hip_get_gemv_max_m(uint32_t *f32_path, uint32_t *f16_path);
 NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path);
 NF_API uint32_t nf_hip_get_skinny_max_m(void);
+NF_API void nf_hip_set_skinny_max_m_f32(uint32_t f32_path);
+NF_API uint32_t nf_hip_get_skinny_max_m_f32(void);
 
 /* Kernel of the fused f16 GEMM path (M above the small-batch range): -1
  * (default) = the kernels that dequantize weights in registers, measured

@@ -25,6 +25,35 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float float2s __attribute__((ext_vector_type(2)));
+
+// Two floats -> their bf16 pair, exact when each float has <= 8 significant
+// bits (upper halves of the f32 patterns).
+__device__ __forceinline__ uint32_t pack_hi16(float a, float b) {
+  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, a), 0x07060302u);
+}
+
+// Exact three-way bf16 split of 8 floats.
+__device__ __forceinline__ void split3(const float (&x)[8], bf16x8& p1, bf16x8& p2, bf16x8& p3) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float2s v = {x[2 * j], x[2 * j + 1]};
+    const bf16x2v h1 = __builtin_convertvector(v, bf16x2v);
+    const float2s r1 = v - __builtin_convertvector(h1, float2s);
+    const bf16x2v h2 = __builtin_convertvector(r1, bf16x2v);
+    const float2s r2 = r1 - __builtin_convertvector(h2, float2s);
+    const bf16x2v h3 = __builtin_convertvector(r2, bf16x2v);
+    p1[2 * j] = h1[0];
+    p1[2 * j + 1] = h1[1];
+    p2[2 * j] = h2[0];
+    p2[2 * j + 1] = h2[1];
+    p3[2 * j] = h3[0];
+    p3[2 * j + 1] = h3[1];
+  }
+}
+
 struct Q4_0 {
   static constexpr int kBytes = 18;
 };

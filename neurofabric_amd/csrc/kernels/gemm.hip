@@ -324,6 +324,42 @@ __device__ __forceinline__ void xcd_tile(int bid, int mt, int nt, int& tm, int& 
   tn = within / rows;
 }
 
+// Split-K fix-up of the last workgroup to arrive at a tile: every workgroup
+// of the tile (this one included) has parked its fp32 partial tile in
+// `tile_ws` (partial g at float4 offset g * stride; values 4q..4q+3 of tile
+// (i, j) of thread tid at ((i*TN + j)*4 + q)*NT + tid).  Their sum, in order
+// g = 0..KG-1 whichever workgroup arrives last, replaces acc.  All of one
+// partial's loads for CH tiles of TM are issued before any is added, so a
+// thread keeps 4*TN*CH loads in flight: the gather costs about KG*TM/CH
+// memory round trips, not one per 16-byte group.
+template <int TM, int TN, int NT, int CH>
+__device__ __forceinline__ void splitk_gather(float16v (&acc)[TM][TN], const float4v* __restrict__ tile_ws,
+                                              size_t stride, int KG, int tid) {
+  static_assert(TM % CH == 0, "chunks of whole tile rows");
+#pragma unroll
+  for (int i0 = 0; i0 < TM; i0 += CH) {
+    for (int g = 0; g < KG; ++g) {
+      float4v p[CH][TN][4];
+#pragma unroll
+      for (int ii = 0; ii < CH; ++ii)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            p[ii][j][q] = tile_ws[(size_t)g * stride + (((i0 + ii) * TN + j) * 4 + q) * NT + tid];
+#pragma unroll
+      for (int ii = 0; ii < CH; ++ii)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[i0 + ii][j][4 * q + e] = g == 0 ? p[ii][j][q][e] : acc[i0 + ii][j][4 * q + e] + p[ii][j][q][e];
+    }
+  }
+}
+
 // CTA tile BM x BN, WGM x WGN waves, each owning (BM/WGM) x (BN/WGN) =
 // TM x TN tiles of 32x32; K step 64, two LDS stages.
 //
@@ -548,20 +584,23 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
     return;
   }
   // Split K across workgroups: each parks its fp32 accumulators in the
-  // workspace (value (i, j, r) of thread tid at ((i*TN + j)*16 + r)*NT + tid);
+  // workspace as 16-byte groups (values 4q..4q+3 of tile (i, j) of thread
+  // tid at float4 index ((i*TN + j)*4 + q)*NT + tid, coalesced per wave);
   // the last workgroup of the tile to arrive (per-tile counter, agent-scope
-  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1, its own
-  // from registers, stores C and resets the counter.
+  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1
+  // (splitk_gather), stores C and resets the counter.
   const int tile = blockIdx.x;
-  float* tile_ws = ws_part + (size_t)tile * KG * (BM * BN);
+  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
   {
-    float* mine = tile_ws + (size_t)kg * (BM * BN);
+    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mine[((i * TN + j) * 16 + r) * NT + tid] = acc[i][j][r];
+        for (int q = 0; q < 4; ++q)
+          mine[((i * TN + j) * 4 + q) * NT + tid] =
+              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -572,17 +611,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
   }
   __syncthreads();
   if (!is_last) return;
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float sum = 0.f;
-        for (int g = 0; g < KG; ++g)
-          sum += g == kg ? acc[i][j][r] : tile_ws[(size_t)g * (BM * BN) + ((i * TN + j) * 16 + r) * NT + tid];
-        acc[i][j][r] = sum;
-      }
+  splitk_gather<TM, TN, NT, (TM % 2 == 0 && TM * TN >= 8) ? TM / 2 : TM>(acc, tile_ws, BM * BN / 4, KG, tid);
   store();
   if (tid == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -837,9 +866,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_wq_kernel(const half_t* __res
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // PROBE_PRE_BARRIER
     lds_barrier();
-    // PROBE_POST_BARRIER
     read_a(wb ^ 1, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -849,9 +876,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_wq_kernel(const half_t* __res
       if (m == 4 || m == 5) load_piece(ks, u, 8 + (m - 4));
       __builtin_amdgcn_sched_barrier(0);
     }
-    // PROBE_STEP_END
   };
-  // PROBE_LOOP_BEGIN
   int s = 0;
   for (; s + PF <= nk; s += PF) {
     step(std::integral_constant<int, 0>{}, s);
@@ -901,10 +926,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_wq_kernel(const half_t* __res
   // workspace as 16-byte groups (values 4q..4q+3 of tile (i, j) of thread tid
   // at float4 index ((i*TN + j)*4 + q)*NT + tid, coalesced per wave); the
   // last workgroup of the tile to arrive (per-tile counter, agent-scope
-  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1, its own
-  // from registers, stores C and resets the counter.  The partials of one
-  // (i, j) tile are loaded for every g before any is added, so a thread has
-  // 4*(KG-1) loads in flight rather than one.
+  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1
+  // (splitk_gather), stores C and resets the counter.
   const int tile = blockIdx.x;
   float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
   {
@@ -927,32 +950,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_wq_kernel(const half_t* __res
   }
   __syncthreads();
   if (!is_last) return;
-  constexpr int kMaxKG = 8;  // the launcher splits K at most 8 ways
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      float4v part[kMaxKG][4];
-#pragma unroll
-      for (int g = 0; g < kMaxKG; ++g)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (g < KG && g != kg) part[g][q] = tile_ws[(size_t)g * (BM * BN / 4) + ((i * TN + j) * 4 + q) * NT + tid];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float4v sum = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int g = 0; g < kMaxKG; ++g) {
-          if (g >= KG) break;
-          sum += g == kg ? float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]}
-                         : part[g][q];
-        }
-        acc[i][j][4 * q + 0] = sum[0];
-        acc[i][j][4 * q + 1] = sum[1];
-        acc[i][j][4 * q + 2] = sum[2];
-        acc[i][j][4 * q + 3] = sum[3];
-      }
-    }
+  splitk_gather<TM, TN, NT, TM>(acc, tile_ws, BM * BN / 4, KG, tid);
   store();
   if (tid == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1260,31 +1258,9 @@ __global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __r
   }
   __syncthreads();
   if (!is_last || grp != 0) return;
-  constexpr int kMaxKG = 8;
-  // One 16-byte group of each partial tile at a time (registers: the
-  // accumulators already use half of them).
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float4v part[kMaxKG];
-#pragma unroll
-        for (int g = 0; g < kMaxKG; ++g)
-          if (g < KG && g != kg) part[g] = tile_ws[(size_t)g * (BM * BN / 4) + ((i * TN + j) * 4 + q) * NT0 + tid];
-        float4v sum = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int g = 0; g < kMaxKG; ++g) {
-          if (g >= KG) break;
-          sum += g == kg ? float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]}
-                         : part[g];
-        }
-        acc[i][j][4 * q + 0] = sum[0];
-        acc[i][j][4 * q + 1] = sum[1];
-        acc[i][j][4 * q + 2] = sum[2];
-        acc[i][j][4 * q + 3] = sum[3];
-      }
+  // (Registers: the accumulators already use half of them, so half a tile
+  // of loads at a time.)
+  splitk_gather<TM, TN, NT0, TM / 2>(acc, tile_ws, BM * BN / 4, KG, tid);
   store();
   if (tid == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1523,6 +1499,343 @@ hipError_t gemm_wq2_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// f32 activations on bf16 MFMA: gemm_f32a_kernel
+//
+// C (f32) = A (f32) x deq(W)^T, every weight the exact f32 value d*(q-8)
+// (Q4_0) or d*q (Q8_0), for batches too large for the small-batch kernel
+// (which takes at most 32 activation rows per launch and so streams the
+// weights once per 32 rows).  Here a workgroup streams each weight once per
+// 32*TM rows, and the products are formed on v_mfma_f32_32x32x16_bf16 from
+// exact bf16 pieces:
+//   * each activation x = a1 + a2 + a3 exactly (split3: round-to-nearest
+//     bf16 pieces, |a2| <= 2^-8 |x|, |a3| <= 2^-16 |x|), split once per
+//     workgroup while its 64-column K step is staged into three bf16 planes
+//     in LDS;
+//   * each weight v (at most 15 significant bits for Q4_0, 18 for Q8_0) =
+//     b1 + b2 (+ b3 for Q8_0) exactly (truncated bf16 pieces, |b2| < 2^-7 |v|,
+//     |b3| < 2^-14 |v|), formed in registers from the codes and the scale one
+//     MFMA slice ahead;
+//   * every piece product a_i*b_j that can exceed 2^-22 |x v| is an MFMA
+//     term: Q4_0 a1b1, a2b1, a3b1, a1b2, a2b2 (dropped: a3b2 < 2^-23 |x v|);
+//     Q8_0 the same and a1b3 (dropped: a2b3, a3b2, a3b3 < 2^-21 |x v|).  The
+//     products are exact and the MFMA accumulates in fp32, so each x*v
+//     enters the sum to within a few units of its fp32 rounding, as in the
+//     reference's sequential f32 loop (metal_provider.mm:1396-1431).
+// Tiling as gemm_wq_kernel: 32*TM x 32*TN per wave, NW waves along N, the
+// same K permutation (slice kk of a step pairs lane group kb with elements
+// 8kk..8kk+7 of block kb) and output layout; A through a two-stage LDS
+// buffer (A of step s+1 loaded into registers at the start of step s, split
+// and written at its end), weights two steps ahead in two register sets.
+// K may be split across workgroups (the fix-up of gemm_wq_kernel).
+
+// Weight pieces of slice kk of the lane's block: 8 values, as NB bf16x8.
+template <class QF, int NB>
+__device__ __forceinline__ void f32a_weight_slice(const uint32_t (&w)[WBlk<QF>::kDwords], uint32_t sel, float d,
+                                                  int kk, u32x4 (&out)[NB]) {
+  float v[8];
+  if constexpr (std::is_same<QF, Q4_0>::value) {
+    const int t0 = 2 * (kk & 1);
+    const uint32_t qa = __builtin_amdgcn_perm(w[t0 + 1], w[t0], sel);
+    const uint32_t qb = __builtin_amdgcn_perm(w[t0 + 2], w[t0 + 1], sel);
+    const uint32_t xa = (kk >> 1) ? (qa >> 4) & 0x0F0F0F0Fu : qa & 0x0F0F0F0Fu;
+    const uint32_t xb = (kk >> 1) ? (qb >> 4) & 0x0F0F0F0Fu : qb & 0x0F0F0F0Fu;
+    const float m8d = -8.f * d;  // exact
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __builtin_fmaf((float)((xa >> (8 * e)) & 0xFFu), d, m8d);  // d*(q-8), exact
+      v[4 + e] = __builtin_fmaf((float)((xb >> (8 * e)) & 0xFFu), d, m8d);
+    }
+  } else {
+    const uint32_t ua = __builtin_amdgcn_perm(w[2 * kk + 1], w[2 * kk], sel) ^ 0x80808080u;  // q + 128
+    const uint32_t ub = __builtin_amdgcn_perm(w[2 * kk + 2], w[2 * kk + 1], sel) ^ 0x80808080u;
+    const float m128d = -128.f * d;  // exact
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __builtin_fmaf((float)((ua >> (8 * e)) & 0xFFu), d, m128d);  // d*q, exact
+      v[4 + e] = __builtin_fmaf((float)((ub >> (8 * e)) & 0xFFu), d, m128d);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < NB; ++p) {
+    out[p] = u32x4{pack_hi16(v[0], v[1]), pack_hi16(v[2], v[3]), pack_hi16(v[4], v[5]), pack_hi16(v[6], v[7])};
+    if (p + 1 < NB) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)  // residual below the truncated piece: exact
+        v[e] -= __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[e]) & 0xFFFF0000u);
+    }
+  }
+}
+
+template <class QF, int TM, int TN, int NW, bool SPLIT>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_f32a_kernel(const float* __restrict__ A,
+                                                               const uint8_t* __restrict__ W, float* __restrict__ C,
+                                                               int M, int N, int K, float* __restrict__ ws_part,
+                                                               uint32_t* __restrict__ ws_cnt) {
+  constexpr bool kQ4 = std::is_same<QF, Q4_0>::value;
+  constexpr int NB = kQ4 ? 2 : 3;  // bf16 pieces of a weight
+  constexpr int NTERM = kQ4 ? 5 : 6;
+  constexpr int BM = 32 * TM, BN = 32 * TN * NW, NT = 64 * NW;
+  constexpr int PLANE = BM * 64;    // bf16 values per piece plane per stage
+  constexpr int STAGE = 3 * PLANE;  // three activation pieces
+  constexpr int A_T = BM / (8 * NW);  // 8-float activation chunks per lane per step
+  static_assert(BM % (8 * NW) == 0, "A rows per wave");
+  constexpr int WD = WBlk<QF>::kDwords;
+  extern __shared__ __attribute__((aligned(16))) uint16_t ldsb[];  // [2][3][BM][64] bf16
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r32 = lane & 31, kb = lane >> 5;
+  int tm, tn;
+  xcd_tile(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN, wn = wave * 32 * TN;
+  const int KG = SPLIT ? (int)gridDim.y : 1, kg = SPLIT ? (int)blockIdx.y : 0;
+  const int nk_all = K / kBK;
+  const int k_first = (int)((long)nk_all * kg / KG);
+  const int nk = (int)((long)nk_all * (kg + 1) / KG) - k_first;
+
+  // A: chunk i of a lane is row (wave*A_T + i)*8 + l/8, floats 8*(l%8) ..
+  // +7 of the step (eight lanes read one row's 256 B).  Rows past M read row
+  // M-1 (their outputs are never stored).
+  const float* asrc[A_T];
+  int adst[A_T];
+#pragma unroll
+  for (int i = 0; i < A_T; ++i) {
+    const int r = (wave * A_T + i) * 8 + (lane >> 3);
+    const int gr = m0 + r < M ? m0 + r : M - 1;
+    asrc[i] = A + (size_t)gr * K + (size_t)k_first * kBK + (lane & 7) * 8;
+    adst[i] = tile_off(r, lane & 7);
+  }
+  // W: frag j of this lane is row n0 + wn + 32j + r32, block kb of each pair
+  // (rows past N read row 0 with the scale forced to zero).
+  const size_t row_bytes = (size_t)(K / 64) * GPair<QF>::kBytes;
+  const uint32_t w_sel = kb ? 0x07060504u : 0x05040302u, w_sh = kb ? 16u : 0u;
+  const uint8_t* wsrc[TN];
+  bool w_valid[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn + 32 * j + r32;
+    w_valid[j] = n < N;
+    wsrc[j] = W + (size_t)(w_valid[j] ? n : 0) * row_bytes + (size_t)k_first * GPair<QF>::kBytes +
+              kb * 4 * WBlk<QF>::kStride;
+  }
+
+  float ra[A_T][8];
+  auto load_a = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < A_T; ++i) {
+      const float4v lo = *reinterpret_cast<const float4v*>(asrc[i] + (size_t)ks * kBK);
+      const float4v hi = *reinterpret_cast<const float4v*>(asrc[i] + (size_t)ks * kBK + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ra[i][e] = lo[e], ra[i][4 + e] = hi[e];
+    }
+  };
+  auto write_a = [&](int stage) {
+    uint16_t* dst = ldsb + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < A_T; ++i) {
+      bf16x8 p1, p2, p3;
+      split3(ra[i], p1, p2, p3);
+      *reinterpret_cast<bf16x8*>(dst + adst[i]) = p1;
+      *reinterpret_cast<bf16x8*>(dst + PLANE + adst[i]) = p2;
+      *reinterpret_cast<bf16x8*>(dst + 2 * PLANE + adst[i]) = p3;
+    }
+  };
+  uint32_t wr[2][TN][WD];
+  auto load_w = [&](int ks, int set) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) load_wblk<QF>(wsrc[j] + (size_t)ks * GPair<QF>::kBytes, wr[set][j]);
+  };
+  float dsc[2][TN];
+  auto scales = [&](int set) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint32_t db = (wr[set][j][0] >> w_sh) & 0xFFFFu;
+      dsc[set][j] = w_valid[j] ? h2f_bits((uint16_t)db) : 0.f;
+    }
+  };
+  u32x4 bp[2][TN][NB];
+  auto weights = [&](int set, int kk, int buf) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) f32a_weight_slice<QF, NB>(wr[set][j], w_sel, dsc[set][j], kk, bp[buf][j]);
+  };
+  bf16x8 ap[2][3][TM];
+  auto read_a = [&](int stage, int kk, int buf) {
+    const uint16_t* As = ldsb + stage * STAGE;
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        ap[buf][p][i] = *reinterpret_cast<const bf16x8*>(As + p * PLANE + tile_off(32 * i + r32, 4 * kb + kk));
+  };
+  float16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
+  // Terms (weight piece, activation piece), most significant first.
+  constexpr int kWb[6] = {0, 0, 0, 1, 1, 2}, kAb[6] = {0, 1, 2, 0, 1, 0};
+  auto mfma = [&](int buf) {
+#pragma unroll
+    for (int t = 0; t < NTERM; ++t)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, bp[buf][j][kWb[t]]),
+                                                              ap[buf][kAb[t]][i], acc[i][j], 0, 0, 0);
+  };
+  auto lds_barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: A of step 0 split into stage 0; weights of steps 0 and 1 (past
+  // the last step: its loads again, never used) in register sets 0 and 1.
+  load_a(0);
+  load_w(0, 0);
+  load_w(nk > 1 ? 1 : 0, 1);
+  write_a(0);
+  scales(0);
+  lds_barrier();
+  read_a(0, 0, 0);
+  weights(0, 0, 0);
+
+  // Step s (register set and stage u = s & 1): A of step s+1 loaded at the
+  // start; per slice kk the next slice's operands, then this slice's MFMAs;
+  // the weights of step s+2 loaded into set u once its last slice is formed;
+  // A of step s+1 split into stage u^1; barrier; slice 0 of step s+1.
+  auto step = [&](auto uc, int s) {
+    constexpr int u = decltype(uc)::value;
+    load_a(s + 1 < nk ? s + 1 : nk - 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk < 3) {
+        read_a(u, kk + 1, (kk + 1) & 1);
+        weights(u, kk + 1, (kk + 1) & 1);
+      } else {
+        load_w(s + 2 < nk ? s + 2 : nk - 1, u);
+        if (s + 1 < nk) write_a(u ^ 1);
+      }
+      mfma(kk & 1);
+    }
+    lds_barrier();
+    if (s + 1 < nk) {
+      scales(u ^ 1);
+      read_a(u ^ 1, 0, 0);
+      weights(u ^ 1, 0, 0);
+    }
+  };
+  int s = 0;
+  for (; s + 2 <= nk; s += 2) {
+    step(std::integral_constant<int, 0>{}, s);
+    step(std::integral_constant<int, 1>{}, s + 1);
+  }
+  if (s < nk) step(std::integral_constant<int, 0>{}, s);
+
+  // accumulator r of lane l: C[m = 32i + l%32][n = 32j + (r/4)*8 + (l/32)*4 + r%4]
+  auto store = [&]() {
+    const bool vec = (N & 3) == 0 && ((uintptr_t)C & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int gm = m0 + 32 * i + r32;
+      if (gm >= M) continue;
+      float* crow = C + (size_t)gm * N;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int gn = n0 + wn + 32 * j + 8 * q + 4 * kb;
+          if (vec && gn + 3 < N) {
+            *reinterpret_cast<float4v*>(crow + gn) =
+                float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (gn + e < N) crow[gn + e] = acc[i][j][4 * q + e];
+          }
+        }
+    }
+  };
+  if constexpr (!SPLIT) {
+    store();
+    return;
+  }
+  // K split across workgroups: the fix-up of gemm_wq_kernel.
+  const int tile = blockIdx.x;
+  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
+  {
+    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          mine[((i * TN + j) * 4 + q) * NT + tid] =
+              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ uint32_t is_last;
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == (uint32_t)(KG - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  splitk_gather<TM, TN, NT, (TM % 2 == 0) ? TM / 2 : TM>(acc, tile_ws, BM * BN / 4, KG, tid);
+  store();
+  if (tid == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// K % 64 == 0.  K split over kg = 1, 2, 4, 8 workgroups per tile as in
+// gemm_wq_launch, with at least 8 K steps per part.
+template <class QF, int TM, int TN, int NW>
+hipError_t gemm_f32a_launch(const float* a, const uint8_t* w, float* c, uint32_t M, uint32_t N, uint32_t K,
+                            const nfhip::Workspace& ws, hipStream_t s) {
+  constexpr int BM = 32 * TM, BN = 32 * TN * NW;
+  const long tiles = (long)((N + BN - 1) / BN) * ((M + BM - 1) / BM);
+  if (tiles > (1L << 31) - 1 || K % kBK != 0) return hipErrorInvalidConfiguration;
+  const int nk = (int)(K / kBK);
+  static const int kg_max = [] {
+    const char* e = std::getenv("NF_HIP_GEMM_SPLITK_MAX");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 ? v : 8;
+  }();
+  constexpr long kCUs = 256;
+  int kg = 1;
+  long best = ((tiles + kCUs - 1) / kCUs) * nk;
+  for (int g = 2; g <= kg_max && g <= 8 && nk / g >= 8 && tiles <= (long)ws.cnt_len &&
+                  (size_t)tiles * g * BM * BN <= ws.part_floats;
+       g *= 2) {
+    const long cost = ((tiles * g + kCUs - 1) / kCUs) * ((nk + g - 1) / g);
+    if (cost < best) best = cost, kg = g;
+  }
+  const size_t lds = (size_t)2 * 3 * BM * 64 * sizeof(uint16_t);
+  if (kg == 1) {
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f32a_kernel<QF, TM, TN, NW, false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    gemm_f32a_kernel<QF, TM, TN, NW, false><<<dim3((unsigned)tiles), dim3(64 * NW), lds, s>>>(a, w, c, M, N, K,
+                                                                                             ws.part, ws.cnt);
+  } else {
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f32a_kernel<QF, TM, TN, NW, true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    gemm_f32a_kernel<QF, TM, TN, NW, true><<<dim3((unsigned)tiles, (unsigned)kg), dim3(64 * NW), lds, s>>>(
+        a, w, c, M, N, K, ws.part, ws.cnt);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace nfk
 
 namespace nfhip {
@@ -1554,7 +1867,19 @@ hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t
 
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                             uint32_t N, uint32_t K, int tile, const Workspace& ws, hipStream_t s) {
-  if (t != EType::F16) return hipErrorInvalidValue;  // f32 path uses the skinny kernels
+  if (t == EType::F32) {  // f32 activations and output: bf16-piece MFMA kernel
+    const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
+    if (K % 64 != 0 || !aligned) return hipErrorInvalidValue;
+    const float* a = static_cast<const float*>(A);
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    float* c = static_cast<float*>(C);
+    if (M <= 64)
+      return q == QFmt::Q4_0 ? nfk::gemm_f32a_launch<nfk::Q4_0, 2, 2, 4>(a, w, c, M, N, K, ws, s)
+                             : nfk::gemm_f32a_launch<nfk::Q8_0, 2, 2, 4>(a, w, c, M, N, K, ws, s);
+    return q == QFmt::Q4_0 ? nfk::gemm_f32a_launch<nfk::Q4_0, 4, 2, 4>(a, w, c, M, N, K, ws, s)
+                           : nfk::gemm_f32a_launch<nfk::Q8_0, 4, 2, 4>(a, w, c, M, N, K, ws, s);
+  }
+  if (t != EType::F16) return hipErrorInvalidValue;
   const nfk::half_t* a = static_cast<const nfk::half_t*>(A);
   const uint8_t* w = static_cast<const uint8_t*>(W);
   nfk::half_t* c = static_cast<nfk::half_t*>(C);

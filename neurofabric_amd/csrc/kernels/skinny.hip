@@ -47,9 +47,6 @@
 
 namespace nfk {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-typedef float float2s __attribute__((ext_vector_type(2)));
 
 template <class QF> struct SkW;
 template <> struct SkW<Q4_0> {
@@ -115,12 +112,6 @@ __device__ __forceinline__ half8 sk_b_f16(const uint32_t (&w)[SkW<QF>::kLoads], 
   return __builtin_bit_cast(half8, o);
 }
 
-// Two floats -> their bf16 pair, exact when each float has <= 8 significant
-// bits (upper halves of the f32 patterns).
-__device__ __forceinline__ uint32_t pack_hi16(float a, float b) {
-  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, a), 0x07060302u);
-}
-
 // B operand, f32 path: the codes of the lane's slot as exact bf16 (Q4_0: n*u
 // with n the unsigned nibble; Q8_0: the signed code).
 template <class QF>
@@ -159,24 +150,6 @@ template <> struct SkK<Q8_0> {  // k = 8s..8s+7
   __device__ static int off1(int s) { return 8 * s + 4; }
 };
 
-// Exact three-way bf16 split of 8 floats.
-__device__ __forceinline__ void split3(const float (&x)[8], bf16x8& p1, bf16x8& p2, bf16x8& p3) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float2s v = {x[2 * j], x[2 * j + 1]};
-    const bf16x2v h1 = __builtin_convertvector(v, bf16x2v);
-    const float2s r1 = v - __builtin_convertvector(h1, float2s);
-    const bf16x2v h2 = __builtin_convertvector(r1, bf16x2v);
-    const float2s r2 = r1 - __builtin_convertvector(h2, float2s);
-    const bf16x2v h3 = __builtin_convertvector(r2, bf16x2v);
-    p1[2 * j] = h1[0];
-    p1[2 * j + 1] = h1[1];
-    p2[2 * j] = h2[0];
-    p2[2 * j + 1] = h2[1];
-    p3[2 * j] = h3[0];
-    p3[2 * j + 1] = h3[1];
-  }
-}
 
 // Staging piece of a weight chunk: 4 B per pair of the chunk (16 B for
 // 4-pair chunks, 8 B for 2-pair, 4 B for 1-pair), so a row of a chunk is

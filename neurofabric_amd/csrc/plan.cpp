@@ -183,14 +183,14 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
       if (p.M <= gemv_max && (gemv_fits || K % 256 != 0)) {
         p.path = Path::Gemv;
         p.kernel = "gemv_" + tag;
-      } else if (K % 256 == 0 && (!f16 || p.M <= tuning.skinny_max_m_f16)) {
+      } else if (K % 256 == 0 && p.M <= (f16 ? tuning.skinny_max_m_f16 : tuning.skinny_max_m_f32)) {
         p.path = Path::Skinny;
         p.kernel = "skinny_mfma_" + tag;
-      } else if (f16) {
+      } else if (f16 || K % 64 == 0) {
         p.path = Path::GemmMfma;
         p.kernel = "gemm_mfma_" + tag;
       } else {
-        p.path = Path::Gemv;  // f32 with K % 256 != 0
+        p.path = Path::Gemv;  // f32 with K % 64 != 0
         p.kernel = "gemv_" + tag;
       }
     }

@@ -72,19 +72,24 @@ struct LayerParams {
 
 // Switch points between the kernel families of the fused op: the VALU GEMV
 // while M <= gemv_max_m (and its activation stage fits in LDS), the
-// small-batch MFMA kernel while M <= skinny_max_m (the f32 path stays there
-// for every larger M, 32 rows per launch), the tiled MFMA GEMM above (f16).
+// small-batch MFMA kernel while M <= skinny_max_m (f16 and f32 activations
+// each have their own; at most 32 f32 rows per launch), the tiled MFMA GEMM
+// above (f16: fp16 MFMA; f32: bf16-piece MFMA, K % 64 == 0, else the GEMV).
 // Defaults from the measured crossover sweep on MI355X (bench.py's configs[4]
 // section: 28672x8192 and 8192x28672 Q4_0, f16 activations, graph replay
 // over 4 weight copies): the GEMV is fastest up to M = 4 wherever its
 // activation stage fits (M = 4 at 28672x8192: 51.2 vs 53.0 us for the
 // small-batch kernel), the small-batch kernel up to M = 16 (64.5 vs 88.8 us
 // and 94.3 vs 97.7 us), the tiled GEMM from M = 32 (88.6 vs 89.3 us and
-// 95.8 vs 144.0 us).
+// 95.8 vs 144.0 us).  f32 activations (Q8_0 14336x4096 / 4096x14336 and
+// Q4_0 4096x4096, graph replay over 4 weight copies): the small-batch kernel
+// up to M = 48 (61.3 vs 80.7 us at 14336x4096), the bf16-piece tiled GEMM
+// from M = 64 (79.7 / 116.6 / 37.5 us against 74.8 / 176.5 / 58.0 us).
 struct Tuning {
   uint32_t gemv_max_m_f32 = 4;
   uint32_t gemv_max_m_f16 = 4;
   uint32_t skinny_max_m_f16 = 16;
+  uint32_t skinny_max_m_f32 = 48;
   // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernels
   // (default: two waves per SIMD where it applies and measured faster),
   // 0..6 = one of the LDS-staged tile shapes, 7 = the register-dequantizing

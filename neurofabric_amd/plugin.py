@@ -73,6 +73,10 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     lib.nf_hip_get_gemm_tile.restype = C.c_int32
     lib.nf_hip_get_skinny_max_m.argtypes = []
     lib.nf_hip_get_skinny_max_m.restype = C.c_uint32
+    lib.nf_hip_set_skinny_max_m_f32.argtypes = [C.c_uint32]
+    lib.nf_hip_set_skinny_max_m_f32.restype = None
+    lib.nf_hip_get_skinny_max_m_f32.argtypes = []
+    lib.nf_hip_get_skinny_max_m_f32.restype = C.c_uint32
     lib.nf_hip_get_stream.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
     lib.nf_hip_get_stream.restype = C.c_int
     lib.nf_hip_run_tasks.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32]
@@ -329,8 +333,11 @@ class Provider:
     def set_gemv_max_m(self, f32: int, f16: int) -> None:
         self.lib.nf_hip_set_gemv_max_m(f32, f16)
 
-    def set_skinny_max_m(self, f16: int) -> None:
+    def set_skinny_max_m(self, f16: int, f32: int | None = None) -> None:
+        """Largest M on the small-batch kernel for f16 (and, if given, f32) activations."""
         self.lib.nf_hip_set_skinny_max_m(f16)
+        if f32 is not None:
+            self.lib.nf_hip_set_skinny_max_m_f32(f32)
 
     def release_staging(self) -> None:
         self.lib.nf_hip_release_staging(self.handle)
@@ -350,6 +357,18 @@ class Provider:
 
     def get_skinny_max_m(self) -> int:
         return self.lib.nf_hip_get_skinny_max_m()
+
+    def get_skinny_max_m_f32(self) -> int:
+        return self.lib.nf_hip_get_skinny_max_m_f32()
+
+    def get_tuning(self) -> tuple:
+        """Every switch point and the GEMM kernel choice, for set_tuning."""
+        return (self.get_gemv_max_m(), self.get_skinny_max_m(), self.get_skinny_max_m_f32(), self.get_gemm_tile())
+
+    def set_tuning(self, t: tuple) -> None:
+        self.set_gemv_max_m(*t[0])
+        self.set_skinny_max_m(t[1], t[2])
+        self.set_gemm_tile(t[3])
 
     def get_gemv_max_m(self):
         a, b = C.c_uint32(), C.c_uint32()

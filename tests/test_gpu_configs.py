@@ -2,7 +2,9 @@
 
 configs[1] TinyLlama q/o and gate/up at M = 4 and 16; configs[2] Llama-2-7B
 prefill at M = 2048 (the non-split tiled GEMM grid); configs[3] Llama-3-8B
-Q8_0 FFN shapes and the 128256 x 4096 lm_head at M = 1, 16 and 64;
+Q8_0 FFN shapes and the 128256 x 4096 lm_head at M = 1, 16 and 64 (f32
+activations: GEMV, small-batch kernel, bf16-piece tiled GEMM), and the FFN
+shapes through the f32 families the switch points do not pick;
 configs[4] the Llama-70B FFN pair at every M of the crossover sweep, through
 the kernel the switch points select and through each kernel family forced.
 
@@ -97,10 +99,10 @@ def _force(provider, path):
         provider.set_gemv_max_m(1 << 30, 1 << 30)
     elif path == "skinny":
         provider.set_gemv_max_m(0, 0)
-        provider.set_skinny_max_m(1 << 30)
+        provider.set_skinny_max_m(1 << 30, 1 << 30)
     else:
         provider.set_gemv_max_m(0, 0)
-        provider.set_skinny_max_m(0)
+        provider.set_skinny_max_m(0, 0)
 
 
 class forced:
@@ -108,14 +110,13 @@ class forced:
         self.provider, self.path = provider, path
 
     def __enter__(self):
-        self.old = (self.provider.get_gemv_max_m(), self.provider.get_skinny_max_m())
+        self.old = self.provider.get_tuning()
         if self.path:
             _force(self.provider, self.path)
         return self
 
     def __exit__(self, *exc):
-        self.provider.set_gemv_max_m(*self.old[0])
-        self.provider.set_skinny_max_m(self.old[1])
+        self.provider.set_tuning(self.old)
 
 
 # ---- TinyLlama decode projections not covered elsewhere ----------------
@@ -140,6 +141,20 @@ def test_config2_prefill_m2048(provider, oracle_mod, weights, NK):
 @pytest.mark.parametrize("NK", [(14336, 4096), (4096, 14336), (128256, 4096)], ids=["gate_up", "down", "lm_head"])
 def test_config3_q8_0_ffn_and_lm_head(provider, oracle_mod, weights, M, NK):
     check_config(provider, oracle_mod, weights, "q8_0", M, *NK, f16=False, seed=M * 5 + NK[0])
+
+
+@pytest.mark.parametrize("path,M", [("tiled", 1), ("tiled", 16), ("tiled", 40), ("skinny", 64)],
+                         ids=lambda v: str(v))
+@pytest.mark.parametrize("NK", [(14336, 4096), (4096, 14336)], ids=["gate_up", "down"])
+def test_config3_forced_family(provider, oracle_mod, weights, path, M, NK):
+    """The f32 families the switch points do not pick at these M: the
+    bf16-piece tiled GEMM at small batches, the small-batch kernel at M = 64
+    (two launches of 32 rows)."""
+    with forced(provider, path):
+        kernel = planned_kernel(provider, "q8_0", M, *NK, False)
+        want = {"skinny": "skinny_mfma_", "tiled": "gemm_mfma_"}[path]
+        assert kernel.startswith(want), f"forced {path} planned {kernel}"
+        check_config(provider, oracle_mod, weights, "q8_0", M, *NK, f16=False, seed=7 * M + NK[1])
 
 
 # ---- configs[4]: Llama-70B FFN crossover sweep ------------------------------------------

@@ -97,15 +97,14 @@ def test_config2_prefill_sampled_columns(provider, oracle_mod, M, N, K):
 
 def _force_path(provider, path, f16):
     """Pin the switch points so `path` ('gemv', 'skinny', 'tiled') serves every M."""
-    g32, g16 = provider.get_gemv_max_m()
     if path == "gemv":
         provider.set_gemv_max_m(1 << 30, 1 << 30)
     elif path == "skinny":
         provider.set_gemv_max_m(0, 0)
-        provider.set_skinny_max_m(1 << 30)
+        provider.set_skinny_max_m(1 << 30, 1 << 30)
     else:
         provider.set_gemv_max_m(0, 0)
-        provider.set_skinny_max_m(0)
+        provider.set_skinny_max_m(0, 0)
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
@@ -113,22 +112,22 @@ def _force_path(provider, path, f16):
 @pytest.mark.parametrize("M", [3, 24, 64, 100])
 def test_kernel_paths_agree(provider, oracle_mod, fmt, f16, M):
     """The same inputs through every kernel family that serves the op (GEMV,
-    small-batch MFMA, and for f16 the tiled MFMA GEMM) each match the oracle
-    within the tolerance; N and M are not multiples of any tile."""
+    small-batch MFMA, tiled MFMA GEMM: fp16 MFMA for f16 activations, bf16
+    pieces for f32) each match the oracle within the tolerance; N and M are
+    not multiples of any tile."""
     N, K = 392, 1024
-    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    old = provider.get_tuning()
     W = syn.weights(fmt, N, K, seed=3 + M)
     A = syn.activations(M, K, seed=4 + M, dtype=np.float16 if f16 else np.float32)
     ref = oracle_mod.fused(A, W, fmt, M, N, K, f16=f16)
     ref = (ref.view(np.float16) if f16 else ref).astype(np.float32)
     try:
-        for path in ("gemv", "skinny", "tiled") if f16 else ("gemv", "skinny"):
+        for path in ("gemv", "skinny", "tiled"):
             _force_path(provider, path, f16)
             got = run_fused(provider, fmt, A, W, M, N, K, f16).astype(np.float32)
             assert_close(got, ref, what=f"{path} {fmt} f16={f16} M={M}")
     finally:
-        provider.set_gemv_max_m(*old[0])
-        provider.set_skinny_max_m(old[1])
+        provider.set_tuning(old)
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
@@ -141,13 +140,12 @@ def test_skinny_mfma_shapes(provider, oracle_mod, fmt, f16, shape):
     K split and the LDS combine), rows beyond one launch (32 for f32, 64 for
     f16); K % 256 != 0 falls back to the GEMV."""
     M, N, K = shape
-    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    old = provider.get_tuning()
     try:
         _force_path(provider, "skinny", f16)
         check_fused(provider, oracle_mod, fmt, M, N, K, f16=f16, seed=M * 7 + N)
     finally:
-        provider.set_gemv_max_m(*old[0])
-        provider.set_skinny_max_m(old[1])
+        provider.set_tuning(old)
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
@@ -157,13 +155,12 @@ def test_gemv_large_activation_staging(provider, oracle_mod, fmt, f16, shape):
     """GEMV with the activations' LDS stage above 64 KB (opt-in dynamic LDS):
     M = 3..4 rows of long K."""
     M, N, K = shape
-    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    old = provider.get_tuning()
     try:
         _force_path(provider, "gemv", f16)
         check_fused(provider, oracle_mod, fmt, M, N, K, f16=f16, seed=M + N + K)
     finally:
-        provider.set_gemv_max_m(*old[0])
-        provider.set_skinny_max_m(old[1])
+        provider.set_tuning(old)
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
@@ -178,7 +175,7 @@ def test_tiled_gemm_split_k(provider, oracle_mod, fmt, tile, shape):
     the one-wave kernel), which the default picks only from M = 1024."""
     M, N, K = shape
     W = syn.weights(fmt, N, K, seed=N + 1)
-    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m(), provider.get_gemm_tile())
+    old = provider.get_tuning()
     try:
         _force_path(provider, "tiled", True)
         provider.set_gemm_tile(tile)
@@ -190,9 +187,7 @@ def test_tiled_gemm_split_k(provider, oracle_mod, fmt, tile, shape):
             assert_close(got[:, cols[0]:cols[1]].astype(np.float32), ref[:, cols[0]:cols[1]].astype(np.float32),
                          what=f"{fmt} {M}x{N}x{K} call {rep}")
     finally:
-        provider.set_gemv_max_m(*old[0])
-        provider.set_skinny_max_m(old[1])
-        provider.set_gemm_tile(old[2])
+        provider.set_tuning(old)
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
@@ -213,34 +208,69 @@ def test_gemm_kernels_edges(provider, oracle_mod, fmt, tile, shape):
     M, N, K = shape
     W = syn.weights(fmt, N, K, seed=N + K)
     A = syn.activations(M, K, seed=M + K, dtype=np.float16)
-    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m(), provider.get_gemm_tile())
+    old = provider.get_tuning()
     try:
         _force_path(provider, "tiled", True)
         provider.set_gemm_tile(tile)
         got = run_fused(provider, fmt, A, W, M, N, K, True)
     finally:
-        provider.set_gemv_max_m(*old[0])
-        provider.set_skinny_max_m(old[1])
-        provider.set_gemm_tile(old[2])
+        provider.set_tuning(old)
     ref = oracle_mod.fused(A, W, fmt, M, N, K, f16=True, threads=8).view(np.float16)
     assert_close(got.astype(np.float32), ref.astype(np.float32), what=f"{fmt} tile {tile} {M}x{N}x{K}")
 
 
-def test_skinny_f32_large_activations(provider, oracle_mod):
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("shape", [(33, 130, 512), (64, 96, 1024), (100, 777, 448), (129, 260, 64),
+                                   (257, 514, 192), (200, 520, 8192), (65, 300, 16384), (512, 4096, 4096)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_f32_tiled_gemm(provider, oracle_mod, fmt, shape):
+    """The f32-activation tiled GEMM (exact bf16 pieces on bf16 MFMA) against
+    the oracle: M and N past tile edges (64- and 128-row tiles), N % 4 != 0,
+    1..7 K steps and long K split over workgroups (two calls in a row: the
+    per-tile counters must be back at zero)."""
+    M, N, K = shape
+    W = syn.weights(fmt, N, K, seed=N + 2 * K)
+    old = provider.get_tuning()
+    try:
+        _force_path(provider, "tiled", False)
+        for rep in range(2 if K >= 8192 else 1):
+            A = syn.activations(M, K, seed=M + K + rep, dtype=np.float32)
+            cols = (0, N) if N <= 1024 else (N - 256, N)
+            got = run_fused(provider, fmt, A, W, M, N, K, False)
+            ref = oracle_mod.fused(A, W, fmt, M, N, K, cols=cols, threads=8)
+            assert_close(got[:, cols[0]:cols[1]], ref[:, cols[0]:cols[1]], what=f"{fmt} {M}x{N}x{K} call {rep}")
+    finally:
+        provider.set_tuning(old)
+
+
+@pytest.mark.parametrize("path", ["skinny", "tiled"])
+def test_f32_large_activations(provider, oracle_mod, path):
     """The exact three-way bf16 split keeps f32 activations far outside the
-    fp16 range (|x| ~ 1e6 and 1e-6) exact before accumulation."""
-    M, N, K = 8, 128, 512
+    fp16 range (|x| ~ 1e6 and 1e-6) exact before accumulation, on both
+    bf16-piece kernels.  With such data most outputs are sums that cancel to
+    far below their terms, where any two fp32 summation orders (the oracle's
+    sequential one included) differ by more than 1e-3 of the result; so each
+    output is held to the fp32 summation bound |got - exact| <= 4 K 2^-24
+    sum_k |x_k w_k| against the float64 result, and to 1e-3 normwise against
+    the oracle.  A lost piece (fp16 overflow at 1e6, underflow at 1e-6, or a
+    dropped term) breaks the bound by orders of magnitude."""
+    M, N, K = 40, 128, 512
     W = syn.q4_0_weights(N, K, seed=11)
     rng = np.random.default_rng(5)
     A = (rng.standard_normal((M, K)) * np.where(rng.random((M, K)) < 0.5, 1e6, 1e-6)).astype(np.float32)
-    old = (provider.get_gemv_max_m(), provider.get_skinny_max_m())
+    old = provider.get_tuning()
     try:
-        _force_path(provider, "skinny", False)
-        got = run_fused(provider, "q4_0", A, W, M, N, K, False)
+        _force_path(provider, path, False)
+        got = run_fused(provider, "q4_0", A, W, M, N, K, False).astype(np.float64)
     finally:
-        provider.set_gemv_max_m(*old[0])
-        provider.set_skinny_max_m(old[1])
-    assert_close(got, oracle_mod.fused(A, W, "q4_0", M, N, K))
+        provider.set_tuning(old)
+    Wd = oracle_mod.dequant(W, "q4_0", N * K).astype(np.float64).reshape(N, K)
+    exact = A.astype(np.float64) @ Wd.T
+    bound = 4 * K * 2.0 ** -24 * (np.abs(A.astype(np.float64)) @ np.abs(Wd).T)
+    worst = float(np.max(np.abs(got - exact) / bound))
+    assert worst <= 1.0, f"{path}: error {worst:.3g} x the fp32 summation bound"
+    ref = oracle_mod.fused(A, W, "q4_0", M, N, K)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) <= 1e-3
 
 
 # ---- the reference's fused-vs-separate test (fused_matmul_test.cpp:134-285) ----------

@@ -267,22 +267,24 @@ def test_crossover_setter_roundtrip():
         assert p["kernel"] == "skinny_mfma_q4_0_f32"
     finally:
         prov.set_gemv_max_m(*old)
-    old_s = prov.get_skinny_max_m()
+    old_s = (prov.get_skinny_max_m(), prov.get_skinny_max_m_f32())
     try:
-        prov.set_skinny_max_m(5)
-        assert prov.get_skinny_max_m() == 5
+        prov.set_skinny_max_m(5, 7)
+        assert (prov.get_skinny_max_m(), prov.get_skinny_max_m_f32()) == (5, 7)
         p = _fused(prov.lib, 6, 64, 256, a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16)
         assert p["kernel"] == "gemm_mfma_q4_0_f16"
-        # f32 activations have no tiled GEMM: every M above the GEMV stays skinny
-        assert _fused(prov.lib, 600, 64, 256)["kernel"] == "skinny_mfma_q4_0_f32"
+        assert _fused(prov.lib, 7, 64, 256)["kernel"] == "skinny_mfma_q4_0_f32"
+        assert _fused(prov.lib, 8, 64, 256)["kernel"] == "gemm_mfma_q4_0_f32"
+        assert _fused(prov.lib, 600, 64, 256)["kernel"] == "gemm_mfma_q4_0_f32"
     finally:
-        prov.set_skinny_max_m(old_s)
+        prov.set_skinny_max_m(*old_s)
 
 
 def test_default_switch_points(lib):
     """Defaults from the measured configs[4] sweep: GEMV for M <= 4 while
     its activation stage fits in 120 KB of LDS, the small-batch MFMA kernel
-    up to 16 rows, the tiled GEMM beyond (f16)."""
+    up to 16 rows, the tiled GEMM beyond (f16); for f32 activations the
+    small-batch kernel up to 48 rows."""
     f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
     assert _fused(lib, 4, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"   # 4 x 8192 x 2 B = 64 KB
     assert _fused(lib, 4, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"  # 4 x 28672 x 2 B > 120 KB
@@ -294,6 +296,12 @@ def test_default_switch_points(lib):
     assert _fused(lib, 2, 28672, 8192)["kernel"] == "gemv_q4_0_f32"           # 2 x 8192 x 4 B + sums
     assert _fused(lib, 3, 28672, 8192)["kernel"] == "skinny_mfma_q4_0_f32"    # 4 x 8192 x 4 B > 120 KB
     assert _fused(lib, 16, 4096, 4096)["kernel"] == "skinny_mfma_q4_0_f32"
+    # f32 activations: small-batch kernel up to 48 rows, then the bf16-piece
+    # tiled GEMM (K % 64 == 0), else the GEMV
+    assert _fused(lib, 48, 14336, 4096, op="dequant_q8_0_linear", bs=34)["kernel"] == "skinny_mfma_q8_0_f32"
+    assert _fused(lib, 49, 14336, 4096, op="dequant_q8_0_linear", bs=34)["kernel"] == "gemm_mfma_q8_0_f32"
+    assert _fused(lib, 512, 4096, 11008)["kernel"] == "gemm_mfma_q4_0_f32"
+    assert _fused(lib, 100, 64, 96)["kernel"] == "gemv_q4_0_f32"  # K % 64 != 0
 
 
 # Every op name of the Metal provider's dispatch map (metal_provider.mm:3180-3209,
