@@ -25,8 +25,9 @@
 //   * A row is covered by a group of L lanes (L = 16, 32 or 64, chosen on the
 //     host so the pairs of a row spread evenly); a wave holds 64/L groups and
 //     each group works on R2 rows at once, reading each activation chunk
-//     from LDS once for all R2 rows.  The next pair's weights are loaded
-//     before the current pair is computed.
+//     from LDS once for all R2 rows.  The weights of the next pair (two
+//     pairs ahead when a lane has three or more) are loaded before the
+//     current pair is computed.
 //   * Partial sums are reduced across the L lanes of a group with DPP adds;
 //     the group's last lane writes the R2 x M outputs.
 //   * The grid is capped at two workgroups per CU; larger row counts loop,
@@ -413,10 +414,7 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
     }
   };
 
-  // The first weights are requested before A is staged, so the two memory
-  // round trips overlap.
-  uint32_t wa[R2][DW], wb[R2][DW];
-  if (T > 0) next_load(wa);
+  uint32_t wa[R2][DW], wb[R2][DW], wc[R2][DW];  // wc: only with k3Sets
 
   // ---- stage A into LDS (and the per-block sums of x) ----
   // Thread tid takes 16-byte chunks tid, tid + 256, ... of the M x K
@@ -435,6 +433,12 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
         const int c = c0 + u * 256 + tid;
         v[u] = *reinterpret_cast<const ChunkT*>(A + (size_t)(c < total ? c : total - 1) * EPC);
       }
+      // The first weights are requested right after the first activation
+      // loads, so the two memory round trips overlap; after them, not
+      // before: loads complete in issue order, and the activations (L2
+      // resident) can then be staged while the weights (HBM) are in flight
+      // (measured on MI355X: 3.3 against 3.8 us at 2048 x 2048).
+      if (c0 == 0 && T > 0) next_load(wa);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int c = c0 + u * 256 + tid;
@@ -505,17 +509,38 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
     }
   };
 
-  // Two register sets: the loads for step t+1 are in flight while step t
-  // computes.
-  for (int t = 0; t < T; t += 2) {
+  // Register sets in rotation: with three or more steps the loads run two
+  // steps ahead (three sets; measured 8.1 against 8.8 us at 11008 x 4096),
+  // else one step ahead (two sets; the extra set's loads would be wasted).
+  // One row per lane group only (two rows with three sets measured slower).
+  constexpr bool k3Sets = R2 == 1;
+  if (k3Sets && T >= 3) {
     next_load(wb);
-    __builtin_amdgcn_sched_barrier(0);
-    step(wa);
-    __builtin_amdgcn_sched_barrier(0);
-    next_load(wa);
-    __builtin_amdgcn_sched_barrier(0);
-    if (t + 1 < T) step(wb);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int t = 0; t < T; t += 3) {
+      next_load(wc);
+      __builtin_amdgcn_sched_barrier(0);
+      step(wa);
+      __builtin_amdgcn_sched_barrier(0);
+      next_load(wa);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < T) step(wb);
+      __builtin_amdgcn_sched_barrier(0);
+      next_load(wb);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 2 < T) step(wc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    for (int t = 0; t < T; t += 2) {
+      next_load(wb);
+      __builtin_amdgcn_sched_barrier(0);
+      step(wa);
+      __builtin_amdgcn_sched_barrier(0);
+      next_load(wa);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < T) step(wb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
@@ -679,25 +704,18 @@ hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint
   // The grid is capped at two workgroups per CU, which loop over the rows
   // reusing their staged activations (measured on MI355X: at 4096x4096 the
   // capped grid takes 5.8 us against 6.6 us for one workgroup per 4 rows).
-  // One row per lane group while that needs at most 8 workgroups per CU,
-  // else two rows per lane group (more loads in flight per lane).
+  // One row per lane group: with the loads two steps ahead (three register
+  // sets) that keeps enough bytes in flight, and it measured faster than two
+  // rows per lane group with one step ahead (11008 x 4096: 8.1 against
+  // 9.5 us; 32000 x 2048: 10.2 against 11.0 us).
   static const long cap = [] {
     const char* e = std::getenv("NF_HIP_GEMV_WG_CAP");  // tuning override
     const long v = e ? std::atol(e) : 0;
     return v > 0 ? v : 256L * 2;
   }();
-  const long wgs1 = ((long)N + 4L * R - 1) / (4L * R);
-  const long wgs2 = ((long)N + 8L * R - 1) / (8L * R);
-  g.R2 = wgs1 <= 256L * 8 ? 1 : 2;
-  const long wgs = g.R2 == 1 ? wgs1 : wgs2;
+  const long wgs = ((long)N + 4L * R - 1) / (4L * R);
+  g.R2 = 1;
   g.grid = (unsigned)(wgs < cap ? wgs : cap);
-  if (g.R2 == 2) {
-    switch (g.MM) {
-      case 1: return gemv_pair_launch<QF, XT, 2, 1>(g, A, W, C, M, N, K, s);
-      case 2: return gemv_pair_launch<QF, XT, 2, 2>(g, A, W, C, M, N, K, s);
-      default: return gemv_pair_launch<QF, XT, 2, 4>(g, A, W, C, M, N, K, s);
-    }
-  }
   switch (g.MM) {
     case 1: return gemv_pair_launch<QF, XT, 1, 1>(g, A, W, C, M, N, K, s);
     case 2: return gemv_pair_launch<QF, XT, 1, 2>(g, A, W, C, M, N, K, s);
