@@ -71,7 +71,7 @@ def parse(argv=None):
     ap.add_argument("--no-extra", action="store_true", help="only the headline decode step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
-    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "c7b", "dq", "up", "layer"], default=None,
+    ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "c7b", "dq", "up", "layer", "floor"], default=None,
                     help="run one configs[i] section alone and print its JSON (profiling aid)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 4 device-to-device copies of BYTES (reference for HBM byte counters)")
@@ -216,6 +216,53 @@ def rotated_linear(prov, fmt, M, N, K, f16: bool, copies: int) -> Step:
         st.buffers.append(w)
         st.add(op, [a, w], [c], M, N, K)
     return st.finish()
+
+
+FLOOR_SHAPES = ((2048, 2048, "tinyllama q/o 2048x2048"), (5632, 2048, "tinyllama gate/up 5632x2048"),
+                (2048, 5632, "tinyllama down 2048x5632"), (32000, 2048, "tinyllama lm_head 32000x2048"),
+                (4096, 4096, "llama-7b q/k/v/o 4096x4096"), (11008, 4096, "llama-7b gate/up 11008x4096"),
+                (4096, 11008, "llama-7b down 4096x11008"))
+
+
+def launch_floor(prov, shapes=FLOOR_SHAPES, copies: int = 64) -> dict:
+    """Per-launch cost of the decode GEMV beside the floors under it, each as
+    graph-replay launch-to-launch time over `copies` distinct weight buffers
+    (HIP events on the provider stream): an empty kernel; a kernel that only
+    streams the same weight bytes (nf_hip_diag_stream_read: every 16-byte
+    chunk loaded once, all loads of a thread in flight, nothing stored); and
+    the fused Q4_0 GEMV (M = 1, f32 activations) over those bytes."""
+    from neurofabric_amd import hiprt
+    stream = prov.stream()
+
+    def replay(fn, steps=10):
+        g = hiprt.Graph(stream, fn)
+        for _ in range(3):
+            g.launch()
+        hiprt.device_synchronize()
+        e0, e1 = hiprt.Event(), hiprt.Event()
+        e0.record(stream)
+        for _ in range(steps):
+            g.launch()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) * 1e3 / steps
+
+    out = {"empty_kernel_us": replay(lambda: [prov.diag_stream_read(0, 0) for _ in range(copies)]) / copies}
+    log(f"[bench] floor: empty kernel {out['empty_kernel_us']:.2f} us/launch")
+    for N, K, name in shapes:
+        st = rotated_linear(prov, "q4_0", 1, N, K, False, copies)
+        wbytes = N * (K // 32) * 18
+        ptrs = [b.device_ptr() for b in st.buffers[2:]]
+        read_us = replay(lambda: [prov.diag_stream_read(p, wbytes) for p in ptrs]) / copies
+        r = time_step(prov, st, 10, 2, "graph")
+        gemv_us = r["us_per_launch"]
+        st.release()
+        out[name] = {"weight_bytes": wbytes, "read_us": read_us, "read_GB_s": wbytes / read_us / 1e3,
+                     "gemv_us": gemv_us, "gemv_GB_s": wbytes / gemv_us / 1e3,
+                     "gemv_over_read_us": gemv_us - read_us}
+        log(f"[bench] floor {name}: read {read_us:.2f} us ({wbytes / read_us / 1e3:.0f} GB/s), "
+            f"fused GEMV {gemv_us:.2f} us ({wbytes / gemv_us / 1e3:.0f} GB/s)")
+    return out
 
 
 def time_step(prov, st: Step, steps: int, warmup: int, mode: str) -> dict:
@@ -664,7 +711,7 @@ def main(argv=None) -> int:
                     "c3": lambda: run_c3(prov, args.mode), "c4": lambda: crossover_sweep(prov),
                     "c7b": lambda: run_step(prov, syn.llama2_7b_step_shapes(), "q4_0", 1, 10, 2, args.mode),
                     "dq": lambda: run_dq(prov), "up": lambda: run_upload(prov),
-                    "layer": lambda: run_layer(prov)}
+                    "layer": lambda: run_layer(prov), "floor": lambda: launch_floor(prov)}
         print(json.dumps({args.only: sections[args.only]()}), flush=True)
         return 0
 
@@ -721,6 +768,7 @@ def main(argv=None) -> int:
         extra["dequant_7b_ffn_weight"] = run_dq(prov)
         extra["weight_upload_512MiB"] = run_upload(prov)
         extra["layer_ops"] = run_layer(prov)
+        extra["gemv_launch_floor"] = launch_floor(prov)
 
     cpu = None
     if not args.no_cpu:

@@ -165,6 +165,16 @@ NF_API nf_status nf_hip_run_tasks(nf_provider self, const nf_task_desc *tasks, u
  * time to its kernel launches. */
 NF_API uint64_t nf_hip_launch_count(nf_provider self);
 
+/* Per-launch floor calibration for benchmarks: enqueues on `stream` (a
+ * hipStream_t, or NULL for the null stream) one kernel that reads the
+ * `bytes` at `src` (16-byte aligned; every 16-byte chunk loaded once, all
+ * loads of a thread in flight together, nothing stored), or an empty kernel
+ * when bytes < 16.  Timing it beside a fused GEMV over the same bytes
+ * separates the cost of moving the weights from the GEMV's own work.
+ * NF_ERROR_INVALID_ARG for a null or misaligned src.  No counterpart in
+ * the reference. */
+NF_API nf_status nf_hip_diag_stream_read(const void *src, uint64_t bytes, void *stream);
+
 /* The in-order hipStream_t (as void*) every dispatch is launched on, so a
  * caller can time or capture (hipStreamBeginCapture) a run of dispatches.
  * NF_ERROR_INVALID_ARG before init. */

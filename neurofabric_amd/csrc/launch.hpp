@@ -31,6 +31,10 @@ hipError_t launch_dequant(QFmt q, EType out_t, const void* w, uint64_t in_bytes,
 hipError_t launch_gemv(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                        uint32_t N, uint32_t K, hipStream_t s);
 
+// Launch-floor calibration: stream `bytes` from `src` (read only, nothing
+// stored), or an empty kernel when bytes < 16.
+hipError_t launch_diag_read(const void* src, uint64_t bytes, hipStream_t s);
+
 // Several decode GEMVs over the same activations A (same format, dtype, M
 // and K; each with its own weights, output and N) in one launch, each job
 // computed exactly as launch_gemv would.  hipErrorNotSupported when the

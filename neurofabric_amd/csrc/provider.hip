@@ -1091,6 +1091,12 @@ NF_API uint64_t nf_hip_launch_count(nf_provider self) {
   return p ? p->launch_groups.load(std::memory_order_relaxed) : 0;
 }
 
+NF_API nf_status nf_hip_diag_stream_read(const void* src, uint64_t bytes, void* stream) {
+  if (bytes >= 16 && (!src || (uintptr_t)src % 16 != 0))
+    return set_error(NF_ERROR_INVALID_ARG, "nf_hip_diag_stream_read: src must be 16-byte aligned");
+  return map_hip(launch_diag_read(src, bytes, static_cast<hipStream_t>(stream)), "nf_hip_diag_stream_read");
+}
+
 NF_API nf_status nf_hip_get_stream(nf_provider self, void** stream) {
   Provider* p = as_prov(self);
   if (!p || !stream) return NF_ERROR_INVALID_ARG;

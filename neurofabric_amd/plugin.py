@@ -73,6 +73,8 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     lib.nf_hip_get_gemm_tile.restype = C.c_int32
     lib.nf_hip_get_skinny_max_m.argtypes = []
     lib.nf_hip_get_skinny_max_m.restype = C.c_uint32
+    lib.nf_hip_diag_stream_read.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p]
+    lib.nf_hip_diag_stream_read.restype = C.c_int
     lib.nf_hip_set_skinny_max_m_f32.argtypes = [C.c_uint32]
     lib.nf_hip_set_skinny_max_m_f32.restype = None
     lib.nf_hip_get_skinny_max_m_f32.argtypes = []
@@ -357,6 +359,12 @@ class Provider:
 
     def get_skinny_max_m(self) -> int:
         return self.lib.nf_hip_get_skinny_max_m()
+
+    def diag_stream_read(self, dev_ptr: int, nbytes: int) -> None:
+        """Enqueue the launch-floor calibration read of `nbytes` at device
+        address `dev_ptr` on the provider stream (an empty kernel for < 16)."""
+        self.check(self.lib.nf_hip_diag_stream_read(C.c_void_p(dev_ptr), nbytes, C.c_void_p(self.stream())),
+                   "nf_hip_diag_stream_read")
 
     def get_skinny_max_m_f32(self) -> int:
         return self.lib.nf_hip_get_skinny_max_m_f32()

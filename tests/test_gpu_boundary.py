@@ -232,3 +232,21 @@ def test_timing_ring(provider):
 
 def test_get_stream(provider):
     assert provider.stream() != 0
+
+
+def test_diag_stream_read(provider):
+    """The launch-floor calibration read: an empty launch, reads of aligned
+    buffers of several sizes (every per-thread chunk count), and a misaligned
+    source rejected without a launch."""
+    for nbytes in (16, 4096, 1 << 21, (1 << 21) + 48, 40 << 20):
+        b = provider.alloc(abi.NF_DTYPE_U8, nbytes)
+        provider.diag_stream_read(b.device_ptr(), nbytes)
+        provider.synchronize()
+        b.release()
+    provider.diag_stream_read(0, 0)
+    provider.synchronize()
+    b = provider.alloc(abi.NF_DTYPE_U8, 4096)
+    with pytest.raises(NfError) as e:
+        provider.diag_stream_read(b.device_ptr() + 4, 1024)
+    assert e.value.status == abi.NF_ERROR_INVALID_ARG
+    b.release()
