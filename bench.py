@@ -441,6 +441,13 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
                     us = r["us_per_launch"]
                     row[path] = {"us": us, "GB_s": st.bytes / copies / (us * 1e-6) / 1e9,
                                  "TFLOP_s": st.flops / copies / (us * 1e-6) / 1e12, "kernel": kern}
+                # the family the default switch points pick for this M
+                prov.set_gemv_max_m(g32, g16)
+                prov.set_skinny_max_m(sk16)
+                sel = Step(prov)
+                sel.add("dequant_q4_0_linear_f16", [a, ws[0]], [c], M, N, K)
+                sel_kern = sorted(sel.kernels)[0]
+                row["selected_by_default"] = next((f for f, pre in family.items() if sel_kern.startswith(pre)), sel_kern)
                 a.release()
                 c.release()
                 fams = [k for k in pins if k in row]
@@ -457,12 +464,18 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
     # defaults: the largest M at which the family is the fastest on every
     # shape it serves (the GEMV does not serve the 28672-long rows beyond
     # M = 2: its activation stage would not fit in LDS).
+    shp = [k for k in out]
+
     def last_m(fam):
         ms = [m for m in Ms if any(fam in r for k in out for r in out[k]["rows"] if r["M"] == m) and
               all(r["fastest"] == fam for k in out for r in out[k]["rows"] if r["M"] == m and fam in r)]
         return max(ms) if ms else 0
     out["switch_points"] = {"measured": {"gemv_max_m_f16": last_m("gemv"), "skinny_max_m_f16": last_m("skinny")},
-                            "defaults": {"gemv_max_m_f16": g16, "skinny_max_m_f16": sk16}}
+                            "defaults": {"gemv_max_m_f16": g16, "skinny_max_m_f16": sk16,
+                                         "gemv_m3_m4_only_up_to_weight_MB": 48},
+                            "default_not_fastest": [(k, r["M"], r["selected_by_default"], r["fastest"])
+                                                    for k in shp for r in out[k]["rows"]
+                                                    if r["selected_by_default"] != r["fastest"]]}
     out["activations"] = "f16 N(0,1); weights Q4_0 per configs[0] statistics"
     return out
 
@@ -514,9 +527,37 @@ def run_c3(prov, mode: str) -> dict:
     return c3
 
 
+def dense_f16_library_tflops(M: int, N: int, K: int, reps: int = 20) -> float | None:
+    """Calibration: the same contraction as a plain dense fp16 GEMM in the
+    vendor library (torch.matmul, which runs hipBLASLt on ROCm), fp16 operands
+    already dequantized, timed with CUDA events.  The ceiling a fused kernel
+    that also dequantizes is compared against; not part of the product path
+    (None where torch has no GPU)."""
+    try:
+        import torch
+        if not torch.cuda.is_available():
+            return None
+        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+        b = torch.randn(N, K, device="cuda", dtype=torch.float16)
+        for _ in range(3):
+            c = a @ b.t()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            c = a @ b.t()
+        e1.record()
+        torch.cuda.synchronize()
+        del a, b, c
+        return 2.0 * M * N * K / (e0.elapsed_time(e1) / reps * 1e-3) / 1e12
+    except Exception:
+        return None
+
+
 def run_c2(prov) -> dict:
     """Llama-2-7B Q4_0 prefill GEMMs, f16 activations, 4 rotated
-    weight copies per shape."""
+    weight copies per shape; beside each, the vendor library's dense fp16
+    GEMM of the same shape (dense_f16_library_tflops)."""
     pre = {}
     for (name, N, K) in [("qkvo_4096x4096", 4096, 4096), ("gate_up_11008x4096", 11008, 4096),
                          ("down_4096x11008", 4096, 11008)]:
@@ -524,9 +565,12 @@ def run_c2(prov) -> dict:
             sp = rotated_linear(prov, "q4_0", M, N, K, True, 4)
             rp = time_step(prov, sp, 5, 2, "eager")
             tf = sp.flops / (rp["ms_per_step"] * 1e-3) / 1e12
+            lib_tf = dense_f16_library_tflops(M, N, K)
             pre[f"{name}_m{M}"] = {"TFLOP_s": tf, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS,
-                                   "us_per_launch": rp["us_per_launch"], "kernels": sorted(sp.kernels)}
-            log(f"[bench] prefill {name} M={M}: {tf:.1f} TFLOP/s")
+                                   "us_per_launch": rp["us_per_launch"], "kernels": sorted(sp.kernels),
+                                   "dense_f16_library_TFLOP_s": lib_tf}
+            log(f"[bench] prefill {name} M={M}: {tf:.1f} TFLOP/s (library dense fp16 GEMM, no dequant: "
+                f"{lib_tf if lib_tf is None else round(lib_tf, 1)} TFLOP/s)")
             sp.release()
     return pre
 

@@ -512,8 +512,9 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   // Register sets in rotation: with three or more steps the loads run two
   // steps ahead (three sets; measured 8.1 against 8.8 us at 11008 x 4096),
   // else one step ahead (two sets; the extra set's loads would be wasted).
-  // One row per lane group only (two rows with three sets measured slower).
-  constexpr bool k3Sets = R2 == 1;
+  // One row per lane group only (two rows with three sets measured slower),
+  // and not for four activation rows, whose third set costs occupancy.
+  constexpr bool k3Sets = R2 == 1 && MM <= 2;
   if (k3Sets && T >= 3) {
     next_load(wb);
     for (int t = 0; t < T; t += 3) {

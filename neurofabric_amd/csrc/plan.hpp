@@ -77,19 +77,27 @@ struct LayerParams {
 // above (f16: fp16 MFMA; f32: bf16-piece MFMA, K % 64 == 0, else the GEMV).
 // Defaults from the measured crossover sweep on MI355X (bench.py's configs[4]
 // section: 28672x8192 and 8192x28672 Q4_0, f16 activations, graph replay
-// over 4 weight copies): the GEMV is fastest up to M = 4 wherever its
-// activation stage fits (M = 4 at 28672x8192: 51.2 vs 53.0 us for the
-// small-batch kernel), the small-batch kernel up to M = 16 (64.5 vs 88.8 us
+// over 4 weight copies): the GEMV is fastest up to M = 2 (31.2 / 37.9 us
+// against 49.2 / 50.6 us for the small-batch kernel at 28672x8192), the
+// small-batch kernel up to M = 16 (64.5 vs 88.8 us
 // and 94.3 vs 97.7 us), the tiled GEMM from M = 32 (88.6 vs 89.3 us and
 // 95.8 vs 144.0 us).  f32 activations (Q8_0 14336x4096 / 4096x14336 and
 // Q4_0 4096x4096, graph replay over 4 weight copies): the small-batch kernel
 // up to M = 48 (61.3 vs 80.7 us at 14336x4096), the bf16-piece tiled GEMM
 // from M = 64 (79.7 / 116.6 / 37.5 us against 74.8 / 176.5 / 58.0 us).
+// At M = 3..4 the winner depends on the weight size (same sweep method, f32
+// and f16): the GEMV wins by far on matrices up to tens of MB, where the
+// small-batch kernel's fixed per-launch cost dominates (4096x4096 Q4_0 f32
+// M = 4: 12.0 vs 18.7 us; 5632x2048: 8.8 vs 12.2 us), and loses on the
+// large ones (28672x8192 Q4_0: 62.7 vs 64.0 us f32, 63.9 vs 54.0 us f16;
+// 14336x4096 Q8_0: 25.1 vs 23.4 us f32).  Hence the GEMV takes M = 3..4 only
+// while the weights are at most gemv_m4_max_weight_bytes.
 struct Tuning {
   uint32_t gemv_max_m_f32 = 4;
   uint32_t gemv_max_m_f16 = 4;
   uint32_t skinny_max_m_f16 = 16;
   uint32_t skinny_max_m_f32 = 48;
+  uint64_t gemv_m4_max_weight_bytes = 48ull << 20;
   // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernels
   // (default: two waves per SIMD where it applies and measured faster),
   // 0..6 = one of the LDS-staged tile shapes, 7 = the register-dequantizing
