@@ -527,31 +527,47 @@ def run_c3(prov, mode: str) -> dict:
     return c3
 
 
-def dense_f16_library_tflops(M: int, N: int, K: int, reps: int = 20) -> float | None:
-    """Calibration: the same contraction as a plain dense fp16 GEMM in the
-    vendor library (torch.matmul, which runs hipBLASLt on ROCm), fp16 operands
-    already dequantized, timed with CUDA events.  The ceiling a fused kernel
-    that also dequantizes is compared against; not part of the product path
-    (None where torch has no GPU)."""
+_LIB_GEMM_CODE = r"""
+import json, sys, torch
+shapes, reps = json.loads(sys.argv[1]), int(sys.argv[2])
+out = []
+for M, N, K in shapes:
+    if not torch.cuda.is_available():
+        out.append(None)
+        continue
+    a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+    b = torch.randn(N, K, device="cuda", dtype=torch.float16)
+    for _ in range(3):
+        c = a @ b.t()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        c = a @ b.t()
+    e1.record()
+    torch.cuda.synchronize()
+    out.append(2.0 * M * N * K / (e0.elapsed_time(e1) / reps * 1e-3) / 1e12)
+    del a, b, c
+print(json.dumps(out))
+"""
+
+
+def dense_f16_library_tflops(shapes, reps: int = 20) -> dict:
+    """Calibration: each (M, N, K) contraction as a plain dense fp16 GEMM in the
+    vendor library (torch.matmul, which runs hipBLASLt on ROCm), operands
+    already fp16, timed with CUDA events, in one child process (torch ships
+    its own HIP runtime, which must not share a process with this
+    library's).  The ceiling a fused kernel that also dequantizes is compared
+    against; not part of the product path.  {shape: TFLOP/s or None}."""
+    import subprocess
+    shapes = [tuple(x) for x in shapes]
     try:
-        import torch
-        if not torch.cuda.is_available():
-            return None
-        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
-        b = torch.randn(N, K, device="cuda", dtype=torch.float16)
-        for _ in range(3):
-            c = a @ b.t()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            c = a @ b.t()
-        e1.record()
-        torch.cuda.synchronize()
-        del a, b, c
-        return 2.0 * M * N * K / (e0.elapsed_time(e1) / reps * 1e-3) / 1e12
+        r = subprocess.run([sys.executable, "-c", _LIB_GEMM_CODE, json.dumps(shapes), str(reps)],
+                           capture_output=True, text=True, timeout=600)
+        vals = json.loads(r.stdout.strip().splitlines()[-1]) if r.returncode == 0 else [None] * len(shapes)
     except Exception:
-        return None
+        vals = [None] * len(shapes)
+    return dict(zip(shapes, vals))
 
 
 def run_c2(prov) -> dict:
@@ -559,13 +575,14 @@ def run_c2(prov) -> dict:
     weight copies per shape; beside each, the vendor library's dense fp16
     GEMM of the same shape (dense_f16_library_tflops)."""
     pre = {}
-    for (name, N, K) in [("qkvo_4096x4096", 4096, 4096), ("gate_up_11008x4096", 11008, 4096),
-                         ("down_4096x11008", 4096, 11008)]:
+    shapes = [("qkvo_4096x4096", 4096, 4096), ("gate_up_11008x4096", 11008, 4096), ("down_4096x11008", 4096, 11008)]
+    lib = dense_f16_library_tflops([(M, N, K) for (_, N, K) in shapes for M in (512, 2048)])
+    for (name, N, K) in shapes:
         for M in (512, 2048):
             sp = rotated_linear(prov, "q4_0", M, N, K, True, 4)
             rp = time_step(prov, sp, 5, 2, "eager")
             tf = sp.flops / (rp["ms_per_step"] * 1e-3) / 1e12
-            lib_tf = dense_f16_library_tflops(M, N, K)
+            lib_tf = lib.get((M, N, K))
             pre[f"{name}_m{M}"] = {"TFLOP_s": tf, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS,
                                    "us_per_launch": rp["us_per_launch"], "kernels": sorted(sp.kernels),
                                    "dense_f16_library_TFLOP_s": lib_tf}
