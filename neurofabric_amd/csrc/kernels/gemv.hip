@@ -426,19 +426,14 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   // all eight are in flight together.
   {
     const int total = M * P * CP;
-    auto stage = [&](int c0) {
-      ChunkT v[8];
+    auto load = [&](int c0, ChunkT (&v)[8]) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int c = c0 + u * 256 + tid;
         v[u] = *reinterpret_cast<const ChunkT*>(A + (size_t)(c < total ? c : total - 1) * EPC);
       }
-      // The first weights are requested right after the first activation
-      // loads, so the two memory round trips overlap; after them, not
-      // before: loads complete in issue order, and the activations (L2
-      // resident) can then be staged while the weights (HBM) are in flight
-      // (measured on MI355X: 3.3 against 3.8 us at 2048 x 2048).
-      if (c0 == 0 && T > 0) next_load(wa);
+    };
+    auto put = [&](int c0, const ChunkT (&v)[8]) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int c = c0 + u * 256 + tid;
@@ -455,10 +450,24 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
         }
       }
     };
-    // The first 2048 chunks (all of them up to M * K = 8192 f32 / 16384
-    // f16 elements) outside the loop, so their loads wait on nothing.
-    stage(0);
-    for (int c0 = 256 * 8; c0 < total; c0 += 256 * 8) stage(c0);
+    // The first two rounds of 2048 chunks (all of them up to M * K = 16384
+    // f32 / 32768 f16 elements) are requested before the first weights, so
+    // the two memory round trips overlap; the activations go first because
+    // loads complete in issue order: the (L2-resident) activations are then
+    // staged while the weights stream from HBM (measured on MI355X: 3.3
+    // against 3.8 us at 2048 x 2048 with the weights first).  Later rounds,
+    // if any, follow the weights.
+    ChunkT v0[8], v1[8];
+    load(0, v0);
+    const bool two = total > 256 * 8;
+    if (two) load(256 * 8, v1);
+    if (T > 0) next_load(wa);
+    put(0, v0);
+    if (two) put(256 * 8, v1);
+    for (int c0 = 2 * 256 * 8; c0 < total; c0 += 256 * 8) {
+      load(c0, v0);
+      put(c0, v0);
+    }
   }
   __syncthreads();
 
@@ -642,13 +651,18 @@ struct PairGeom {
 // Lanes per row: the largest of 64/32/16 whose round-robin split of the P
 // pairs keeps >= 95% of the lanes busy, else the best split.
 inline int pick_log2L(int P) {
+  static const double min_u = [] {
+    const char* e = std::getenv("NF_HIP_GEMV_MIN_UTIL");  // tuning override
+    const double v = e ? std::atof(e) : 0.0;
+    return v > 0.0 && v <= 1.0 ? v : 0.95;
+  }();
   int best = 6;
   double best_u = 0.0;
   for (int lg = 6; lg >= 4; --lg) {
     const int L = 1 << lg;
     const int it = (P + L - 1) / L;
     const double u = (double)P / (double)(L * it);
-    if (u >= 0.95) return lg;
+    if (u >= min_u) return lg;
     if (u > best_u + 1e-9) {
       best_u = u;
       best = lg;
