@@ -415,6 +415,7 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
     from neurofabric_amd import abi, synthetic as syn
     g32, g16 = prov.get_gemv_max_m()
     sk16 = prov.get_skinny_max_m()
+    tuning = prov.get_tuning()
     pins = {"gemv": (1 << 30, 1 << 30), "skinny": (0, 1 << 30), "tiled": (0, 0)}
     family = {"gemv": "gemv_", "skinny": "skinny_mfma_", "tiled": "gemm_mfma_"}
     out = {}
@@ -429,7 +430,7 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
                 row = {"M": M}
                 for path, (gmax, smax) in pins.items():
                     prov.set_gemv_max_m(g32, gmax)
-                    prov.set_skinny_max_m(smax)
+                    prov.set_skinny_max_m(smax, None, 1 << 30 if path == "skinny" else tuning[4])
                     st = Step(prov)
                     for w in ws:
                         st.add("dequant_q4_0_linear_f16", [a, w], [c], M, N, K)
@@ -442,8 +443,7 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
                     row[path] = {"us": us, "GB_s": st.bytes / copies / (us * 1e-6) / 1e9,
                                  "TFLOP_s": st.flops / copies / (us * 1e-6) / 1e12, "kernel": kern}
                 # the family the default switch points pick for this M
-                prov.set_gemv_max_m(g32, g16)
-                prov.set_skinny_max_m(sk16)
+                prov.set_tuning(tuning)
                 sel = Step(prov)
                 sel.add("dequant_q4_0_linear_f16", [a, ws[0]], [c], M, N, K)
                 sel_kern = sorted(sel.kernels)[0]
@@ -458,8 +458,7 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
                 w.release()
             out[f"{N}x{K}"] = {"rows": rows, "fastest_by_M": {r["M"]: r["fastest"] for r in rows}}
     finally:
-        prov.set_gemv_max_m(g32, g16)
-        prov.set_skinny_max_m(sk16)
+        prov.set_tuning(tuning)
     # The switch points these measurements imply beside the provider's
     # defaults: the largest M at which the family is the fastest on every
     # shape it serves (the GEMV does not serve the 28672-long rows beyond
@@ -472,7 +471,8 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
         return max(ms) if ms else 0
     out["switch_points"] = {"measured": {"gemv_max_m_f16": last_m("gemv"), "skinny_max_m_f16": last_m("skinny")},
                             "defaults": {"gemv_max_m_f16": g16, "skinny_max_m_f16": sk16,
-                                         "gemv_m3_m4_only_up_to_weight_MB": 48},
+                                         "gemv_m3_m4_only_up_to_weight_MB": 48,
+                                         "skinny_f16_above_m4_only_up_to_k": tuning[4]},
                             "default_not_fastest": [(k, r["M"], r["selected_by_default"], r["fastest"])
                                                     for k in shp for r in out[k]["rows"]
                                                     if r["selected_by_default"] != r["fastest"]]}

@@ -126,16 +126,23 @@ NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path);
 NF_API uint32_t nf_hip_get_skinny_max_m(void);
 NF_API void nf_hip_set_skinny_max_m_f32(uint32_t f32_path);
 NF_API uint32_t nf_hip_get_skinny_max_m_f32(void);
+/* f16 activations: above M = 4 the small-batch kernel serves only rows of
+ * K <= skinny_f16_max_k (default 16384; the tiled GEMM measured faster on
+ * longer rows); environment override NF_HIP_SKINNY_F16_MAX_K. */
+NF_API void nf_hip_set_skinny_f16_max_k(uint32_t k);
+NF_API uint32_t nf_hip_get_skinny_f16_max_k(void);
 
 /* Kernel of the fused f16 GEMM path (M above the small-batch range): -1
- * (default) = the kernels that dequantize weights in registers, measured
- * fastest on MI355X (two waves per SIMD for Q4_0 with K % 128 == 0 and
- * M >= 1024, one wave per SIMD otherwise); 0..6 = the kernel that
- * dequantizes weight tiles into LDS, tile shape 256x256, 256x128, 128x128,
- * 256x128 with 4 waves, 256x128 with 4 waves and 3 stages, 128x128 with 3
- * stages, 128x256; 7 = the register-dequantizing kernel with one wave per
- * SIMD for every shape; 8 = the two-wave kernel wherever it applies (Q4_0,
- * K % 128 == 0), else as 7.
+ * (default) = the kernels that dequantize weights in registers, picked by M
+ * from measurement on MI355X (two waves per SIMD with 32-row waves up to
+ * M = 32 and 64-row waves up to M = 64; 128-row waves for Q4_0 from
+ * M = 1024; one wave per SIMD otherwise; the two-wave kernels need
+ * K % 128 == 0); 0..6 = the kernel that dequantizes weight tiles into LDS,
+ * tile shape 256x256, 256x128, 128x128, 256x128 with 4 waves, 256x128 with
+ * 4 waves and 3 stages, 128x128 with 3 stages, 128x256; 7 = the
+ * register-dequantizing kernel with one wave per SIMD for every shape;
+ * 8 / 9 / 10 = the two-wave kernel with 128 / 64 / 32-row waves wherever it
+ * applies (K % 128 == 0; 8: Q4_0 only), else as 7.
  * Other values mean -1.  Environment override NF_HIP_GEMM_TILE (the shape
  * name or number) is read at nf_plugin_register.  No counterpart in the
  * reference (its Metal provider has one fused GEMM kernel); this is

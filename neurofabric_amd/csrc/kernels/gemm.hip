@@ -1013,6 +1013,13 @@ __device__ __forceinline__ u32x4 dequant_slice(const uint32_t (&w)[WBlk<QF>::kDw
   return o;
 }
 
+// Dynamic LDS of gemm_wq2_kernel: the four A stages (two per K-group), or,
+// if larger, one row of 32x32 tiles of group 1's accumulators for the final
+// reduction (2 x 16 floats x 64*NW threads).
+constexpr int wq2_lds_bytes(int TM, int NW) {
+  return (4 * 32 * TM * 64 * 2) > (2 * 16 * 64 * NW * 4) ? (4 * 32 * TM * 64 * 2) : (2 * 16 * 64 * NW * 4);
+}
+
 template <class QF, int TM, int NW, bool SPLIT>
 __global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __restrict__ A,
                                                               const uint8_t* __restrict__ W, half_t* __restrict__ C,
@@ -1021,7 +1028,7 @@ __global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __r
   constexpr int TN = 2, BM = 32 * TM, BN = 32 * TN * NW, NT0 = 64 * NW;
   constexpr int STAGE = BM * 64;     // halves per LDS stage
   constexpr int A_DMA = BM / 8 / NW;  // direct-to-LDS loads (8 rows each) per wave per step
-  static_assert(BM % (8 * NW) == 0 && A_DMA % 2 == 0, "A rows per wave");
+  static_assert(BM % (8 * NW) == 0 && A_DMA >= 1, "A rows per wave");
   constexpr int WD = WBlk<QF>::kDwords;
   extern __shared__ __attribute__((aligned(16))) half_t lds[];  // [group][2][BM][64]
 
@@ -1177,7 +1184,8 @@ __global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __r
   // Group 1 hands its sums to group 0 through LDS (the stages are free now),
   // RT tiles of TM at a time: value (i, j, r) of thread t at float index
   // ((i' * TN + j) * 16 + r) * NT0 + t (i' = i - round * RT), conflict-free.
-  constexpr int RT = (4 * STAGE * 2) / (TN * 16 * NT0 * 4);  // tiles of TM per round that fit the stages
+  constexpr int RT_FIT = wq2_lds_bytes(TM, NW) / (TN * 16 * NT0 * 4);  // tiles of TM per round that fit
+  constexpr int RT = RT_FIT < TM ? RT_FIT : TM;
   static_assert(RT >= 1 && TM % RT == 0, "reduction rounds");
   float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
@@ -1260,7 +1268,7 @@ __global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __r
   if (!is_last || grp != 0) return;
   // (Registers: the accumulators already use half of them, so half a tile
   // of loads at a time.)
-  splitk_gather<TM, TN, NT0, TM / 2>(acc, tile_ws, BM * BN / 4, KG, tid);
+  splitk_gather<TM, TN, NT0, (TM >= 2 ? TM / 2 : 1)>(acc, tile_ws, BM * BN / 4, KG, tid);
   store();
   if (tid == 0) __hip_atomic_store(&ws_cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1480,7 +1488,7 @@ hipError_t gemm_wq2_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_
     const long cost = ((tiles * g + kCUs - 1) / kCUs) * ((np + g - 1) / g);
     if (cost < best) best = cost, kg = g;
   }
-  const size_t lds = (size_t)4 * BM * 64 * sizeof(half_t);
+  const size_t lds = (size_t)wq2_lds_bytes(TM, NW);
   if (kg == 1) {
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&gemm_wq2_kernel<QF, TM, NW, false>), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1886,16 +1894,31 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
   const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
   if (K % 64 == 0 && aligned) {
     // Default: the register-dequantizing kernels (measured faster than the
-    // LDS-staged tiles at every prefill shape with M > 64): two waves per
-    // SIMD (gemm_wq2_kernel) for Q4_0 with K % 128 == 0 and M >= 1024, where
-    // it measured faster (816 / 747 / 859 against 785 / 735 / 804 TFLOP/s on
-    // the three Llama-2-7B projection shapes at M = 2048), else one wave per
-    // SIMD (gemm_wq_kernel; also Q8_0, whose weight window does not fit the
-    // two-wave register budget).  Tile 7 forces the one-wave kernel, tile 8
-    // the two-wave kernel wherever it applies; 0..6 select one of the
-    // LDS-staged tile shapes.
-    const bool wq2_fits = q == QFmt::Q4_0 && K % 128 == 0;
-    if ((tile == 8 && wq2_fits) || (tile < 0 && wq2_fits && M >= 1024))
+    // LDS-staged tiles at every prefill shape with M > 64), picked by M
+    // (bench sweeps on MI355X, f16 activations, graph replay over 4 weight
+    // copies):
+    //   * M <= 32: two waves per SIMD with 32-row waves (gemm_wq2_kernel,
+    //     TM = 1): 71 against 96-102 us at 28672x8192 / 8192x28672 M = 32;
+    //   * M <= 64: the same with 64-row waves (TM = 2): 81 / 84 against
+    //     102 / 110 us at M = 64;
+    //   * Q4_0 with M >= 1024: 128-row waves (TM = 4): 816 / 747 / 859
+    //     against 785 / 735 / 804 TFLOP/s on the three Llama-2-7B
+    //     projection shapes at M = 2048;
+    //   * otherwise one wave per SIMD (gemm_wq_kernel; also Q8_0 at larger
+    //     M, where the two-wave kernel measured 5-12 % slower);
+    // all of them need K % 128 == 0 but gemm_wq_kernel.  Tile 7 forces the
+    // one-wave kernel, tiles 8 / 9 / 10 the two-wave kernel with 128 / 64 /
+    // 32-row waves (8: Q4_0 only); 0..6 select one of the LDS-staged tile
+    // shapes.
+    const bool k128 = K % 128 == 0;
+    const bool q4 = q == QFmt::Q4_0;
+    if ((tile == 10 || (tile < 0 && M <= 32)) && k128)
+      return q4 ? nfk::gemm_wq2_launch<nfk::Q4_0, 1, 4>(a, w, c, M, N, K, ws, s)
+                : nfk::gemm_wq2_launch<nfk::Q8_0, 1, 4>(a, w, c, M, N, K, ws, s);
+    if ((tile == 9 || (tile < 0 && M <= 64)) && k128)
+      return q4 ? nfk::gemm_wq2_launch<nfk::Q4_0, 2, 4>(a, w, c, M, N, K, ws, s)
+                : nfk::gemm_wq2_launch<nfk::Q8_0, 2, 4>(a, w, c, M, N, K, ws, s);
+    if ((tile == 8 || (tile < 0 && M >= 1024)) && k128 && q4)
       return nfk::gemm_wq2_launch<nfk::Q4_0, 4, 4>(a, w, c, M, N, K, ws, s);
     if (tile < 0 || tile > 6)
       return (q == QFmt::Q4_0) ? nfk::gemm_wq_launch<nfk::Q4_0, 4, 2, 4, 4>(a, w, c, M, N, K, ws, s)

@@ -186,7 +186,8 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
       if (p.M <= gemv_max && gemv_rows_ok && (gemv_fits || K % 256 != 0)) {
         p.path = Path::Gemv;
         p.kernel = "gemv_" + tag;
-      } else if (K % 256 == 0 && p.M <= (f16 ? tuning.skinny_max_m_f16 : tuning.skinny_max_m_f32)) {
+      } else if (K % 256 == 0 && p.M <= (f16 ? tuning.skinny_max_m_f16 : tuning.skinny_max_m_f32) &&
+                 (!f16 || p.M <= 4 || K <= tuning.skinny_f16_max_k)) {
         p.path = Path::Skinny;
         p.kernel = "skinny_mfma_" + tag;
       } else if (f16 || K % 64 == 0) {
@@ -227,10 +228,11 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
 int gemm_tile_from_name(const char* name) {
   if (!name) return -1;
   static const char* const kNames[] = {"256x256", "256x128", "128x128", "256x128w4",
-                                       "256x128w4s3", "128x128s3", "128x256", "wq1", "wq2"};
-  for (int i = 0; i < 9; ++i)
+                                       "256x128w4s3", "128x128s3", "128x256", "wq1", "wq2", "wq2m64", "wq2m32"};
+  for (int i = 0; i < 11; ++i)
     if (std::strcmp(name, kNames[i]) == 0) return i;
-  if (name[0] >= '0' && name[0] <= '8' && name[1] == '\0') return name[0] - '0';
+  if (name[0] >= '0' && name[0] <= '9' && name[1] == '\0') return name[0] - '0';
+  if (std::strcmp(name, "10") == 0) return 10;
   return -1;
 }
 

@@ -91,24 +91,31 @@ struct LayerParams {
 // M = 4: 12.0 vs 18.7 us; 5632x2048: 8.8 vs 12.2 us), and loses on the
 // large ones (28672x8192 Q4_0: 62.7 vs 64.0 us f32, 63.9 vs 54.0 us f16;
 // 14336x4096 Q8_0: 25.1 vs 23.4 us f32).  Hence the GEMV takes M = 3..4 only
-// while the weights are at most gemv_m4_max_weight_bytes.
+// while the weights are at most gemv_m4_max_weight_bytes.  With the
+// two-wave tiled GEMM's 32-row waves (M <= 32), the tiled kernel also wins at
+// M = 8..16 on long rows: 8192x28672 f16 M = 8 / 16: 67.4 / 68.7 against
+// 76.5 / 94.8 us for the small-batch kernel, while 28672x8192 keeps the
+// small-batch kernel (55.8 / 65.3 against 66.6 / 67.5 us); so for f16 the
+// small-batch kernel takes M = 5..16 only while K <= skinny_f16_max_k.
 struct Tuning {
   uint32_t gemv_max_m_f32 = 4;
   uint32_t gemv_max_m_f16 = 4;
   uint32_t skinny_max_m_f16 = 16;
   uint32_t skinny_max_m_f32 = 48;
   uint64_t gemv_m4_max_weight_bytes = 48ull << 20;
-  // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernels
-  // (default: two waves per SIMD where it applies and measured faster),
-  // 0..6 = one of the LDS-staged tile shapes, 7 = the register-dequantizing
-  // kernel with one wave per SIMD, 8 = the two-wave kernel wherever it
-  // applies (Q4_0, K % 128 == 0).
+  uint32_t skinny_f16_max_k = 16384;
+  // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernels,
+  // picked by M (launch_gemm_mfma); 0..6 = one of the LDS-staged tile
+  // shapes; 7 = the register-dequantizing kernel with one wave per SIMD;
+  // 8 / 9 / 10 = the two-wave kernel with 128 / 64 / 32-row waves wherever
+  // it applies (K % 128 == 0; 8: Q4_0 only).
   int32_t gemm_tile = -1;
 };
 
 // "256x256" -> 0, "256x128" -> 1, "128x128" -> 2, "256x128w4" -> 3,
 // "256x128w4s3" -> 4, "128x128s3" -> 5, "128x256" -> 6, "wq1" -> 7,
-// "wq2" -> 8, or the number 0..8; anything else (including null) -> -1.
+// "wq2" -> 8, "wq2m64" -> 9, "wq2m32" -> 10, or the number 0..10; anything
+// else (including null) -> -1.
 int gemm_tile_from_name(const char* name);
 
 struct Plan {

@@ -898,6 +898,7 @@ NF_API nf_status nf_plugin_register(nf_provider_vtable* vt, nf_provider* out) {
   g_prov.tuning.gemv_max_m_f16 = env_u32("NF_HIP_GEMV_MAX_M_F16", g_prov.tuning.gemv_max_m_f16);
   g_prov.tuning.skinny_max_m_f16 = env_u32("NF_HIP_SKINNY_MAX_M_F16", g_prov.tuning.skinny_max_m_f16);
   g_prov.tuning.skinny_max_m_f32 = env_u32("NF_HIP_SKINNY_MAX_M_F32", g_prov.tuning.skinny_max_m_f32);
+  g_prov.tuning.skinny_f16_max_k = env_u32("NF_HIP_SKINNY_F16_MAX_K", g_prov.tuning.skinny_f16_max_k);
   g_prov.tuning.gemm_tile = gemm_tile_from_name(std::getenv("NF_HIP_GEMM_TILE"));
   *out = reinterpret_cast<nf_provider>(&g_prov);
   return NF_OK;
@@ -1015,9 +1016,16 @@ NF_API void nf_hip_set_skinny_max_m_f32(uint32_t f32_path) {
 
 NF_API uint32_t nf_hip_get_skinny_max_m_f32(void) { return g_prov.tuning.skinny_max_m_f32; }
 
+NF_API void nf_hip_set_skinny_f16_max_k(uint32_t k) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  g_prov.tuning.skinny_f16_max_k = k;
+}
+
+NF_API uint32_t nf_hip_get_skinny_f16_max_k(void) { return g_prov.tuning.skinny_f16_max_k; }
+
 NF_API void nf_hip_set_gemm_tile(int32_t tile) {
   std::lock_guard<std::mutex> lk(g_prov.mu);
-  g_prov.tuning.gemm_tile = (tile >= 0 && tile <= 8) ? tile : -1;
+  g_prov.tuning.gemm_tile = (tile >= 0 && tile <= 10) ? tile : -1;
 }
 
 NF_API int32_t nf_hip_get_gemm_tile(void) { return g_prov.tuning.gemm_tile; }

@@ -75,6 +75,10 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     lib.nf_hip_get_skinny_max_m.restype = C.c_uint32
     lib.nf_hip_diag_stream_read.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p]
     lib.nf_hip_diag_stream_read.restype = C.c_int
+    lib.nf_hip_set_skinny_f16_max_k.argtypes = [C.c_uint32]
+    lib.nf_hip_set_skinny_f16_max_k.restype = None
+    lib.nf_hip_get_skinny_f16_max_k.argtypes = []
+    lib.nf_hip_get_skinny_f16_max_k.restype = C.c_uint32
     lib.nf_hip_set_skinny_max_m_f32.argtypes = [C.c_uint32]
     lib.nf_hip_set_skinny_max_m_f32.restype = None
     lib.nf_hip_get_skinny_max_m_f32.argtypes = []
@@ -335,11 +339,14 @@ class Provider:
     def set_gemv_max_m(self, f32: int, f16: int) -> None:
         self.lib.nf_hip_set_gemv_max_m(f32, f16)
 
-    def set_skinny_max_m(self, f16: int, f32: int | None = None) -> None:
-        """Largest M on the small-batch kernel for f16 (and, if given, f32) activations."""
+    def set_skinny_max_m(self, f16: int, f32: int | None = None, f16_max_k: int | None = None) -> None:
+        """Largest M on the small-batch kernel for f16 (and, if given, f32)
+        activations; f16_max_k: longest rows it takes at M > 4 (f16)."""
         self.lib.nf_hip_set_skinny_max_m(f16)
         if f32 is not None:
             self.lib.nf_hip_set_skinny_max_m_f32(f32)
+        if f16_max_k is not None:
+            self.lib.nf_hip_set_skinny_f16_max_k(f16_max_k)
 
     def release_staging(self) -> None:
         self.lib.nf_hip_release_staging(self.handle)
@@ -349,9 +356,10 @@ class Provider:
         return int(self.lib.nf_hip_launch_count(self.handle))
 
     def set_gemm_tile(self, tile: int) -> None:
-        """-1: register-dequantizing GEMM kernels (default); 0..6: LDS-staged tile
-        shapes; 7: the register-dequantizing kernel with one wave per SIMD;
-        8: the two-wave-per-SIMD kernel wherever it applies (Q4_0, K % 128 == 0)."""
+        """-1: register-dequantizing GEMM kernels picked by M (default); 0..6:
+        LDS-staged tile shapes; 7: the one-wave-per-SIMD register kernel;
+        8 / 9 / 10: the two-wave kernel with 128 / 64 / 32-row waves wherever
+        it applies (K % 128 == 0; 8: Q4_0 only)."""
         self.lib.nf_hip_set_gemm_tile(tile)
 
     def get_gemm_tile(self) -> int:
@@ -371,11 +379,12 @@ class Provider:
 
     def get_tuning(self) -> tuple:
         """Every switch point and the GEMM kernel choice, for set_tuning."""
-        return (self.get_gemv_max_m(), self.get_skinny_max_m(), self.get_skinny_max_m_f32(), self.get_gemm_tile())
+        return (self.get_gemv_max_m(), self.get_skinny_max_m(), self.get_skinny_max_m_f32(), self.get_gemm_tile(),
+                int(self.lib.nf_hip_get_skinny_f16_max_k()))
 
     def set_tuning(self, t: tuple) -> None:
         self.set_gemv_max_m(*t[0])
-        self.set_skinny_max_m(t[1], t[2])
+        self.set_skinny_max_m(t[1], t[2], t[4])
         self.set_gemm_tile(t[3])
 
     def get_gemv_max_m(self):

@@ -99,7 +99,7 @@ def _force(provider, path):
         provider.set_gemv_max_m(1 << 30, 1 << 30)
     elif path == "skinny":
         provider.set_gemv_max_m(0, 0)
-        provider.set_skinny_max_m(1 << 30, 1 << 30)
+        provider.set_skinny_max_m(1 << 30, 1 << 30, 1 << 30)
     else:
         provider.set_gemv_max_m(0, 0)
         provider.set_skinny_max_m(0, 0)

@@ -296,6 +296,9 @@ def test_default_switch_points(lib):
     assert _fused(lib, 4, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"  # 4 x 28672 x 2 B > 120 KB
     assert _fused(lib, 5, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
     assert _fused(lib, 16, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
+    # f16, long rows: the tiled GEMM from M = 5 (K > 16384)
+    assert _fused(lib, 8, 8192, 28672, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
+    assert _fused(lib, 4, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
     assert _fused(lib, 17, 28672, 8192, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
     assert _fused(lib, 32, 8192, 28672, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
     assert _fused(lib, 4, 4096, 4096)["kernel"] == "gemv_q4_0_f32"
