@@ -38,9 +38,9 @@
 // then weights, so chunk c computes while both of chunk c+1 are in flight.
 // At most 32 activation rows per launch keep the two activation register sets
 // and the accumulators in registers; more rows take more launches.
-#include <type_traits>
-
+#include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "../launch.hpp"
 #include "common.hpp"
@@ -461,12 +461,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 }
 
 // Waves per workgroup (ks) and workgroups per row tile (kg) for a launch of
-// `wgs` row tiles: up to 8 waves per workgroup (the kernel's launch bound of
-// 512 threads); for launches with very few row tiles (under 512 waves), also
-// kg workgroups per row tile, while every wave keeps at least one chunk; kg
-// is bounded by the workspace.
+// `wgs` row tiles, bounded by the kernel's launch bound of 512 threads, by
+// at least one chunk per wave and by the workspace.
+// f32 activations: 8 waves per workgroup up to 256 row tiles, else 4; then
+// up to 4 workgroups per row tile while the launch stays within 2048 waves.
+// Measured on MI355X at M = 16 (waves x kg sweep): a few chunks per wave
+// leave each wave one memory round trip per chunk, so spreading K over more
+// waves pays for the fix-up: Llama-3-8B Q8_0 4096x14336 72 -> 33 us,
+// 4096x4096 25 -> 15 us, TinyLlama 2048x5632 18 -> 13 us; row-rich shapes
+// (11264 rows and up) stay at kg = 1, and 28672x4096 is faster with 4 waves
+// than 8 (47 against 53 us).
+// f16 activations: up to 8 waves per workgroup while the launch has under
+// 2048 waves; for launches with very few row tiles (under 512 waves), also
+// kg workgroups per row tile.
 template <int MT, int CHP>
-void skinny_split(long wgs, uint32_t K, const nfhip::Workspace& ws, int& ks, int& kg) {
+void skinny_split(long wgs, uint32_t K, bool f32, const nfhip::Workspace& ws, int& ks, int& kg) {
   constexpr int NV = MT * 4 * 4;
   const int NC = (int)(K / (64 * CHP));
   static const int ks_max = [] {
@@ -479,6 +488,15 @@ void skinny_split(long wgs, uint32_t K, const nfhip::Workspace& ws, int& ks, int
     const int v = e ? std::atoi(e) : 0;
     return v > 0 && v <= 64 ? v : 64;
   }();
+  if (f32) {
+    ks = std::min(ks_max, wgs <= 256 ? 8 : 4);
+    while (ks > 1 && NC < ks) ks >>= 1;
+    kg = 1;
+    while (kg < 4 && kg < kg_max && wgs * ks * kg * 2 <= 2048 && NC >= 2 * ks * kg && wgs <= (long)ws.cnt_len &&
+           (size_t)wgs * 2 * kg * NV * 64 <= ws.part_floats)
+      kg *= 2;
+    return;
+  }
   ks = 1;
   while (ks < ks_max && wgs * ks < 2048 && NC >= 2 * ks) ks *= 2;
   kg = 1;
@@ -508,7 +526,7 @@ hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint
                          const nfhip::Workspace& ws, hipStream_t s) {
   const long wgs = ((long)N + 63) / 64;
   int ks, kg;
-  skinny_split<MT, CHP>(wgs, K, ws, ks, kg);
+  skinny_split<MT, CHP>(wgs, K, sizeof(XT) == 4, ws, ks, kg);
   SkinnyGroup grp{};
   grp.W[0] = static_cast<const uint8_t*>(W);
   grp.C[0] = C;
@@ -530,7 +548,7 @@ hipError_t skinny_group_same_split(const void* A, const nfhip::GemvJob* jobs, ui
   for (uint32_t j = 0; j < n; ++j) {
     const long wgs = ((long)jobs[j].N + 63) / 64;
     int ks, kg;
-    skinny_split<MT, CHP>(wgs, K, ws, ks, kg);
+    skinny_split<MT, CHP>(wgs, K, sizeof(XT) == 4, ws, ks, kg);
     if (j == 0) {
       ks0 = ks;
       kg0 = kg;
@@ -555,11 +573,12 @@ template <class QF, typename XT>
 hipError_t skinny_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
                            const nfhip::Workspace& ws, hipStream_t s) {
   constexpr bool kQ4 = SkW<QF>::kLoads == 5;
-  // Few row tiles: one-pair chunks, so the K split reaches more CUs.
+  // Few row tiles: one-pair chunks, so the K split reaches more CUs (f16;
+  // f32 takes two-pair chunks at every N: 4-12 % faster at M = 16, the K
+  // split reaching the CUs through workgroups per row tile instead).
   const bool small = N < 64u * 128u;
   if constexpr (sizeof(XT) == 4) {
-    if (M <= 16) return small ? skinny_launch<QF, XT, 1, 1>(A, W, C, M, N, K, ws, s)
-                              : skinny_launch<QF, XT, 1, 2>(A, W, C, M, N, K, ws, s);
+    if (M <= 16) return skinny_launch<QF, XT, 1, 2>(A, W, C, M, N, K, ws, s);
     return skinny_launch<QF, XT, 2, 1>(A, W, C, M, N, K, ws, s);
   } else {
     if (M <= 16) return small ? skinny_launch<QF, XT, 1, 1>(A, W, C, M, N, K, ws, s)
@@ -574,7 +593,7 @@ hipError_t skinny_dispatch(const void* A, const void* W, void* C, uint32_t M, ui
 template <class QF, typename XT>
 int skinny_variant(uint32_t M, uint32_t N) {
   const bool small = N < 64u * 128u;
-  if constexpr (sizeof(XT) == 4) return M <= 16 ? (small ? 0 : 1) : 2;
+  if constexpr (sizeof(XT) == 4) return M <= 16 ? 1 : 2;
   return M <= 16 ? (small ? 0 : 3) : (small ? 2 : 4);
 }
 
@@ -587,7 +606,6 @@ hipError_t skinny_group_dispatch(const void* A, const nfhip::GemvJob* jobs, uint
   for (uint32_t j = 1; j < n; ++j)
     if (skinny_variant<QF, XT>(M, jobs[j].N) != v) return hipErrorNotSupported;
   if constexpr (sizeof(XT) == 4) {
-    if (v == 0) return skinny_group_same_split<QF, XT, 1, 1>(A, jobs, n, M, K, ws, s);
     if (v == 1) return skinny_group_same_split<QF, XT, 1, 2>(A, jobs, n, M, K, ws, s);
     return skinny_group_same_split<QF, XT, 2, 1>(A, jobs, n, M, K, ws, s);
   } else {
