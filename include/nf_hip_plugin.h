@@ -127,8 +127,9 @@ NF_API uint32_t nf_hip_get_skinny_max_m(void);
 NF_API void nf_hip_set_skinny_max_m_f32(uint32_t f32_path);
 NF_API uint32_t nf_hip_get_skinny_max_m_f32(void);
 /* f16 activations: above M = 4 the small-batch kernel serves only rows of
- * K <= skinny_f16_max_k (default 16384; the tiled GEMM measured faster on
- * longer rows); environment override NF_HIP_SKINNY_F16_MAX_K. */
+ * K <= skinny_f16_max_k (default 2^30, no cap: with its K split over
+ * workgroups the small-batch kernel measured faster than the tiled GEMM at
+ * K = 28672 too); environment override NF_HIP_SKINNY_F16_MAX_K. */
 NF_API void nf_hip_set_skinny_f16_max_k(uint32_t k);
 NF_API uint32_t nf_hip_get_skinny_f16_max_k(void);
 

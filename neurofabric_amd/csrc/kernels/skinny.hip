@@ -462,20 +462,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 
 // Waves per workgroup (ks) and workgroups per row tile (kg) for a launch of
 // `wgs` row tiles, bounded by the kernel's launch bound of 512 threads, by
-// at least one chunk per wave and by the workspace.
-// f32 activations: 8 waves per workgroup up to 256 row tiles, else 4; then
-// up to 4 workgroups per row tile while the launch stays within 2048 waves.
-// Measured on MI355X at M = 16 (waves x kg sweep): a few chunks per wave
-// leave each wave one memory round trip per chunk, so spreading K over more
-// waves pays for the fix-up: Llama-3-8B Q8_0 4096x14336 72 -> 33 us,
-// 4096x4096 25 -> 15 us, TinyLlama 2048x5632 18 -> 13 us; row-rich shapes
-// (11264 rows and up) stay at kg = 1, and 28672x4096 is faster with 4 waves
-// than 8 (47 against 53 us).
-// f16 activations: up to 8 waves per workgroup while the launch has under
-// 2048 waves; for launches with very few row tiles (under 512 waves), also
-// kg workgroups per row tile.
+// at least one chunk per wave and by the workspace: 8 waves per workgroup up
+// to 256 row tiles, else 4; then up to 4 workgroups per row tile while the
+// launch stays within 2048 waves.  Measured on MI355X at M = 8 and 16 (waves
+// x kg sweep): with a few chunks per wave each wave pays about one memory
+// round trip per chunk, so spreading K over more waves pays for the fix-up:
+// Llama-3-8B Q8_0 4096x14336 f32 72 -> 33 us, 4096x4096 25 -> 15 us;
+// Llama-7B Q4_0 4096x11008 f16 45 -> 22 us; 8192x28672 f16 92 -> 60 us;
+// TinyLlama 2048x5632 f32 18 -> 13 us.  Row-rich shapes (11264 rows and up)
+// stay at kg = 1, with 4 waves once past 256 row tiles (28672x4096 f32: 47
+// against 53 us with 8).
 template <int MT, int CHP>
-void skinny_split(long wgs, uint32_t K, bool f32, const nfhip::Workspace& ws, int& ks, int& kg) {
+void skinny_split(long wgs, uint32_t K, const nfhip::Workspace& ws, int& ks, int& kg) {
   constexpr int NV = MT * 4 * 4;
   const int NC = (int)(K / (64 * CHP));
   static const int ks_max = [] {
@@ -486,21 +484,12 @@ void skinny_split(long wgs, uint32_t K, bool f32, const nfhip::Workspace& ws, in
   static const int kg_max = [] {
     const char* e = std::getenv("NF_HIP_SKINNY_KG_MAX");  // tuning override
     const int v = e ? std::atoi(e) : 0;
-    return v > 0 && v <= 64 ? v : 64;
+    return v > 0 && v <= 64 ? v : 4;
   }();
-  if (f32) {
-    ks = std::min(ks_max, wgs <= 256 ? 8 : 4);
-    while (ks > 1 && NC < ks) ks >>= 1;
-    kg = 1;
-    while (kg < 4 && kg < kg_max && wgs * ks * kg * 2 <= 2048 && NC >= 2 * ks * kg && wgs <= (long)ws.cnt_len &&
-           (size_t)wgs * 2 * kg * NV * 64 <= ws.part_floats)
-      kg *= 2;
-    return;
-  }
-  ks = 1;
-  while (ks < ks_max && wgs * ks < 2048 && NC >= 2 * ks) ks *= 2;
+  ks = std::min(ks_max, wgs <= 256 ? 8 : 4);
+  while (ks > 1 && NC < ks) ks >>= 1;
   kg = 1;
-  while (wgs * ks * kg < 512 && NC >= 2 * ks * kg && kg < kg_max && wgs <= (long)ws.cnt_len &&
+  while (kg < kg_max && wgs * ks * kg * 2 <= 2048 && NC >= 2 * ks * kg && wgs <= (long)ws.cnt_len &&
          (size_t)wgs * 2 * kg * NV * 64 <= ws.part_floats)
     kg *= 2;
 }
@@ -526,7 +515,7 @@ hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint
                          const nfhip::Workspace& ws, hipStream_t s) {
   const long wgs = ((long)N + 63) / 64;
   int ks, kg;
-  skinny_split<MT, CHP>(wgs, K, sizeof(XT) == 4, ws, ks, kg);
+  skinny_split<MT, CHP>(wgs, K, ws, ks, kg);
   SkinnyGroup grp{};
   grp.W[0] = static_cast<const uint8_t*>(W);
   grp.C[0] = C;
@@ -548,7 +537,7 @@ hipError_t skinny_group_same_split(const void* A, const nfhip::GemvJob* jobs, ui
   for (uint32_t j = 0; j < n; ++j) {
     const long wgs = ((long)jobs[j].N + 63) / 64;
     int ks, kg;
-    skinny_split<MT, CHP>(wgs, K, sizeof(XT) == 4, ws, ks, kg);
+    skinny_split<MT, CHP>(wgs, K, ws, ks, kg);
     if (j == 0) {
       ks0 = ks;
       kg0 = kg;
@@ -573,16 +562,15 @@ template <class QF, typename XT>
 hipError_t skinny_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
                            const nfhip::Workspace& ws, hipStream_t s) {
   constexpr bool kQ4 = SkW<QF>::kLoads == 5;
-  // Few row tiles: one-pair chunks, so the K split reaches more CUs (f16;
-  // f32 takes two-pair chunks at every N: 4-12 % faster at M = 16, the K
-  // split reaching the CUs through workgroups per row tile instead).
+  // Up to 16 rows: two-pair chunks at every N (4-12 % faster than one-pair
+  // chunks at M = 16, and as fast as four-pair ones); 17..32 rows: one-pair
+  // chunks for f32 and for f16 with few row tiles, so two activation tiles'
+  // registers fit.
   const bool small = N < 64u * 128u;
+  if (M <= 16) return skinny_launch<QF, XT, 1, 2>(A, W, C, M, N, K, ws, s);
   if constexpr (sizeof(XT) == 4) {
-    if (M <= 16) return skinny_launch<QF, XT, 1, 2>(A, W, C, M, N, K, ws, s);
     return skinny_launch<QF, XT, 2, 1>(A, W, C, M, N, K, ws, s);
   } else {
-    if (M <= 16) return small ? skinny_launch<QF, XT, 1, 1>(A, W, C, M, N, K, ws, s)
-                              : skinny_launch<QF, XT, 1, kQ4 ? 4 : 2>(A, W, C, M, N, K, ws, s);
     if (small) return skinny_launch<QF, XT, 2, 1>(A, W, C, M, N, K, ws, s);
     return skinny_launch<QF, XT, 2, kQ4 ? 2 : 1>(A, W, C, M, N, K, ws, s);
   }
@@ -593,8 +581,9 @@ hipError_t skinny_dispatch(const void* A, const void* W, void* C, uint32_t M, ui
 template <class QF, typename XT>
 int skinny_variant(uint32_t M, uint32_t N) {
   const bool small = N < 64u * 128u;
-  if constexpr (sizeof(XT) == 4) return M <= 16 ? 1 : 2;
-  return M <= 16 ? (small ? 0 : 3) : (small ? 2 : 4);
+  if (M <= 16) return 1;
+  if constexpr (sizeof(XT) == 4) return 2;
+  return small ? 2 : 4;
 }
 
 template <class QF, typename XT>
@@ -605,15 +594,9 @@ hipError_t skinny_group_dispatch(const void* A, const nfhip::GemvJob* jobs, uint
   const int v = skinny_variant<QF, XT>(M, jobs[0].N);
   for (uint32_t j = 1; j < n; ++j)
     if (skinny_variant<QF, XT>(M, jobs[j].N) != v) return hipErrorNotSupported;
-  if constexpr (sizeof(XT) == 4) {
-    if (v == 1) return skinny_group_same_split<QF, XT, 1, 2>(A, jobs, n, M, K, ws, s);
-    return skinny_group_same_split<QF, XT, 2, 1>(A, jobs, n, M, K, ws, s);
-  } else {
-    if (v == 0) return skinny_group_same_split<QF, XT, 1, 1>(A, jobs, n, M, K, ws, s);
-    if (v == 3) return skinny_group_same_split<QF, XT, 1, kQ4 ? 4 : 2>(A, jobs, n, M, K, ws, s);
-    if (v == 2) return skinny_group_same_split<QF, XT, 2, 1>(A, jobs, n, M, K, ws, s);
-    return skinny_group_same_split<QF, XT, 2, kQ4 ? 2 : 1>(A, jobs, n, M, K, ws, s);
-  }
+  if (v == 1) return skinny_group_same_split<QF, XT, 1, 2>(A, jobs, n, M, K, ws, s);
+  if (v == 2) return skinny_group_same_split<QF, XT, 2, 1>(A, jobs, n, M, K, ws, s);
+  return skinny_group_same_split<QF, XT, 2, kQ4 ? 2 : 1>(A, jobs, n, M, K, ws, s);
 }
 
 }  // namespace nfk

@@ -75,35 +75,34 @@ struct LayerParams {
 // small-batch MFMA kernel while M <= skinny_max_m (f16 and f32 activations
 // each have their own; at most 32 f32 rows per launch), the tiled MFMA GEMM
 // above (f16: fp16 MFMA; f32: bf16-piece MFMA, K % 64 == 0, else the GEMV).
-// Defaults from the measured crossover sweep on MI355X (bench.py's configs[4]
-// section: 28672x8192 and 8192x28672 Q4_0, f16 activations, graph replay
-// over 4 weight copies): the GEMV is fastest up to M = 2 (31.2 / 37.9 us
-// against 49.2 / 50.6 us for the small-batch kernel at 28672x8192), the
-// small-batch kernel up to M = 16 (64.5 vs 88.8 us
-// and 94.3 vs 97.7 us), the tiled GEMM from M = 32 (88.6 vs 89.3 us and
-// 95.8 vs 144.0 us).  f32 activations (Q8_0 14336x4096 / 4096x14336 and
-// Q4_0 4096x4096, graph replay over 4 weight copies): the small-batch kernel
-// up to M = 48 (61.3 vs 80.7 us at 14336x4096), the bf16-piece tiled GEMM
-// from M = 64 (79.7 / 116.6 / 37.5 us against 74.8 / 176.5 / 58.0 us).
-// At M = 3..4 the winner depends on the weight size (same sweep method, f32
-// and f16): the GEMV wins by far on matrices up to tens of MB, where the
-// small-batch kernel's fixed per-launch cost dominates (4096x4096 Q4_0 f32
-// M = 4: 12.0 vs 18.7 us; 5632x2048: 8.8 vs 12.2 us), and loses on the
-// large ones (28672x8192 Q4_0: 62.7 vs 64.0 us f32, 63.9 vs 54.0 us f16;
-// 14336x4096 Q8_0: 25.1 vs 23.4 us f32).  Hence the GEMV takes M = 3..4 only
-// while the weights are at most gemv_m4_max_weight_bytes.  With the
-// two-wave tiled GEMM's 32-row waves (M <= 32), the tiled kernel also wins at
-// M = 8..16 on long rows: 8192x28672 f16 M = 8 / 16: 67.4 / 68.7 against
-// 76.5 / 94.8 us for the small-batch kernel, while 28672x8192 keeps the
-// small-batch kernel (55.8 / 65.3 against 66.6 / 67.5 us); so for f16 the
-// small-batch kernel takes M = 5..16 only while K <= skinny_f16_max_k.
+// Defaults from measured sweeps on MI355X (graph replay over 4 rotated weight
+// copies).  bench.py's configs[4] section (28672x8192 and 8192x28672 Q4_0,
+// f16 activations): the GEMV is fastest up to M = 2 (31.0 / 38.8 us against
+// 46.3 / 47.1 us for the small-batch kernel at 28672x8192; 47.7 / 47.4 us, a
+// tie, at 8192x28672 M = 2), the small-batch kernel for M = 4..16 (58.6 and
+// 61.6 us at M = 16 against 67.6 and 69.2 us for the tiled GEMM), the tiled
+// GEMM from M = 32 (70.2 vs 88.8 us and 69.4 vs 88.7 us).  f32 activations
+// (configs[3] Llama-3-8B Q8_0 step): the small-batch kernel up to M = 64 (two
+// 32-row launches: 11.7 against 14.3 ms per M = 64 step; 14336x4096 69.6 vs
+// 79.5 us, 4096x14336 84.2 vs 116.3 us), the bf16-piece tiled GEMM above
+// (14336x4096 M = 128: 124.4 vs 137.8 us).
+// At M = 3..4 the winner depends on the weight size: the GEMV wins by far on
+// matrices up to tens of MB, where the small-batch kernel's fixed per-launch
+// cost dominates (f32 M = 4: 2048x2048 6.8 vs 10.4 us, 4096x4096 12.2 vs
+// 15.2 us; f16 5632x2048 8.3 vs 11.5 us), and not on the large ones
+// (28672x8192 f16 M = 3: 49.2 vs 48.5 us).  Hence the GEMV takes M = 3..4
+// only while the weights are at most gemv_m4_max_weight_bytes.
+// skinny_f16_max_k caps K for f16 batches above M = 4 on the small-batch
+// kernel (longer K goes to the tiled GEMM); no cap by default, since the
+// small-batch kernel's K split over workgroups (skinny_split) makes it the
+// faster one at K = 28672 too (M = 8: 52.8 against 68.1 us).
 struct Tuning {
   uint32_t gemv_max_m_f32 = 4;
   uint32_t gemv_max_m_f16 = 4;
   uint32_t skinny_max_m_f16 = 16;
-  uint32_t skinny_max_m_f32 = 48;
+  uint32_t skinny_max_m_f32 = 64;
   uint64_t gemv_m4_max_weight_bytes = 48ull << 20;
-  uint32_t skinny_f16_max_k = 16384;
+  uint32_t skinny_f16_max_k = 1u << 30;
   // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernels,
   // picked by M (launch_gemm_mfma); 0..6 = one of the LDS-staged tile
   // shapes; 7 = the register-dequantizing kernel with one wave per SIMD;

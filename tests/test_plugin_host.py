@@ -281,11 +281,10 @@ def test_crossover_setter_roundtrip():
 
 
 def test_default_switch_points(lib):
-    """Defaults from the measured configs[4] sweep: GEMV for M <= 4 while
-    its activation stage fits in 120 KB of LDS (M = 3..4 only for weights up
-    to 48 MB), the small-batch MFMA kernel
-    up to 16 rows, the tiled GEMM beyond (f16); for f32 activations the
-    small-batch kernel up to 48 rows."""
+    """Defaults from the measured sweeps: GEMV for M <= 4 while its
+    activation stage fits in 120 KB of LDS (M = 3..4 only for weights up to
+    48 MB), the small-batch MFMA kernel up to 16 rows, the tiled GEMM beyond
+    (f16); for f32 activations the small-batch kernel up to 64 rows."""
     f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
     assert _fused(lib, 2, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"   # 2 x 8192 x 2 B = 32 KB
     # M = 3..4: the GEMV only for weights up to 48 MB (132 MB here)
@@ -296,19 +295,19 @@ def test_default_switch_points(lib):
     assert _fused(lib, 4, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"  # 4 x 28672 x 2 B > 120 KB
     assert _fused(lib, 5, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
     assert _fused(lib, 16, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
-    # f16, long rows: the tiled GEMM from M = 5 (K > 16384)
-    assert _fused(lib, 8, 8192, 28672, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
-    assert _fused(lib, 4, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
+    # f16, long rows: the small-batch kernel too (no K cap by default)
+    assert _fused(lib, 8, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
+    assert _fused(lib, 16, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
     assert _fused(lib, 17, 28672, 8192, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
     assert _fused(lib, 32, 8192, 28672, **f16)["kernel"] == "gemm_mfma_q4_0_f16"
     assert _fused(lib, 4, 4096, 4096)["kernel"] == "gemv_q4_0_f32"
     assert _fused(lib, 2, 28672, 8192)["kernel"] == "gemv_q4_0_f32"           # 2 x 8192 x 4 B + sums
     assert _fused(lib, 3, 28672, 8192)["kernel"] == "skinny_mfma_q4_0_f32"    # 4 x 8192 x 4 B > 120 KB
     assert _fused(lib, 16, 4096, 4096)["kernel"] == "skinny_mfma_q4_0_f32"
-    # f32 activations: small-batch kernel up to 48 rows, then the bf16-piece
+    # f32 activations: small-batch kernel up to 64 rows, then the bf16-piece
     # tiled GEMM (K % 64 == 0), else the GEMV
-    assert _fused(lib, 48, 14336, 4096, op="dequant_q8_0_linear", bs=34)["kernel"] == "skinny_mfma_q8_0_f32"
-    assert _fused(lib, 49, 14336, 4096, op="dequant_q8_0_linear", bs=34)["kernel"] == "gemm_mfma_q8_0_f32"
+    assert _fused(lib, 64, 14336, 4096, op="dequant_q8_0_linear", bs=34)["kernel"] == "skinny_mfma_q8_0_f32"
+    assert _fused(lib, 65, 14336, 4096, op="dequant_q8_0_linear", bs=34)["kernel"] == "gemm_mfma_q8_0_f32"
     assert _fused(lib, 512, 4096, 11008)["kernel"] == "gemm_mfma_q4_0_f32"
     assert _fused(lib, 100, 64, 96)["kernel"] == "gemv_q4_0_f32"  # K % 64 != 0
 
