@@ -686,7 +686,7 @@ def run_layer(prov) -> dict:
         pc = push_constants(seq_len=1, n_heads=H, head_dim=D, M=KV, step_idx=ctx - 1, max_seq_len=ctx)
         measure(f"decode_attention_gqa_{'f16' if f16 else 'f32'}_h32kv8d128_ctx4096", "flash_attention_gqa",
                 lambda: ([buf(H * D, dt), buf(KV * D, dt), buf(KV * D, dt), buf(KV * ctx * D, dt),
-                          buf(KV * ctx * D, dt)], [buf(H * D, dt, False)]), pc)
+                          buf(KV * ctx * D, dt)], [buf(H * D, dt, False)]), pc, copies=8, steps=40)
     S = 2048
     pc = push_constants(seq_len=S, n_heads=H, head_dim=D, M=KV, step_idx=0, max_seq_len=S)
     measure("prefill_attention_f16_h32kv8d128_s2048", "flash_attention_cached",

@@ -28,6 +28,8 @@
 // the output once.  Mathematically the same softmax as each reference
 // variant (two-pass, 32-key tiles, per-key online, per-block online); the
 // results agree to fp32 rounding.
+#include <type_traits>
+
 #include "../launch.hpp"
 #include "common.hpp"
 
@@ -736,6 +738,217 @@ __global__ __launch_bounds__(64) void decode_split_kernel(Params p, uint32_t key
   }
 }
 
+// ---- f16 decode with the scores on MFMA ----------------------------------------
+//
+// One query token, f16 K/V caches, head_dim DD = 64 or 128, G <= 8 query heads
+// per KV head, 16-byte aligned rows.  A workgroup of NW waves covers one KV
+// head and NW x TK keys, one TK-key tile per wave:
+//  * scores: S[key][head] = K[key][dims] . Q[head][dims] on
+//    v_mfma_f32_16x16x32_f16 (A = 16 key rows, B = the query heads as the 16
+//    columns, exact f16 products, fp32 sums); each lane loads its A pieces
+//    (8 dims of one key row) with 16-byte loads straight into registers, the
+//    query operand is loaded once;
+//  * softmax in base 2 on the scores (scaled by scale * log2 e), per head
+//    across the lanes that hold its 64 keys;
+//  * P.V on the vector ALU: lane (kq, dc) holds 8 dims (chunk dc) of the
+//    value rows RPI*i + kq, loaded with 16-byte loads together with the keys,
+//    and takes the tile's weights from LDS;
+//  * the NW waves' (m, l, acc) are merged in LDS and written as the split's
+//    partial (m in natural-log units); decode_combine_kernel adds the
+//    splits.
+//    (Measured and not kept: the merge in the last-arriving workgroup of
+//    each KV head, 15.7 against 11.4 us at 4096 keys: the store, counter
+//    and reload round trips cost more than a second launch.)
+// Rows past the range or without storage read row 0 and drop out by select
+// (score -inf, value 0), so no load is predicated and unused memory never
+// reaches the sums.  Row `step` is read from K_new / V_new when the append is
+// fused; the workgroup whose range holds it writes it into the cache.
+template <nfhip::AttnMode MODE, int DD, int G, int TK, int NW>
+__global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t keys_per_split, uint32_t lo,
+                                                              float* __restrict__ part) {
+  constexpr int KSTEP = DD / 32;   // MFMA k-steps per 16-key block
+  constexpr int KB = TK / 16;      // 16-key blocks per tile
+  constexpr int CPR = DD / 8;      // 16-byte chunks per f16 row
+  constexpr int RPI = 64 / CPR;    // value rows per load instruction
+  constexpr int NV = TK / RPI;     // value loads per lane per tile
+  static_assert(TK % RPI == 0 && TK % 16 == 0, "tile");
+  typedef half_t T;
+  constexpr int NT = NW * 64;
+  __shared__ __attribute__((aligned(16))) float ps[NW][TK][G];  // tile weights [wave][key][head]
+  __shared__ float wm[NW][G], wl[NW][G];
+  __shared__ __attribute__((aligned(16))) float wacc[NW][G][DD];
+  const uint32_t split = blockIdx.x, kvh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t H = p.n_heads, KV = p.n_kv, D = p.dim;
+  const uint32_t h0 = (uint32_t)(((uint64_t)kvh * H + KV - 1) / KV);
+  const uint32_t h1 = (uint32_t)(((uint64_t)(kvh + 1) * H + KV - 1) / KV);
+  const int ng = (int)(h1 - h0);
+  const T* Q = static_cast<const T*>(p.q);
+  const T* K = static_cast<const T*>(p.k);
+  const T* V = static_cast<const T*>(p.v);
+
+  int64_t last = p.step;
+  if constexpr (MODE == nfhip::AttnMode::Paged) {
+    const int64_t cap = (int64_t)p.n_blocks * p.block_size - 1;
+    if (last > cap) last = cap;
+  }
+  const int64_t k_begin = (int64_t)lo + (int64_t)split * keys_per_split;
+  int64_t k_end = k_begin + keys_per_split - 1;
+  if (k_end > last) k_end = last;
+  const int64_t t0 = k_begin + TK * w;  // this wave's tile
+  if (p.fused_append && k_begin <= (int64_t)p.step && (int64_t)p.step <= k_end) {
+    const uint64_t src = (uint64_t)kvh * D, dst = ((uint64_t)kvh * p.max_seq + p.step) * D;
+    for (uint32_t d = tid; d < D; d += NT) {
+      static_cast<T*>(p.k)[dst + d] = static_cast<const T*>(p.k_new)[src + d];
+      static_cast<T*>(p.v)[dst + d] = static_cast<const T*>(p.v_new)[src + d];
+    }
+  }
+  // row pointer and validity of tile key j (0..63)
+  auto key_ptr = [&](const T* base, const void* fresh, int j, bool& ok) -> const T* {
+    const int64_t pos = t0 + j;
+    uint64_t row = ~0ull;
+    if (pos <= k_end) row = kv_row<MODE>(p, kvh, (uint32_t)pos);
+    ok = row != ~0ull;
+    const T* r = base + (ok ? row : 0);
+    if (p.fused_append && pos == (int64_t)p.step) r = static_cast<const T*>(fresh) + (uint64_t)kvh * D;
+    return r;
+  };
+
+  // ---- loads: query operand, key operands, value chunks -------------------------
+  const int n = lane & 15, kg = lane >> 4;  // MFMA column (head) / k-group of the lane
+  half8 qb[KSTEP];
+#pragma unroll
+  for (int s = 0; s < KSTEP; ++s) {
+    const T* qr = Q + q_row<MODE>(p, 0, h0 + (uint32_t)(n < ng ? n : ng - 1)) + 32 * s + 8 * kg;
+    qb[s] = *reinterpret_cast<const half8*>(qr);
+    if (n >= ng) qb[s] = half8{};
+  }
+  half8 ka[KB][KSTEP];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    bool ok;
+    const T* kr = key_ptr(K, p.k_new, 16 * j + n, ok);
+#pragma unroll
+    for (int s = 0; s < KSTEP; ++s) ka[j][s] = *reinterpret_cast<const half8*>(kr + 32 * s + 8 * kg);
+  }
+  const int kq = lane / CPR, dc = lane % CPR;
+  half8 vx[NV];
+  bool vok[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const T* vr = key_ptr(V, p.v_new, RPI * i + kq, vok[i]);
+    vx[i] = *reinterpret_cast<const half8*>(vr + 8 * dc);
+  }
+
+  // ---- scores and the tile softmax (lane: keys 16j + 4kg + i, head n) -----------
+  float4v sc[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    sc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KSTEP; ++s) sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[j][s], qb[s], sc[j], 0, 0, 0);
+  }
+  const float sl2 = p.scale * 1.44269504088896341f;
+  float sv[KB][4];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < KB; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t pos = t0 + 16 * j + 4 * kg + i;
+      bool ok = pos <= k_end;
+      if constexpr (MODE == nfhip::AttnMode::Paged)
+        if (ok) ok = kv_row<MODE>(p, kvh, (uint32_t)pos) != ~0ull;
+      sv[j][i] = ok ? sc[j][i] * sl2 : -INFINITY;
+      tmax = fmaxf(tmax, sv[j][i]);
+    }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+  float psum = 0.f;
+#pragma unroll
+  for (int j = 0; j < KB; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pw = sv[j][i] == -INFINITY ? 0.f : exp2f(sv[j][i] - tmax);
+      psum += pw;
+      if (n < G) ps[w][16 * j + 4 * kg + i][n] = pw;
+    }
+  psum += __shfl_xor(psum, 16);
+  psum += __shfl_xor(psum, 32);
+  if (kg == 0 && n < G) {
+    wm[w][n] = tmax;
+    wl[w][n] = psum;
+  }
+  __syncthreads();
+
+  // ---- P.V (lane: dims 8dc..8dc+7 of rows RPI*i + kq) ----------------------------
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int r = RPI * i + kq;
+    float pr[G];
+    if constexpr (G % 4 == 0) {
+#pragma unroll
+      for (int g4 = 0; g4 < G; g4 += 4) {
+        const float4v t = *reinterpret_cast<const float4v*>(&ps[w][r][g4]);
+        pr[g4] = t.x; pr[g4 + 1] = t.y; pr[g4 + 2] = t.z; pr[g4 + 3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < G; ++g) pr[g] = ps[w][r][g];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = vok[i] ? (float)vx[i][e] : 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g][e] = __builtin_fmaf(pr[g], x, acc[g][e]);
+    }
+  }
+  // add the RPI row groups (lanes dc, dc + CPR, ...) in a fixed order
+#pragma unroll
+  for (int o = CPR; o < 64; o <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
+  if (kq == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float4v* dst = reinterpret_cast<float4v*>(&wacc[w][g][8 * dc]);
+      dst[0] = float4v{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+      dst[1] = float4v{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+    }
+  }
+  __syncthreads();
+
+  // ---- merge the 4 waves and write the split's partial per head -----------------
+  const uint32_t stride = D + 2;
+  for (int idx = tid; idx < ng * DD; idx += NT) {
+    const int g = idx / DD, d = idx % DD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) M = fmaxf(M, wm[v][g]);
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float f = wm[v][g] == -INFINITY ? 0.f : exp2f(wm[v][g] - M);
+      L += f * wl[v][g];
+      A += f * wacc[v][g][d];
+    }
+    float* dst = part + ((uint64_t)split * H + h0 + g) * stride;
+    if (d == 0) {
+      dst[0] = M == -INFINITY ? -INFINITY : M * 0.69314718055994531f;  // natural-log units
+      dst[1] = L;
+    }
+    dst[2 + d] = A;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(1024) void decode_combine_kernel(const float* __restrict__ part, uint32_t n_splits,
                                                               uint32_t H, uint32_t D, T* __restrict__ out,
@@ -812,9 +1025,40 @@ hipError_t run_decode_split(const Params& p, float* ws, size_t ws_floats, hipStr
   if (kps > 1024) kps = 1024;
   const uint64_t n_splits = (n_keys + kps - 1) / kps;
   if (n_splits > (uint64_t)kMaxSplits || n_splits * H * (p.dim + 2) > ws_floats) return hipErrorNotSupported;
+  const int G = gmax == 1 ? 1 : gmax == 2 ? 2 : gmax <= 4 ? 4 : 8;
+  // f16 caches with head_dim 64 / 128 and 16-byte aligned rows: scores on MFMA,
+  // 256 keys per workgroup (one 64-key tile per wave)
+  if constexpr (std::is_same<T, half_t>::value) {
+    const bool al = ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k) |
+                      reinterpret_cast<uintptr_t>(p.v) |
+                      (p.fused_append ? reinterpret_cast<uintptr_t>(p.k_new) | reinterpret_cast<uintptr_t>(p.v_new)
+                                      : 0)) & 15) == 0;
+    if (al && (p.dim == 64 || p.dim == 128)) {
+      // 4 waves of 32 keys per workgroup (measured at 4096 keys: 7.1 us
+      // against 9.0 with 8 waves of 32 and 9.1 with 4 of 64), 64-key tiles
+      // past 8192 keys
+      const uint32_t tk = n_keys <= 8192 ? 32u : 64u;
+      const uint64_t ns = (n_keys + 4 * tk - 1) / (4 * tk);
+      if (ns <= (uint64_t)kMaxSplits && ns * H * (p.dim + 2) <= ws_floats) {
+        const dim3 g2((unsigned)ns, KV);
+#define NF_DECODE_MFMA(DDD, GG)                                                                      \
+  if (p.dim == DDD && G == GG) {                                                                     \
+    if (tk == 32) decode_mfma_kernel<MODE, DDD, GG, 32, 4><<<g2, 256, 0, s>>>(p, 4 * tk, lo, ws);     \
+    else decode_mfma_kernel<MODE, DDD, GG, 64, 4><<<g2, 256, 0, s>>>(p, 4 * tk, lo, ws);              \
+  }
+        NF_DECODE_MFMA(64, 1) NF_DECODE_MFMA(64, 2) NF_DECODE_MFMA(64, 4) NF_DECODE_MFMA(64, 8)
+        NF_DECODE_MFMA(128, 1) NF_DECODE_MFMA(128, 2) NF_DECODE_MFMA(128, 4) NF_DECODE_MFMA(128, 8)
+#undef NF_DECODE_MFMA
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        decode_combine_kernel<T><<<H, 1024, 0, s>>>(ws, (uint32_t)ns, H, p.dim, static_cast<T*>(p.out),
+                                                   q_row<MODE>(p, 0, 0), p.dim);
+        return hipGetLastError();
+      }
+    }
+  }
   const dim3 grid((unsigned)n_splits, KV);
   const int R = p.dim <= 64 ? 1 : p.dim <= 128 ? 2 : 4;
-  const int G = gmax == 1 ? 1 : gmax == 2 ? 2 : gmax <= 4 ? 4 : 8;
 #define NF_DECODE_SPLIT(GG, RR) \
   if (G == GG && R == RR) decode_split_kernel<T, MODE, GG, RR><<<grid, 64, 0, s>>>(p, (uint32_t)kps, lo, ws);
   NF_DECODE_SPLIT(1, 1) NF_DECODE_SPLIT(1, 2) NF_DECODE_SPLIT(1, 4)

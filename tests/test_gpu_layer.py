@@ -310,6 +310,15 @@ GPU_ATTN = [
     ("flash_attention_paged", False, dict(H=4, KV=4, D=64, S=1, step=37, max_seq=0, bs=16, n_blocks=3)),
     ("flash_attention_paged", False, dict(H=8, KV=2, D=128, S=24, step=0, max_seq=0, bs=8, n_blocks=3, q_offset=2)),
     ("flash_attention_paged", False, dict(H=2, KV=1, D=64, S=1, step=500, max_seq=0, bs=16, n_blocks=20)),
+    # f16 decode with the scores on MFMA (head_dim 64 / 128): partial last
+    # tiles, groups of 1 / 3 / 4 / 8 query heads, a sliding window, a 6-key
+    # cache (the paged op is f32-only, as in the reference)
+    ("flash_attention_cached", True, dict(H=32, KV=8, D=128, S=1, step=2000, max_seq=2048)),
+    ("flash_attention_cached", True, dict(H=8, KV=2, D=128, S=1, step=300, max_seq=512, window=100)),
+    ("flash_attention_gqa", True, dict(H=32, KV=8, D=128, S=1, step=777, max_seq=1024)),
+    ("flash_attention_gqa", True, dict(H=8, KV=1, D=64, S=1, step=100, max_seq=128)),
+    ("flash_attention_gqa", True, dict(H=6, KV=2, D=64, S=1, step=70, max_seq=128)),
+    ("flash_attention_gqa", True, dict(H=4, KV=4, D=128, S=1, step=5, max_seq=16)),
 ]
 
 
