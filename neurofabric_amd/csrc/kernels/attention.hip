@@ -453,6 +453,227 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
   }
 }
 
+// Prefill on MFMA (f16, head_dim DD = 64 or 128; not paged): flash attention
+// with the matrices transposed so that every operand comes out of registers
+// or LDS in the layout the next MFMA wants.  A workgroup takes 64 query
+// tokens of one head, 16 per wave; per 64-key tile of K and V (staged once
+// in LDS for the workgroup: K row-major, V transposed):
+//  * S^T[key][query] = K[key][dims] . Q^T[dims][query] on
+//    v_mfma_f32_16x16x32_f16: A = 16 key rows from LDS, B = the wave's 16
+//    queries (held in registers for the whole kernel);
+//  * online softmax in base 2 per query (a query's 64 scores are spread over
+//    the 4 lane groups of its column);
+//  * O^T[dim][query] += V^T[dim][key] . P^T[key][query]: the softmax weights
+//    of S^T's output layout are the B operand as they are (in a fixed key
+//    order), each split into two f16 pieces (two MFMAs, so the products keep
+//    fp32-level accuracy); the A operand is two 8-byte reads of the
+//    transposed V tile; fp32 accumulation.
+// Masked scores are -inf by select.  A weight of 0 times a non-finite value
+// would still be NaN inside the MFMA, so a tile that holds a non-finite
+// value and a key outside some query's range (the diagonal and window-edge
+// tiles) takes the vector-ALU P.V, which skips such (key, query) pairs as
+// the per-query kernel does.
+constexpr float kPScale = 32768.f;  // 2^15: softmax weights on the f16 MFMA path
+
+template <nfhip::AttnMode MODE, int DD>
+__global__ __launch_bounds__(256) void prefill_mfma_kernel(Params p) {
+  typedef half_t T;
+  constexpr int KSTEP = DD / 32, CPR = DD / 8, DB = DD / 16;
+  constexpr int KP = DD + 8, VP = 64 + 8;  // padded LDS row lengths (halves)
+  __shared__ __attribute__((aligned(16))) T Ks[64 * KP];
+  __shared__ __attribute__((aligned(16))) T Vt[DD * VP];
+  __shared__ __attribute__((aligned(16))) float ps[4][64][16];  // weights for the vector-ALU P.V
+  __shared__ int tile_bad;
+  const uint32_t h = blockIdx.y;
+  const uint32_t kvh = (uint32_t)((uint64_t)h * p.n_kv / p.n_heads);
+  const uint32_t S = p.seq_len;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  // heavy (late) query blocks first
+  const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * 64;
+  const uint32_t q1 = q0 + 64 < S ? q0 + 64 : S;
+  const T* Q = static_cast<const T*>(p.q);
+  const T* K = static_cast<const T*>(p.k);
+  const T* V = static_cast<const T*>(p.v);
+  auto lo_of = [&](uint32_t pos) -> uint32_t {
+    if constexpr (MODE == nfhip::AttnMode::Cached)
+      if (p.window > 0 && pos >= p.window) return pos - p.window + 1;
+    return 0u;
+  };
+  const uint32_t lo_blk = lo_of(q0), hi_blk = q1 - 1;
+
+  // this lane's query (MFMA column n of the wave's 16)
+  const uint32_t qw0 = q0 + 16 * w;
+  const uint32_t qpos = qw0 + n;
+  const bool qok = qpos < q1;
+  const uint32_t qlo = lo_of(qpos);
+  half8 qb[KSTEP];
+#pragma unroll
+  for (int st = 0; st < KSTEP; ++st) {
+    qb[st] = *reinterpret_cast<const half8*>(Q + q_row<MODE>(p, qok ? qpos : q0, h) + 32 * st + 8 * g);
+    if (!qok) qb[st] = half8{};
+  }
+  // the wave's query range (for the tiles it can skip or take unmasked)
+  const uint32_t wq_last = qw0 + 15 < q1 ? qw0 + 15 : q1 - 1;
+  const bool wave_live = qw0 < q1;
+
+  float4v ot[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b) ot[b] = float4v{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  const float sl2 = p.scale * 1.44269504088896341f;
+
+  // Tile loads into registers (next tile while this one computes): K chunk
+  // i = tid + 256u is row i / CPR, 16-byte chunk i % CPR (coalesced); V
+  // chunk u is row tid % 64, chunk tid / 64 + 4u (consecutive threads take
+  // consecutive rows, so the transposed LDS writes do not collide).  Rows
+  // past the block's last query read that query's row (in bounds) and are
+  // masked.
+  constexpr int NL = 64 * CPR / 256;
+  half8 kr[NL], vr[NL];
+  auto fetch = [&](int64_t t0) {
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+      const int i = tid + 256 * u;
+      const int kk = i / CPR, kc = i % CPR;
+      const int64_t kt = t0 + kk <= (int64_t)hi_blk ? t0 + kk : (int64_t)hi_blk;
+      kr[u] = *reinterpret_cast<const half8*>(K + kv_row<MODE>(p, kvh, (uint32_t)kt) + 8 * kc);
+      const int vk = tid & 63, vc = (tid >> 6) + 4 * u;
+      const int64_t vt = t0 + vk <= (int64_t)hi_blk ? t0 + vk : (int64_t)hi_blk;
+      vr[u] = *reinterpret_cast<const half8*>(V + kv_row<MODE>(p, kvh, (uint32_t)vt) + 8 * vc);
+    }
+  };
+  auto stage = [&](int64_t t0) {
+    bool bad = false;
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+      const int i = tid + 256 * u;
+      const int kk = i / CPR, kc = i % CPR;
+      *reinterpret_cast<half8*>(&Ks[kk * KP + 8 * kc]) = kr[u];
+      const int vk = tid & 63, vc = (tid >> 6) + 4 * u;
+      const bool vin = t0 + vk <= (int64_t)hi_blk;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const T x = vin ? vr[u][e] : (T)0.f;
+        bad = bad || !__builtin_isfinite((float)x);
+        Vt[(8 * vc + e) * VP + vk] = x;
+      }
+    }
+    if (bad) tile_bad = 1;
+  };
+
+  fetch(lo_blk);
+  for (int64_t t0 = lo_blk; t0 <= (int64_t)hi_blk; t0 += 64) {
+    __syncthreads();  // the previous tile's readers are done
+    if (tid == 0) tile_bad = 0;
+    __syncthreads();
+    stage(t0);
+    __syncthreads();
+    if (t0 + 64 <= (int64_t)hi_blk) fetch(t0 + 64);
+    if (!wave_live || t0 > (int64_t)wq_last) continue;  // no key of this tile for the wave (uniform)
+    // scores S^T: lane holds keys t0 + 16j + 4g + i for query qpos
+    float4v sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < KSTEP; ++st) {
+        const half8 a = *reinterpret_cast<const half8*>(&Ks[(16 * j + n) * KP + 32 * st + 8 * g]);
+        sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[st], sc[j], 0, 0, 0);
+      }
+    }
+    float sv[4][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t kt = t0 + 16 * j + 4 * g + i;
+        const bool in = qok && kt >= (int64_t)qlo && kt <= (int64_t)qpos;
+        sv[j][i] = in ? sc[j][i] * sl2 : -INFINITY;
+        tmax = fmaxf(tmax, sv[j][i]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float corr = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
+    float pv[4][4];
+    float psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pv[j][i] = sv[j][i] == -INFINITY ? 0.f : exp2f(sv[j][i] - m_new);
+        psum += pv[j][i];
+      }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int b = 0; b < DB; ++b) ot[b] *= corr;
+    // P.V: unmasked for the wave, or no non-finite value: on MFMA
+    const bool interior = t0 + 63 <= (int64_t)qw0 && t0 >= (int64_t)lo_of(wq_last);
+    if (interior || !tile_bad) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        // each weight times 2^15 as two f16 pieces (hi + lo, within 2^-22 of
+        // it), so the products keep fp32-level accuracy; the power of two
+        // keeps the pieces of small weights out of the f16 subnormal range
+        // and is divided out with the sum at the end
+        half8 bh, bl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p0 = pv[2 * c][i] * kPScale, p1 = pv[2 * c + 1][i] * kPScale;
+          bh[i] = (T)p0;
+          bl[i] = (T)(p0 - (float)bh[i]);
+          bh[4 + i] = (T)p1;
+          bl[4 + i] = (T)(p1 - (float)bh[4 + i]);
+        }
+#pragma unroll
+        for (int b = 0; b < DB; ++b) {
+          const T* vrow = &Vt[(16 * b + n) * VP + 32 * c + 4 * g];
+          const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow);
+          const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + 16);
+          const half8 av = __builtin_bit_cast(half8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
+          ot[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh, ot[b], 0, 0, 0);
+          ot[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl, ot[b], 0, 0, 0);
+        }
+      }
+    } else {
+      // predicated vector-ALU P.V: key kt enters query qpos only in range
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ps[w][16 * j + 4 * g + i][n] = pv[j][i];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      for (int k = 0; k < 64; ++k) {
+        const int64_t kt = t0 + k;
+        if (!(qok && kt >= (int64_t)qlo && kt <= (int64_t)qpos)) continue;
+        const float pk = ps[w][k][n] * kPScale;
+#pragma unroll
+        for (int b = 0; b < DB; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ot[b][i] += pk * (float)Vt[(16 * b + 4 * g + i) * VP + k];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+
+  if (qok) {
+    const float inv = l_run > 0.f ? 1.0f / (l_run * kPScale) : 0.f;
+    T* O = static_cast<T*>(p.out) + q_row<MODE>(p, qpos, h);
+#pragma unroll
+    for (int b = 0; b < DB; ++b) {
+      half2v lo = {(T)(ot[b][0] * inv), (T)(ot[b][1] * inv)};
+      half2v hi = {(T)(ot[b][2] * inv), (T)(ot[b][3] * inv)};
+      *reinterpret_cast<uint2*>(O + 16 * b + 4 * g) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+    }
+  }
+}
+
 // Append K_new / V_new rows to the caches: prefill rows 0..seq_len-1, decode
 // row `step`.  Cached: K_new [tokens, n_kv, dim]; Gqa: [n_kv, tokens, dim].
 template <typename T, bool HEAD_MAJOR>
@@ -1093,6 +1314,17 @@ hipError_t run(const Params& p, uint32_t nq, float* ws, size_t ws_floats, hipStr
   if (p.decode) {
     attention_kernel<T, MODE, 16><<<dim3(nq, p.n_heads), 1024, 0, s>>>(p);
     return hipGetLastError();
+  }
+  if constexpr (MODE != nfhip::AttnMode::Paged && std::is_same<T, half_t>::value) {
+    // f16, head_dim 64 / 128, 16-byte aligned rows: flash attention on MFMA
+    const bool al16 = ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k) |
+                        reinterpret_cast<uintptr_t>(p.v) | reinterpret_cast<uintptr_t>(p.out)) & 15) == 0;
+    if (al16 && (p.dim == 64 || p.dim == 128)) {
+      const dim3 grid((nq + 63) / 64, p.n_heads);
+      if (p.dim == 128) prefill_mfma_kernel<MODE, 128><<<grid, 256, 0, s>>>(p);
+      else prefill_mfma_kernel<MODE, 64><<<grid, 256, 0, s>>>(p);
+      return hipGetLastError();
+    }
   }
   if constexpr (MODE != nfhip::AttnMode::Paged) {
     // many queries per workgroup when the tiles fit and the rows allow
