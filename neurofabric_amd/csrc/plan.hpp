@@ -78,8 +78,9 @@ struct LayerParams {
 // Defaults from measured sweeps on MI355X (graph replay over 4 rotated weight
 // copies).  bench.py's configs[4] section (28672x8192 and 8192x28672 Q4_0,
 // f16 activations): the GEMV is fastest up to M = 2 (31.0 / 38.8 us against
-// 46.3 / 47.1 us for the small-batch kernel at 28672x8192; 47.7 / 47.4 us, a
-// tie, at 8192x28672 M = 2), the small-batch kernel for M = 4..16 (58.6 and
+// 46.3 / 47.1 us for the small-batch kernel at 28672x8192) while two of its
+// workgroups fit a CU's LDS (at 8192x28672 M = 2 its 112 KB activation stage
+// leaves one: 47.9 against 46.3 us; plan.cpp), the small-batch kernel for M = 4..16 (58.6 and
 // 61.6 us at M = 16 against 67.6 and 69.2 us for the tiled GEMM), the tiled
 // GEMM from M = 32 (70.2 vs 88.8 us and 69.4 vs 88.7 us).  f32 activations
 // (configs[3] Llama-3-8B Q8_0 step): the small-batch kernel up to M = 64 (two

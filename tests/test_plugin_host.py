@@ -287,6 +287,9 @@ def test_default_switch_points(lib):
     (f16); for f32 activations the small-batch kernel up to 64 rows."""
     f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
     assert _fused(lib, 2, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"   # 2 x 8192 x 2 B = 32 KB
+    # M = 2: the GEMV while two of its workgroups fit a CU (stage <= 80 KB)
+    assert _fused(lib, 2, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"  # 112 KB stage
+    assert _fused(lib, 1, 8192, 28672, **f16)["kernel"] == "gemv_q4_0_f16"
     # M = 3..4: the GEMV only for weights up to 48 MB (132 MB here)
     assert _fused(lib, 4, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
     assert _fused(lib, 4, 11008, 4096, **f16)["kernel"] == "gemv_q4_0_f16"  # 25 MB
