@@ -431,6 +431,8 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
                 for path, (gmax, smax) in pins.items():
                     prov.set_gemv_max_m(g32, gmax)
                     prov.set_skinny_max_m(smax, None, 1 << 30 if path == "skinny" else tuning[4])
+                    # the GEMV at two rows also past its default stage limit
+                    prov.set_gemv_row_limits((1 << 32) - 1 if path == "gemv" else tuning[5][0], tuning[5][1])
                     st = Step(prov)
                     for w in ws:
                         st.add("dequant_q4_0_linear_f16", [a, w], [c], M, N, K)
@@ -471,7 +473,8 @@ def crossover_sweep(prov, shapes=((28672, 8192), (8192, 28672)), Ms=(1, 2, 4, 8,
         return max(ms) if ms else 0
     out["switch_points"] = {"measured": {"gemv_max_m_f16": last_m("gemv"), "skinny_max_m_f16": last_m("skinny")},
                             "defaults": {"gemv_max_m_f16": g16, "skinny_max_m_f16": sk16,
-                                         "gemv_m3_m4_only_up_to_weight_MB": 48,
+                                         "gemv_m2_only_up_to_stage_KB": tuning[5][0] // 1024,
+                                         "gemv_m3_m4_only_up_to_weight_MB": tuning[5][1] >> 20,
                                          "skinny_f16_above_m4_only_up_to_k": tuning[4]},
                             "default_not_fastest": [(k, r["M"], r["selected_by_default"], r["fastest"])
                                                     for k in shp for r in out[k]["rows"]

@@ -122,6 +122,16 @@ NF_API nf_status nf_hip_plan_dispatch(const char *op_name,
  * the simdgroup variant disabled). */
 NF_API void nf_hip_set_gemv_max_m(uint32_t f32_path, uint32_t f16_path);
 NF_API void nf_hip_get_gemv_max_m(uint32_t *f32_path, uint32_t *f16_path);
+/* Further limits on the GEMV at M <= gemv_max_m: two rows only while the
+ * activation stage (2 x K x element size, plus the f32 Q4_0 path's
+ * partial sums) is at most m2_max_stage_bytes (default 80 KB: two
+ * workgroups per CU), three or four rows only while the weights are at
+ * most m34_max_weight_bytes (default 48 MB); past either the small-batch
+ * kernel takes the rows.  Environment overrides NF_HIP_GEMV_M2_MAX_STAGE
+ * and NF_HIP_GEMV_M4_MAX_WEIGHT (bytes).  No counterpart in the reference
+ * (one kernel for every M, metal_provider.mm:3009-3019). */
+NF_API void nf_hip_set_gemv_row_limits(uint32_t m2_max_stage_bytes, uint64_t m34_max_weight_bytes);
+NF_API void nf_hip_get_gemv_row_limits(uint32_t *m2_max_stage_bytes, uint64_t *m34_max_weight_bytes);
 NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path);
 NF_API uint32_t nf_hip_get_skinny_max_m(void);
 NF_API void nf_hip_set_skinny_max_m_f32(uint32_t f32_path);

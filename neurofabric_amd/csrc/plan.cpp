@@ -181,12 +181,12 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
       const uint64_t stage = mm * K * elt_bytes(p.a) + ((!f16 && p.q == QFmt::Q4_0) ? mm * (K / 64) * 8 : 0);
       const bool gemv_fits = K % 64 != 0 || stage <= 120 * 1024;
       // Two rows: the GEMV only while two of its workgroups fit a CU's LDS
-      // (stage <= 80 KB); past that the small-batch kernel is as fast
+      // (stage <= gemv_m2_max_stage_bytes, 80 KB); past that the small-batch kernel is as fast
       // (8192x28672 f16, 112 KB stage: 46.3 against 47.9 us; 28672x8192
       // f32, 66 KB: the GEMV 44.5 against 57.0 us).  Three or four rows:
       // the GEMV only while the weights are small enough that the
       // small-batch kernel's fixed per-launch cost dominates it.
-      const bool gemv_rows_ok = p.M == 1 || (p.M == 2 ? (stage <= 80 * 1024 || K % 256 != 0)
+      const bool gemv_rows_ok = p.M == 1 || (p.M == 2 ? (stage <= tuning.gemv_m2_max_stage_bytes || K % 256 != 0)
                                                       : p.weight_bytes <= tuning.gemv_m4_max_weight_bytes);
       if (p.M <= gemv_max && gemv_rows_ok && (gemv_fits || K % 256 != 0)) {
         p.path = Path::Gemv;

@@ -103,6 +103,7 @@ struct Tuning {
   uint32_t skinny_max_m_f16 = 16;
   uint32_t skinny_max_m_f32 = 64;
   uint64_t gemv_m4_max_weight_bytes = 48ull << 20;
+  uint32_t gemv_m2_max_stage_bytes = 80 * 1024;
   uint32_t skinny_f16_max_k = 1u << 30;
   // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernels,
   // picked by M (launch_gemm_mfma); 0..6 = one of the LDS-staged tile

@@ -875,6 +875,14 @@ uint32_t env_u32(const char* name, uint32_t dflt) {
   return (end && *end == '\0') ? (uint32_t)x : dflt;
 }
 
+uint64_t env_u64(const char* name, uint64_t dflt) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return dflt;
+  char* end = nullptr;
+  unsigned long long x = std::strtoull(v, &end, 10);
+  return (end && *end == '\0') ? (uint64_t)x : dflt;
+}
+
 }  // namespace
 }  // namespace nfhip
 
@@ -899,6 +907,10 @@ NF_API nf_status nf_plugin_register(nf_provider_vtable* vt, nf_provider* out) {
   g_prov.tuning.skinny_max_m_f16 = env_u32("NF_HIP_SKINNY_MAX_M_F16", g_prov.tuning.skinny_max_m_f16);
   g_prov.tuning.skinny_max_m_f32 = env_u32("NF_HIP_SKINNY_MAX_M_F32", g_prov.tuning.skinny_max_m_f32);
   g_prov.tuning.skinny_f16_max_k = env_u32("NF_HIP_SKINNY_F16_MAX_K", g_prov.tuning.skinny_f16_max_k);
+  g_prov.tuning.gemv_m2_max_stage_bytes =
+      env_u32("NF_HIP_GEMV_M2_MAX_STAGE", g_prov.tuning.gemv_m2_max_stage_bytes);
+  g_prov.tuning.gemv_m4_max_weight_bytes =
+      env_u64("NF_HIP_GEMV_M4_MAX_WEIGHT", g_prov.tuning.gemv_m4_max_weight_bytes);
   g_prov.tuning.gemm_tile = gemm_tile_from_name(std::getenv("NF_HIP_GEMM_TILE"));
   *out = reinterpret_cast<nf_provider>(&g_prov);
   return NF_OK;
@@ -1000,6 +1012,18 @@ NF_API void nf_hip_set_gemv_max_m(uint32_t f32_path, uint32_t f16_path) {
   std::lock_guard<std::mutex> lk(g_prov.mu);
   g_prov.tuning.gemv_max_m_f32 = f32_path;
   g_prov.tuning.gemv_max_m_f16 = f16_path;
+}
+
+NF_API void nf_hip_set_gemv_row_limits(uint32_t m2_max_stage_bytes, uint64_t m34_max_weight_bytes) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  g_prov.tuning.gemv_m2_max_stage_bytes = m2_max_stage_bytes;
+  g_prov.tuning.gemv_m4_max_weight_bytes = m34_max_weight_bytes;
+}
+
+NF_API void nf_hip_get_gemv_row_limits(uint32_t* m2_max_stage_bytes, uint64_t* m34_max_weight_bytes) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  if (m2_max_stage_bytes) *m2_max_stage_bytes = g_prov.tuning.gemv_m2_max_stage_bytes;
+  if (m34_max_weight_bytes) *m34_max_weight_bytes = g_prov.tuning.gemv_m4_max_weight_bytes;
 }
 
 NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path) {

@@ -61,6 +61,10 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
     lib.nf_hip_plan_dispatch.restype = C.c_int
     lib.nf_hip_set_gemv_max_m.argtypes = [C.c_uint32, C.c_uint32]
     lib.nf_hip_set_gemv_max_m.restype = None
+    lib.nf_hip_set_gemv_row_limits.argtypes = [C.c_uint32, C.c_uint64]
+    lib.nf_hip_set_gemv_row_limits.restype = None
+    lib.nf_hip_get_gemv_row_limits.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]
+    lib.nf_hip_get_gemv_row_limits.restype = None
     lib.nf_hip_get_gemv_max_m.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]
     lib.nf_hip_get_gemv_max_m.restype = None
     lib.nf_hip_set_skinny_max_m.argtypes = [C.c_uint32]
@@ -339,6 +343,17 @@ class Provider:
     def set_gemv_max_m(self, f32: int, f16: int) -> None:
         self.lib.nf_hip_set_gemv_max_m(f32, f16)
 
+    def set_gemv_row_limits(self, m2_max_stage_bytes: int, m34_max_weight_bytes: int) -> None:
+        """The GEMV takes two rows only while their activation stage is at
+        most m2_max_stage_bytes, three or four only while the weights are at
+        most m34_max_weight_bytes."""
+        self.lib.nf_hip_set_gemv_row_limits(m2_max_stage_bytes, m34_max_weight_bytes)
+
+    def get_gemv_row_limits(self) -> tuple:
+        a, b = C.c_uint32(), C.c_uint64()
+        self.lib.nf_hip_get_gemv_row_limits(C.byref(a), C.byref(b))
+        return a.value, b.value
+
     def set_skinny_max_m(self, f16: int, f32: int | None = None, f16_max_k: int | None = None) -> None:
         """Largest M on the small-batch kernel for f16 (and, if given, f32)
         activations; f16_max_k: longest rows it takes at M > 4 (f16)."""
@@ -380,12 +395,13 @@ class Provider:
     def get_tuning(self) -> tuple:
         """Every switch point and the GEMM kernel choice, for set_tuning."""
         return (self.get_gemv_max_m(), self.get_skinny_max_m(), self.get_skinny_max_m_f32(), self.get_gemm_tile(),
-                int(self.lib.nf_hip_get_skinny_f16_max_k()))
+                int(self.lib.nf_hip_get_skinny_f16_max_k()), self.get_gemv_row_limits())
 
     def set_tuning(self, t: tuple) -> None:
         self.set_gemv_max_m(*t[0])
         self.set_skinny_max_m(t[1], t[2], t[4])
         self.set_gemm_tile(t[3])
+        self.set_gemv_row_limits(*t[5])
 
     def get_gemv_max_m(self):
         a, b = C.c_uint32(), C.c_uint32()

@@ -97,6 +97,7 @@ def check_config(provider, oracle_mod, weights, fmt, M, N, K, f16, seed):
 def _force(provider, path):
     if path == "gemv":
         provider.set_gemv_max_m(1 << 30, 1 << 30)
+        provider.set_gemv_row_limits((1 << 32) - 1, (1 << 64) - 1)
     elif path == "skinny":
         provider.set_gemv_max_m(0, 0)
         provider.set_skinny_max_m(1 << 30, 1 << 30, 1 << 30)

@@ -315,6 +315,25 @@ def test_default_switch_points(lib):
     assert _fused(lib, 100, 64, 96)["kernel"] == "gemv_q4_0_f32"  # K % 64 != 0
 
 
+def test_gemv_row_limits(lib):
+    """The GEMV's two-row stage limit and three/four-row weight limit are
+    settable through the C-ABI; the defaults come back unchanged."""
+    f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
+    st, wb = C.c_uint32(), C.c_uint64()
+    lib.nf_hip_get_gemv_row_limits(C.byref(st), C.byref(wb))
+    assert (st.value, wb.value) == (80 * 1024, 48 << 20)
+    try:
+        lib.nf_hip_set_gemv_row_limits(C.c_uint32(120 * 1024), C.c_uint64(200 << 20))
+        assert _fused(lib, 2, 8192, 28672, **f16)["kernel"] == "gemv_q4_0_f16"   # 112 KB stage
+        assert _fused(lib, 4, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"   # 132 MB
+        lib.nf_hip_set_gemv_row_limits(C.c_uint32(0), C.c_uint64(0))
+        assert _fused(lib, 2, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
+        assert _fused(lib, 4, 4096, 4096)["kernel"] == "skinny_mfma_q4_0_f32"
+        assert _fused(lib, 1, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"
+    finally:
+        lib.nf_hip_set_gemv_row_limits(C.c_uint32(st.value), C.c_uint64(wb.value))
+
+
 # Every op name of the Metal provider's dispatch map (metal_provider.mm:3180-3209,
 # the dequant names registered from s_dequant_map) plus the model layer's fp16
 # rope name (arch_registry.hpp:140).
