@@ -1248,7 +1248,7 @@ hipError_t run_decode_split(const Params& p, float* ws, size_t ws_floats, hipStr
   if (n_splits > (uint64_t)kMaxSplits || n_splits * H * (p.dim + 2) > ws_floats) return hipErrorNotSupported;
   const int G = gmax == 1 ? 1 : gmax == 2 ? 2 : gmax <= 4 ? 4 : 8;
   // f16 caches with head_dim 64 / 128 and 16-byte aligned rows: scores on MFMA,
-  // 256 keys per workgroup (one 64-key tile per wave)
+  // 4 waves per workgroup, each over its own range of tk keys
   if constexpr (std::is_same<T, half_t>::value) {
     const bool al = ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k) |
                       reinterpret_cast<uintptr_t>(p.v) |
