@@ -861,8 +861,11 @@ nf_status ddi_query_caps(nf_provider self, nf_driver_caps* caps) {
   std::lock_guard<std::mutex> lk(p->mu);
   if (p->initialized) caps->memory_bytes = p->props.totalGlobalMem;
   caps->flops = 2516600000000000ull;  // MI355X dense fp16 MFMA peak, FLOP/s
+  // f32 / f16 tensors and every block format a dequant op decodes
   caps->supported_dtypes = (1u << NF_DTYPE_F32) | (1u << NF_DTYPE_F16) | (1u << NF_DTYPE_Q4_0) |
-                           (1u << NF_DTYPE_Q8_0);
+                           (1u << NF_DTYPE_Q8_0) | (1u << NF_DTYPE_Q4_1) | (1u << NF_DTYPE_Q5_0) |
+                           (1u << NF_DTYPE_Q5_1) | (1u << NF_DTYPE_Q2_K) | (1u << NF_DTYPE_Q3_K) |
+                           (1u << NF_DTYPE_Q4_K) | (1u << NF_DTYPE_Q5_K) | (1u << NF_DTYPE_Q6_K);
   caps->flags = NF_CAP_ASYNC | NF_CAP_FP16 | NF_CAP_INT8;
   return NF_OK;
 }

@@ -180,7 +180,11 @@ def test_async_ddi_and_caps(provider, oracle_mod):
     caps = provider.caps()
     assert caps.memory_bytes > 200 * 2 ** 30  # 288 GB HBM3E
     assert caps.flags & abi.NF_CAP_ASYNC and caps.flags & abi.NF_CAP_FP16
-    assert caps.supported_dtypes & (1 << abi.NF_DTYPE_Q4_0) and caps.supported_dtypes & (1 << abi.NF_DTYPE_Q8_0)
+    for dt in (abi.NF_DTYPE_F32, abi.NF_DTYPE_F16, abi.NF_DTYPE_Q4_0, abi.NF_DTYPE_Q8_0, abi.NF_DTYPE_Q4_1,
+               abi.NF_DTYPE_Q5_0, abi.NF_DTYPE_Q5_1, abi.NF_DTYPE_Q2_K, abi.NF_DTYPE_Q3_K, abi.NF_DTYPE_Q4_K,
+               abi.NF_DTYPE_Q5_K, abi.NF_DTYPE_Q6_K):
+        assert caps.supported_dtypes & (1 << dt), dt
+    assert not caps.supported_dtypes & (1 << abi.NF_DTYPE_BF16)
     M, N, K = 1, 1024, 2048
     A = syn.activations(M, K, seed=8)
     W = syn.q4_0_weights(N, K, seed=9)
