@@ -462,7 +462,9 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
 //    v_mfma_f32_16x16x32_f16: A = 16 key rows from LDS, B = the wave's 16
 //    queries (held in registers for the whole kernel);
 //  * online softmax in base 2 per query (a query's 64 scores are spread over
-//    the 4 lane groups of its column);
+//    the 4 lane groups of its column); the weights carry a factor 2^15
+//    (folded into the exponent), which keeps the f16 pieces below out of the
+//    subnormal range and is divided out with the sum at the end;
 //  * O^T[dim][query] += V^T[dim][key] . P^T[key][query]: the softmax weights
 //    of S^T's output layout are the B operand as they are (in a fixed key
 //    order), each split into two f16 pieces (two MFMAs, so the products keep
@@ -472,36 +474,58 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
 // would still be NaN inside the MFMA, so a tile that holds a non-finite
 // value and a key outside some query's range (the diagonal and window-edge
 // tiles) takes the vector-ALU P.V, which skips such (key, query) pairs as
-// the per-query kernel does.
-constexpr float kPScale = 32768.f;  // 2^15: softmax weights on the f16 MFMA path
+// the per-query kernel does.  Tiles inside every query's range (all but the
+// last one or two of a workgroup) skip the masking, the zeroing of rows past
+// the range and the non-finite check: the vector-ALU work per tile is then
+// about what the 48 MFMAs take.
+// Workgroup order: workgroup L runs on XCD L % 8, so each XCD gets the query
+// blocks of whole KV heads (heavy, late blocks first) and its L2 holds one
+// head's K and V (2048 tokens x 32 heads x 128: 240 -> 147 us).
+constexpr float kPLog2Scale = 15.f;  // softmax weights carry 2^15 on the f16 MFMA path
 
 template <nfhip::AttnMode MODE, int DD>
-__global__ __launch_bounds__(256) void prefill_mfma_kernel(Params p) {
+__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
+  static_assert(MODE != nfhip::AttnMode::Paged, "rows of a KV head must be contiguous in position");
   typedef half_t T;
   constexpr int KSTEP = DD / 32, CPR = DD / 8, DB = DD / 16;
   constexpr int KP = DD + 8, VP = 64 + 8;  // padded LDS row lengths (halves)
+  constexpr int NL = 64 * CPR / 256;       // 16-byte K and V chunks per thread and tile
   __shared__ __attribute__((aligned(16))) T Ks[64 * KP];
   __shared__ __attribute__((aligned(16))) T Vt[DD * VP];
   __shared__ __attribute__((aligned(16))) float ps[4][64][16];  // weights for the vector-ALU P.V
-  __shared__ int tile_bad;
-  const uint32_t h = blockIdx.y;
+  __shared__ int tile_bad[2];  // per tile parity: the staged V holds a non-finite value
+  const uint32_t S = p.seq_len, nqb = gridDim.x;
+  uint32_t h, qblk;
+  {
+    const uint32_t total = nqb * gridDim.y, L = blockIdx.x + nqb * blockIdx.y;
+    const uint32_t G = p.n_heads / p.n_kv;
+    if (total % 8 == 0 && p.n_heads % p.n_kv == 0) {
+      const uint32_t i = (L % 8) * (total / 8) + L / 8;  // a bijection of [0, total)
+      const uint32_t kv_i = i / (G * nqb), rem = i % (G * nqb);
+      h = kv_i * G + rem % G;
+      qblk = nqb - 1 - rem / G;
+    } else {
+      h = blockIdx.y;
+      qblk = nqb - 1 - blockIdx.x;
+    }
+  }
   const uint32_t kvh = (uint32_t)((uint64_t)h * p.n_kv / p.n_heads);
-  const uint32_t S = p.seq_len;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  // heavy (late) query blocks first
-  const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * 64;
+  const uint32_t q0 = qblk * 64;
   const uint32_t q1 = q0 + 64 < S ? q0 + 64 : S;
   const T* Q = static_cast<const T*>(p.q);
-  const T* K = static_cast<const T*>(p.k);
-  const T* V = static_cast<const T*>(p.v);
+  // rows of this KV head: position pos at Kh + pos * DD
+  const T* Kh = static_cast<const T*>(p.k) + kv_row<MODE>(p, kvh, 0);
+  const T* Vh = static_cast<const T*>(p.v) + kv_row<MODE>(p, kvh, 0);
   auto lo_of = [&](uint32_t pos) -> uint32_t {
     if constexpr (MODE == nfhip::AttnMode::Cached)
       if (p.window > 0 && pos >= p.window) return pos - p.window + 1;
     return 0u;
   };
   const uint32_t lo_blk = lo_of(q0), hi_blk = q1 - 1;
+  const uint32_t lo_last = lo_of(hi_blk);
 
   // this lane's query (MFMA column n of the wave's 16)
   const uint32_t qw0 = q0 + 16 * w;
@@ -517,6 +541,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(Params p) {
   // the wave's query range (for the tiles it can skip or take unmasked)
   const uint32_t wq_last = qw0 + 15 < q1 ? qw0 + 15 : q1 - 1;
   const bool wave_live = qw0 < q1;
+  const uint32_t wlo_last = lo_of(wq_last);
 
   float4v ot[DB];
 #pragma unroll
@@ -527,119 +552,185 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(Params p) {
   // Tile loads into registers (next tile while this one computes): K chunk
   // i = tid + 256u is row i / CPR, 16-byte chunk i % CPR (coalesced); V
   // chunk u is row tid % 64, chunk tid / 64 + 4u (consecutive threads take
-  // consecutive rows, so the transposed LDS writes do not collide).  Rows
-  // past the block's last query read that query's row (in bounds) and are
-  // masked.
-  constexpr int NL = 64 * CPR / 256;
+  // consecutive rows, so the transposed LDS writes do not collide).  In the
+  // last tile, rows past the block's last query read that query's row (in
+  // bounds) and are zeroed when staged.
   half8 kr[NL], vr[NL];
+  const int vk = tid & 63;
   auto fetch = [&](int64_t t0) {
+    if (t0 + 63 <= (int64_t)hi_blk) {  // uniform: the whole tile is in range
+      const T* kt = Kh + (uint64_t)t0 * DD;
+      const T* vt = Vh + (uint64_t)(t0 + vk) * DD;
 #pragma unroll
-    for (int u = 0; u < NL; ++u) {
-      const int i = tid + 256 * u;
-      const int kk = i / CPR, kc = i % CPR;
-      const int64_t kt = t0 + kk <= (int64_t)hi_blk ? t0 + kk : (int64_t)hi_blk;
-      kr[u] = *reinterpret_cast<const half8*>(K + kv_row<MODE>(p, kvh, (uint32_t)kt) + 8 * kc);
-      const int vk = tid & 63, vc = (tid >> 6) + 4 * u;
-      const int64_t vt = t0 + vk <= (int64_t)hi_blk ? t0 + vk : (int64_t)hi_blk;
-      vr[u] = *reinterpret_cast<const half8*>(V + kv_row<MODE>(p, kvh, (uint32_t)vt) + 8 * vc);
+      for (int u = 0; u < NL; ++u) {
+        const int i = tid + 256 * u;
+        kr[u] = *reinterpret_cast<const half8*>(kt + (i / CPR) * DD + 8 * (i % CPR));
+        vr[u] = *reinterpret_cast<const half8*>(vt + 8 * ((tid >> 6) + 4 * u));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < NL; ++u) {
+        const int i = tid + 256 * u;
+        const int64_t kt = t0 + i / CPR <= (int64_t)hi_blk ? t0 + i / CPR : (int64_t)hi_blk;
+        kr[u] = *reinterpret_cast<const half8*>(Kh + (uint64_t)kt * DD + 8 * (i % CPR));
+        const int64_t vt = t0 + vk <= (int64_t)hi_blk ? t0 + vk : (int64_t)hi_blk;
+        vr[u] = *reinterpret_cast<const half8*>(Vh + (uint64_t)vt * DD + 8 * ((tid >> 6) + 4 * u));
+      }
     }
   };
-  auto stage = [&](int64_t t0) {
-    bool bad = false;
+  T* const vtw = &Vt[8 * (tid >> 6) * VP + vk];  // dim 8 (tid / 64 + 4u) + e of key vk
+  auto stage_k = [&]() {
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
       const int i = tid + 256 * u;
-      const int kk = i / CPR, kc = i % CPR;
-      *reinterpret_cast<half8*>(&Ks[kk * KP + 8 * kc]) = kr[u];
-      const int vk = tid & 63, vc = (tid >> 6) + 4 * u;
-      const bool vin = t0 + vk <= (int64_t)hi_blk;
+      *reinterpret_cast<half8*>(&Ks[(i / CPR) * KP + 8 * (i % CPR)]) = kr[u];
+    }
+  };
+  auto stage_v = [&]() {
+#pragma unroll
+    for (int u = 0; u < NL; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vtw[(32 * u + e) * VP] = vr[u][e];
+  };
+  // rows past the range as zeros; a non-finite value marks the tile
+  auto stage_v_checked = [&](int64_t t0, int par) {
+    bool bad = false;
+    const bool vin = t0 + vk <= (int64_t)hi_blk;
+#pragma unroll
+    for (int u = 0; u < NL; ++u)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const T x = vin ? vr[u][e] : (T)0.f;
         bad = bad || !__builtin_isfinite((float)x);
-        Vt[(8 * vc + e) * VP + vk] = x;
+        vtw[(32 * u + e) * VP] = x;
       }
-    }
-    if (bad) tile_bad = 1;
+    if (bad) tile_bad[par] = 1;
   };
 
-  fetch(lo_blk);
-  for (int64_t t0 = lo_blk; t0 <= (int64_t)hi_blk; t0 += 64) {
-    __syncthreads();  // the previous tile's readers are done
-    if (tid == 0) tile_bad = 0;
-    __syncthreads();
-    stage(t0);
-    __syncthreads();
-    if (t0 + 64 <= (int64_t)hi_blk) fetch(t0 + 64);
-    if (!wave_live || t0 > (int64_t)wq_last) continue;  // no key of this tile for the wave (uniform)
-    // scores S^T: lane holds keys t0 + 16j + 4g + i for query qpos
+  // Sum / max over the 4 lanes of a query's column (lanes n, n + 16, n + 32,
+  // n + 48).  v_permlane16_swap / v_permlane32_swap exchange rows between
+  // their two registers, so with both holding v each lane ends with its own
+  // value and its partner's (lane ^ 16, then lane ^ 32) in the pair.  Inline
+  // asm: the compiler's builtins for these instructions lose the second
+  // result; the s_nop gives the two wait states a VALU write needs before a
+  // permlane reads it.
+  auto swap_pair = [](float v, auto row32) {
+    float a = v, b = v;
+    if constexpr (decltype(row32)::value)
+      asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    else
+      asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return float2s{a, b};
+  };
+  auto col_max = [&](float v) {
+    float2s r = swap_pair(v, std::false_type{});
+    r = swap_pair(fmaxf(r[0], r[1]), std::true_type{});
+    return fmaxf(r[0], r[1]);
+  };
+  auto col_sum = [&](float v) {
+    float2s r = swap_pair(v, std::false_type{});
+    r = swap_pair(r[0] + r[1], std::true_type{});
+    return r[0] + r[1];
+  };
+
+  // One staged tile for this wave.  INTERIOR: every key in every query's
+  // range (no masking; P.V always on MFMA).
+  auto tile = [&](int64_t t0, int par, auto interior_c) {
+    constexpr bool INTERIOR = decltype(interior_c)::value;
+    // scores S^T: lane holds keys t0 + 16j + 4g + i for query qpos; the
+    // operand reads of half the head_dim first, then the 4 independent
+    // accumulation chains
     float4v sc[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      sc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) sc[j] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int st = 0; st < KSTEP; ++st) {
-        const half8 a = *reinterpret_cast<const half8*>(&Ks[(16 * j + n) * KP + 32 * st + 8 * g]);
-        sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[st], sc[j], 0, 0, 0);
-      }
+    for (int h2 = 0; h2 < (KSTEP + 1) / 2; ++h2) {
+      constexpr int NS = KSTEP < 2 ? KSTEP : 2;
+      half8 a[NS][4];
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          a[st][j] = *reinterpret_cast<const half8*>(&Ks[(16 * j + n) * KP + 32 * (NS * h2 + st) + 8 * g]);
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[st][j], qb[NS * h2 + st], sc[j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // bounds the operand registers in flight
     }
-    float sv[4][4];
-    float tmax = -INFINITY;
+    // base-2 scores (the scale folded into the exponent's fma); the max of
+    // the raw scores times the positive scale is the max of the scaled ones
+    float sr[4][4];
+    float rmax = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t kt = t0 + 16 * j + 4 * g + i;
-        const bool in = qok && kt >= (int64_t)qlo && kt <= (int64_t)qpos;
-        sv[j][i] = in ? sc[j][i] * sl2 : -INFINITY;
-        tmax = fmaxf(tmax, sv[j][i]);
+        if constexpr (INTERIOR) {
+          sr[j][i] = sc[j][i];
+        } else {
+          const int64_t kt = t0 + 16 * j + 4 * g + i;
+          const bool in = qok && kt >= (int64_t)qlo && kt <= (int64_t)qpos;
+          sr[j][i] = in ? sc[j][i] : -INFINITY;
+        }
+        rmax = fmaxf(rmax, sr[j][i]);
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float corr = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
+    rmax = col_max(rmax);
+    const float m_new = fmaxf(m_run, rmax * sl2);
+    const float corr = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    const float mb = m_new - kPLog2Scale;
     float pv[4][4];
     float psum = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        pv[j][i] = sv[j][i] == -INFINITY ? 0.f : exp2f(sv[j][i] - m_new);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sr[j][i], sl2, -mb));
+        if constexpr (INTERIOR) {
+          pv[j][i] = e;
+        } else {
+          // a masked score is -inf: exp2 gives 0 unless the whole column is
+          // masked so far (m_new = -inf, a NaN argument)
+          pv[j][i] = sr[j][i] == -INFINITY ? 0.f : e;
+        }
         psum += pv[j][i];
       }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
+    psum = col_sum(psum);
     l_run = l_run * corr + psum;
     m_run = m_new;
 #pragma unroll
     for (int b = 0; b < DB; ++b) ot[b] *= corr;
     // P.V: unmasked for the wave, or no non-finite value: on MFMA
-    const bool interior = t0 + 63 <= (int64_t)qw0 && t0 >= (int64_t)lo_of(wq_last);
-    if (interior || !tile_bad) {
+    if (INTERIOR || !tile_bad[par]) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        // each weight times 2^15 as two f16 pieces (hi + lo, within 2^-22 of
-        // it), so the products keep fp32-level accuracy; the power of two
-        // keeps the pieces of small weights out of the f16 subnormal range
-        // and is divided out with the sum at the end
-        half8 bh, bl;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p0 = pv[2 * c][i] * kPScale, p1 = pv[2 * c + 1][i] * kPScale;
-          bh[i] = (T)p0;
-          bl[i] = (T)(p0 - (float)bh[i]);
-          bh[4 + i] = (T)p1;
-          bl[4 + i] = (T)(p1 - (float)bh[4 + i]);
-        }
+        __builtin_amdgcn_sched_barrier(0);  // bounds the operand registers in flight
+        half8 av[DB];
 #pragma unroll
         for (int b = 0; b < DB; ++b) {
           const T* vrow = &Vt[(16 * b + n) * VP + 32 * c + 4 * g];
           const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow);
           const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + 16);
-          const half8 av = __builtin_bit_cast(half8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
-          ot[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh, ot[b], 0, 0, 0);
-          ot[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl, ot[b], 0, 0, 0);
+          av[b] = __builtin_bit_cast(half8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
         }
+        // each weight as two f16 pieces, hi (rounded toward zero) + lo (the
+        // remainder, exact in fp32, rounded toward zero), within 2^-20 of it
+        uint32_t wh[4], wl[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float a0 = pv[2 * c + (k >> 1)][2 * (k & 1)], a1 = pv[2 * c + (k >> 1)][2 * (k & 1) + 1];
+          const half2v hh = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a0, a1));
+          const half2v ll = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a0 - (float)hh[0], a1 - (float)hh[1]));
+          wh[k] = __builtin_bit_cast(uint32_t, hh);
+          wl[k] = __builtin_bit_cast(uint32_t, ll);
+        }
+        const half8 bh = __builtin_bit_cast(half8, u32x4{wh[0], wh[1], wh[2], wh[3]});
+        const half8 bl = __builtin_bit_cast(half8, u32x4{wl[0], wl[1], wl[2], wl[3]});
+#pragma unroll
+        for (int b = 0; b < DB; ++b) ot[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[b], bh, ot[b], 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < DB; ++b) ot[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[b], bl, ot[b], 0, 0, 0);
       }
     } else {
       // predicated vector-ALU P.V: key kt enters query qpos only in range
@@ -652,7 +743,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(Params p) {
       for (int k = 0; k < 64; ++k) {
         const int64_t kt = t0 + k;
         if (!(qok && kt >= (int64_t)qlo && kt <= (int64_t)qpos)) continue;
-        const float pk = ps[w][k][n] * kPScale;
+        const float pk = ps[w][k][n];
 #pragma unroll
         for (int b = 0; b < DB; ++b)
 #pragma unroll
@@ -660,10 +751,32 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(Params p) {
       }
       __builtin_amdgcn_wave_barrier();
     }
+  };
+
+  if (tid == 0) tile_bad[0] = tile_bad[1] = 0;
+  fetch(lo_blk);
+  int par = 0;
+  for (int64_t t0 = lo_blk; t0 <= (int64_t)hi_blk; t0 += 64, par ^= 1) {
+    __syncthreads();  // the previous tile's readers are done
+    // the other parity's flag was last read before this barrier and is next
+    // set after the following tile's first barrier
+    if (tid == 0) tile_bad[par ^ 1] = 0;
+    stage_k();
+    // every key of the tile in every query's range: no zeroing, no check
+    // (each wave then takes the MFMA P.V)
+    if (t0 + 63 <= (int64_t)q0 && t0 >= (int64_t)lo_last) stage_v();
+    else stage_v_checked(t0, par);
+    __syncthreads();
+    if (t0 + 64 <= (int64_t)hi_blk) fetch(t0 + 64);
+    if (!wave_live || t0 > (int64_t)wq_last) continue;  // no key of this tile for the wave (uniform)
+    // every key of the tile in every query's range of the wave (uniform):
+    // the tile body without masking, else with it
+    if (t0 + 63 <= (int64_t)qw0 && t0 >= (int64_t)wlo_last) tile(t0, par, std::true_type{});
+    else tile(t0, par, std::false_type{});
   }
 
   if (qok) {
-    const float inv = l_run > 0.f ? 1.0f / (l_run * kPScale) : 0.f;
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
     T* O = static_cast<T*>(p.out) + q_row<MODE>(p, qpos, h);
 #pragma unroll
     for (int b = 0; b < DB; ++b) {
