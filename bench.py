@@ -692,10 +692,11 @@ def run_layer(prov) -> dict:
                           buf(KV * ctx * D, dt)], [buf(H * D, dt, False)]), pc, copies=8, steps=40)
     S = 2048
     pc = push_constants(seq_len=S, n_heads=H, head_dim=D, M=KV, step_idx=0, max_seq_len=S)
-    measure("prefill_attention_f16_h32kv8d128_s2048", "flash_attention_cached",
-            lambda: ([buf(S * H * D, F16), buf(S * KV * D, F16), buf(S * KV * D, F16), buf(KV * S * D, F16, False),
-                      buf(KV * S * D, F16, False)], [buf(S * H * D, F16, False)]), pc,
-            flops=2 * S * S * D * H, steps=3)
+    for dt, tag in ((F16, "f16"), (F32, "f32")):
+        measure(f"prefill_attention_{tag}_h32kv8d128_s2048", "flash_attention_cached",
+                lambda: ([buf(S * H * D, dt), buf(S * KV * D, dt), buf(S * KV * D, dt), buf(KV * S * D, dt, False),
+                          buf(KV * S * D, dt, False)], [buf(S * H * D, dt, False)]), pc,
+                flops=2 * S * S * D * H, steps=3)
     T, E = 2048, 4096
     for f16 in (True, False):
         dt, tag = (F16, "f16") if f16 else (F32, "f32")

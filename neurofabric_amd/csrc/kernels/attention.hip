@@ -84,6 +84,25 @@ __device__ __forceinline__ uint64_t kv_row(const Params& p, uint32_t kvh, uint32
   return (((uint64_t)phys * p.n_kv + kvh) * p.block_size + pos % p.block_size) * D;
 }
 
+// Workgroup -> (query head, query block) for the prefill kernels and the
+// per-query kernel (grid x = query blocks, y = heads).  Workgroup L runs on XCD L % 8, and each XCD
+// has its own L2: give each XCD the query blocks of whole KV heads, so its
+// L2 holds those heads' K and V instead of every head's, with the heavy
+// (late, most keys) blocks first.  Any other grid keeps the plain order.
+__device__ __forceinline__ void prefill_block(const Params& p, uint32_t& h, uint32_t& qblk) {
+  const uint32_t nqb = gridDim.x, total = nqb * gridDim.y, L = blockIdx.x + nqb * blockIdx.y;
+  const uint32_t G = p.n_heads / p.n_kv;
+  if (total % 8 == 0 && p.n_heads % p.n_kv == 0) {
+    const uint32_t i = (L % 8) * (total / 8) + L / 8;  // a bijection of [0, total)
+    const uint32_t kv_i = i / (G * nqb), rem = i % (G * nqb);
+    h = kv_i * G + rem % G;
+    qblk = nqb - 1 - rem / G;
+  } else {
+    h = blockIdx.y;
+    qblk = nqb - 1 - blockIdx.x;
+  }
+}
+
 constexpr int kBatch = 8;
 
 // Columns lane + 64 r of value rows t0 + j0 .. t0 + j0 + kBatch - 1.  Every
@@ -118,8 +137,8 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(Params p) {
   __shared__ float part_acc[NW][kMaxDim];
   __shared__ float part_m[NW], part_l[NW];
 
-  const uint32_t qi = blockIdx.x;  // query token
-  const uint32_t h = blockIdx.y;
+  uint32_t qi, h;  // query token, head
+  prefill_block(p, h, qi);
   const uint32_t kvh = (uint32_t)((uint64_t)h * p.n_kv / p.n_heads);
   const uint32_t D = p.dim;
   const int lane = threadIdx.x & 63;
@@ -273,11 +292,12 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
   __shared__ float4v ps[NW][kTile];
 
   typedef typename Vec4<T>::type T4;
-  const uint32_t h = blockIdx.y;
+  uint32_t h, qblk;
+  prefill_block(p, h, qblk);
   const uint32_t kvh = (uint32_t)((uint64_t)h * p.n_kv / p.n_heads);
   const uint32_t D = p.dim, D4 = D / 4;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t q0 = blockIdx.x * kQB;
+  const uint32_t q0 = qblk * kQB;
   const uint32_t q1 = q0 + kQB < p.seq_len ? q0 + kQB : p.seq_len;
   const T* Q = static_cast<const T*>(p.q);
   const T* K = static_cast<const T*>(p.k);
@@ -462,9 +482,10 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
 //    v_mfma_f32_16x16x32_f16: A = 16 key rows from LDS, B = the wave's 16
 //    queries (held in registers for the whole kernel);
 //  * online softmax in base 2 per query (a query's 64 scores are spread over
-//    the 4 lane groups of its column); the weights carry a factor 2^15
+//    the 4 lane groups of its column); the weights carry a factor 2^7
 //    (folded into the exponent), which keeps the f16 pieces below out of the
-//    subnormal range and is divided out with the sum at the end;
+//    subnormal range and is divided out with the sum at the end, and the
+//    reference max is rescaled lazily (only when a score passes it by 2^8);
 //  * O^T[dim][query] += V^T[dim][key] . P^T[key][query]: the softmax weights
 //    of S^T's output layout are the B operand as they are (in a fixed key
 //    order), each split into two f16 pieces (two MFMAs, so the products keep
@@ -478,10 +499,10 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
 // last one or two of a workgroup) skip the masking, the zeroing of rows past
 // the range and the non-finite check: the vector-ALU work per tile is then
 // about what the 48 MFMAs take.
-// Workgroup order: workgroup L runs on XCD L % 8, so each XCD gets the query
-// blocks of whole KV heads (heavy, late blocks first) and its L2 holds one
-// head's K and V (2048 tokens x 32 heads x 128: 240 -> 147 us).
-constexpr float kPLog2Scale = 15.f;  // softmax weights carry 2^15 on the f16 MFMA path
+// Workgroup order: prefill_block (2048 tokens x 32 heads x 128: 240 -> 147
+// us from the L2 locality alone).
+constexpr float kPLog2Scale = 7.f;  // softmax weights carry 2^7 on the f16 MFMA path
+constexpr float kLazyLog2 = 8.f;    // the reference max may lag the running max by 2^8
 
 template <nfhip::AttnMode MODE, int DD>
 __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
@@ -494,21 +515,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) T Vt[DD * VP];
   __shared__ __attribute__((aligned(16))) float ps[4][64][16];  // weights for the vector-ALU P.V
   __shared__ int tile_bad[2];  // per tile parity: the staged V holds a non-finite value
-  const uint32_t S = p.seq_len, nqb = gridDim.x;
+  const uint32_t S = p.seq_len;
   uint32_t h, qblk;
-  {
-    const uint32_t total = nqb * gridDim.y, L = blockIdx.x + nqb * blockIdx.y;
-    const uint32_t G = p.n_heads / p.n_kv;
-    if (total % 8 == 0 && p.n_heads % p.n_kv == 0) {
-      const uint32_t i = (L % 8) * (total / 8) + L / 8;  // a bijection of [0, total)
-      const uint32_t kv_i = i / (G * nqb), rem = i % (G * nqb);
-      h = kv_i * G + rem % G;
-      qblk = nqb - 1 - rem / G;
-    } else {
-      h = blockIdx.y;
-      qblk = nqb - 1 - blockIdx.x;
-    }
-  }
+  prefill_block(p, h, qblk);
   const uint32_t kvh = (uint32_t)((uint64_t)h * p.n_kv / p.n_heads);
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -677,9 +686,20 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
         rmax = fmaxf(rmax, sr[j][i]);
       }
     rmax = col_max(rmax);
-    const float m_new = fmaxf(m_run, rmax * sl2);
-    const float corr = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-    const float mb = m_new - kPLog2Scale;
+    // Lazy rescale: the reference max m_run moves (and the sum and the
+    // accumulators are rescaled) only when a score of the wave exceeds it by
+    // more than kLazyLog2; the weights then stay below 2^(kLazyLog2 +
+    // kPLog2Scale) = 2^15, within f16 range.
+    const float tmax = rmax * sl2;
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + kLazyLog2) != 0) {  // uniform
+      const float m_new = fmaxf(m_run, tmax);
+      const float corr = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= corr;
+#pragma unroll
+      for (int b = 0; b < DB; ++b) ot[b] *= corr;
+      m_run = m_new;
+    }
+    const float mb = m_run - kPLog2Scale;
     float pv[4][4];
     float psum = 0.f;
 #pragma unroll
@@ -691,16 +711,12 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
           pv[j][i] = e;
         } else {
           // a masked score is -inf: exp2 gives 0 unless the whole column is
-          // masked so far (m_new = -inf, a NaN argument)
+          // masked so far (m_run = -inf, a NaN argument)
           pv[j][i] = sr[j][i] == -INFINITY ? 0.f : e;
         }
         psum += pv[j][i];
       }
-    psum = col_sum(psum);
-    l_run = l_run * corr + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int b = 0; b < DB; ++b) ot[b] *= corr;
+    l_run += col_sum(psum);
     // P.V: unmasked for the wave, or no non-finite value: on MFMA
     if (INTERIOR || !tile_bad[par]) {
 #pragma unroll
@@ -721,7 +737,8 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
         for (int k = 0; k < 4; ++k) {
           const float a0 = pv[2 * c + (k >> 1)][2 * (k & 1)], a1 = pv[2 * c + (k >> 1)][2 * (k & 1) + 1];
           const half2v hh = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a0, a1));
-          const half2v ll = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a0 - (float)hh[0], a1 - (float)hh[1]));
+          const half2v ll = __builtin_bit_cast(
+              half2v, __builtin_amdgcn_cvt_pkrtz(__builtin_fmaf((float)hh[0], -1.f, a0), __builtin_fmaf((float)hh[1], -1.f, a1)));
           wh[k] = __builtin_bit_cast(uint32_t, hh);
           wl[k] = __builtin_bit_cast(uint32_t, ll);
         }
