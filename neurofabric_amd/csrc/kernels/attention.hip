@@ -804,6 +804,259 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
   }
 }
 
+// Prefill on fp32 MFMA (f32, head_dim DD = 64 or 128; not paged): the same
+// flash attention on v_mfma_f32_16x16x4_f32, whose products and sums are
+// fp32 like the reference's loops.  A workgroup takes 64 query tokens of one
+// head, 16 per wave, and 32-key tiles of K and V staged row-major in LDS
+// (rows padded to DD + 4 floats).  The MFMA takes one value per lane per
+// operand (A[i][k] from lane i + 16k, B[k][j] from lane j + 16k; lane
+// j + 16k holds D[4k .. 4k + 3][j]), and the order in which the head_dim
+// (scores) or the keys (P.V) are summed is free, so both products read whole
+// 16-byte LDS chunks:
+//  * S^T[key][query]: k-step s of lane group g takes dim DD/4 g + s, so a
+//    lane reads DD/4 consecutive floats of its key row; the wave's queries
+//    are the B operand (DD/4 floats per lane, in registers);
+//  * O^T[dim][query] += V^T . P^T: the k-step over keys 16j + 4g + i (lane
+//    group g) takes the weight the scores left in lane (query, g) as
+//    element (j, i), and row m of dim block b is dim 4m + b % 4 + 64 (b / 4),
+//    so a lane reads 4 (or 8) consecutive floats of one V row per k-step and
+//    ends with 16 consecutive dims per 4 dim blocks for the output.
+// Masking, the order of the workgroups, the lazy rescale and the vector-ALU
+// P.V for a tile with a non-finite value and masked pairs are the f16
+// kernel's.
+template <nfhip::AttnMode MODE, int DD>
+__global__ __launch_bounds__(256, 2) void prefill_f32_mfma_kernel(Params p) {
+  static_assert(MODE != nfhip::AttnMode::Paged, "rows of a KV head must be contiguous in position");
+  static_assert(DD == 64 || DD == 128, "head_dim 64 or 128");
+  constexpr int TK = 32;              // keys per tile
+  constexpr int DP = DD + 4;          // padded LDS row (floats)
+  constexpr int DG = DD / 4;          // dims per lane group in the scores
+  constexpr int DB = DD / 16;         // dim blocks of the output
+  constexpr int NCH = TK * DD / 4 / 256;  // 16-byte chunks of K (and of V) per thread and tile
+  __shared__ __attribute__((aligned(16))) float Ks[TK * DP];
+  __shared__ __attribute__((aligned(16))) float Vs[TK * DP];
+  __shared__ __attribute__((aligned(16))) float ps[4][TK][16];
+  __shared__ int tile_bad[2];
+  const uint32_t S = p.seq_len;
+  uint32_t h, qblk;
+  prefill_block(p, h, qblk);
+  const uint32_t kvh = (uint32_t)((uint64_t)h * p.n_kv / p.n_heads);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const uint32_t q0 = qblk * 64;
+  const uint32_t q1 = q0 + 64 < S ? q0 + 64 : S;
+  const float* Q = static_cast<const float*>(p.q);
+  const float* Kh = static_cast<const float*>(p.k) + kv_row<MODE>(p, kvh, 0);
+  const float* Vh = static_cast<const float*>(p.v) + kv_row<MODE>(p, kvh, 0);
+  auto lo_of = [&](uint32_t pos) -> uint32_t {
+    if constexpr (MODE == nfhip::AttnMode::Cached)
+      if (p.window > 0 && pos >= p.window) return pos - p.window + 1;
+    return 0u;
+  };
+  const uint32_t lo_blk = lo_of(q0), hi_blk = q1 - 1;
+  const uint32_t lo_last = lo_of(hi_blk);
+  const uint32_t qw0 = q0 + 16 * w;
+  const uint32_t qpos = qw0 + n;
+  const bool qok = qpos < q1;
+  const uint32_t qlo = lo_of(qpos);
+  // B operand of the scores: dims DG g .. DG g + DG - 1 of this lane's query
+  float qb[DG];
+  {
+    const float* qr = Q + q_row<MODE>(p, qok ? qpos : q0, h) + DG * g;
+#pragma unroll
+    for (int c = 0; c < DG / 4; ++c) {
+      const float4v x = *reinterpret_cast<const float4v*>(qr + 4 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qb[4 * c + e] = qok ? x[e] : 0.f;
+    }
+  }
+  const uint32_t wq_last = qw0 + 15 < q1 ? qw0 + 15 : q1 - 1;
+  const bool wave_live = qw0 < q1;
+  const uint32_t wlo_last = lo_of(wq_last);
+
+  float4v ot[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b) ot[b] = float4v{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  const float sl2 = p.scale * 1.44269504088896341f;
+
+  // tile loads: chunk u of a thread is row (tid + 256u) / (DD/4), 16-byte
+  // chunk (tid + 256u) % (DD/4) (coalesced); in the last tile, rows past the
+  // block's last query read that query's row and are zeroed when staged
+  float4v kr[NCH], vr[NCH];
+  auto fetch = [&](int64_t t0) {
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+      const int i = tid + 256 * u;
+      const int64_t row = t0 + i / (DD / 4) <= (int64_t)hi_blk ? t0 + i / (DD / 4) : (int64_t)hi_blk;
+      kr[u] = *reinterpret_cast<const float4v*>(Kh + (uint64_t)row * DD + 4 * (i % (DD / 4)));
+      vr[u] = *reinterpret_cast<const float4v*>(Vh + (uint64_t)row * DD + 4 * (i % (DD / 4)));
+    }
+  };
+  auto stage = [&](int64_t t0, int par, bool checked) {
+    bool bad = false;
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+      const int i = tid + 256 * u;
+      const int r = i / (DD / 4), c = i % (DD / 4);
+      float4v v = vr[u];
+      if (checked) {
+        const bool vin = t0 + r <= (int64_t)hi_blk;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = vin ? v[e] : 0.f;
+          bad = bad || !__builtin_isfinite(v[e]);
+        }
+      }
+      *reinterpret_cast<float4v*>(&Ks[r * DP + 4 * c]) = kr[u];
+      *reinterpret_cast<float4v*>(&Vs[r * DP + 4 * c]) = v;
+    }
+    if (bad) tile_bad[par] = 1;
+  };
+
+  auto swap_pair = [](float v, auto row32) {
+    float a = v, b = v;
+    if constexpr (decltype(row32)::value)
+      asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    else
+      asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return float2s{a, b};
+  };
+  auto col_max = [&](float v) {
+    float2s r = swap_pair(v, std::false_type{});
+    r = swap_pair(fmaxf(r[0], r[1]), std::true_type{});
+    return fmaxf(r[0], r[1]);
+  };
+  auto col_sum = [&](float v) {
+    float2s r = swap_pair(v, std::false_type{});
+    r = swap_pair(r[0] + r[1], std::true_type{});
+    return r[0] + r[1];
+  };
+
+  auto tile = [&](int64_t t0, int par, auto interior_c) {
+    constexpr bool INTERIOR = decltype(interior_c)::value;
+    // scores S^T: lane holds keys t0 + 16j + 4g + i for query qpos
+    float4v sc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float a[DG];
+      const float* kr0 = &Ks[(16 * j + n) * DP + DG * g];
+#pragma unroll
+      for (int c = 0; c < DG / 4; ++c) {
+        const float4v x = *reinterpret_cast<const float4v*>(kr0 + 4 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[4 * c + e] = x[e];
+      }
+      sc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < DG; ++st) sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], qb[st], sc[j], 0, 0, 0);
+    }
+    float sr[2][4];
+    float rmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (INTERIOR) {
+          sr[j][i] = sc[j][i];
+        } else {
+          const int64_t kt = t0 + 16 * j + 4 * g + i;
+          const bool in = qok && kt >= (int64_t)qlo && kt <= (int64_t)qpos;
+          sr[j][i] = in ? sc[j][i] : -INFINITY;
+        }
+        rmax = fmaxf(rmax, sr[j][i]);
+      }
+    rmax = col_max(rmax);
+    const float tmax = rmax * sl2;
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + kLazyLog2) != 0) {  // uniform
+      const float m_new = fmaxf(m_run, tmax);
+      const float corr = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= corr;
+#pragma unroll
+      for (int b = 0; b < DB; ++b) ot[b] *= corr;
+      m_run = m_new;
+    }
+    float pv[2][4];
+    float psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sr[j][i], sl2, -m_run));
+        if constexpr (INTERIOR) pv[j][i] = e;
+        else pv[j][i] = sr[j][i] == -INFINITY ? 0.f : e;
+        psum += pv[j][i];
+      }
+    l_run += col_sum(psum);
+    if (INTERIOR || !tile_bad[par]) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        // V rows of the 4 k-steps (keys 16j + 4g + i), dims 4n' .. 4n' + 3
+        // (+ 64) of lane row n' = n
+        float4v va[4][DB / 4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int hh = 0; hh < DB / 4; ++hh)
+            va[i][hh] = *reinterpret_cast<const float4v*>(&Vs[(16 * j + 4 * g + i) * DP + 4 * n + 64 * hh]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int b = 0; b < DB; ++b)
+            ot[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[i][b / 4][b % 4], pv[j][i], ot[b], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ps[w][16 * j + 4 * g + i][n] = pv[j][i];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      for (int k = 0; k < TK; ++k) {
+        const int64_t kt = t0 + k;
+        if (!(qok && kt >= (int64_t)qlo && kt <= (int64_t)qpos)) continue;
+        const float pk = ps[w][k][n];
+        // lane (n, g) holds O^T rows 4g + r of block b: dim 4(4g + r) + b % 4 + 64 (b / 4)
+#pragma unroll
+        for (int b = 0; b < DB; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ot[b][r] += pk * Vs[k * DP + 4 * (4 * g + r) + b % 4 + 64 * (b / 4)];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  };
+
+  if (tid == 0) tile_bad[0] = tile_bad[1] = 0;
+  fetch(lo_blk);
+  int par = 0;
+  for (int64_t t0 = lo_blk; t0 <= (int64_t)hi_blk; t0 += TK, par ^= 1) {
+    __syncthreads();  // the previous tile's readers are done
+    if (tid == 0) tile_bad[par ^ 1] = 0;
+    // every key of the tile in every query's range: no zeroing, no check
+    stage(t0, par, !(t0 + TK - 1 <= (int64_t)q0 && t0 >= (int64_t)lo_last));
+    __syncthreads();
+    if (t0 + TK <= (int64_t)hi_blk) fetch(t0 + TK);
+    if (!wave_live || t0 > (int64_t)wq_last) continue;  // no key of this tile for the wave (uniform)
+    if (t0 + TK - 1 <= (int64_t)qw0 && t0 >= (int64_t)wlo_last) tile(t0, par, std::true_type{});
+    else tile(t0, par, std::false_type{});
+  }
+
+  if (qok) {
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    float* O = static_cast<float*>(p.out) + q_row<MODE>(p, qpos, h);
+    // lane (n, g): dims 16g + 4r + (b % 4) + 64 (b / 4) of block b, row r
+#pragma unroll
+    for (int hh = 0; hh < DB / 4; ++hh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float4v v = {ot[4 * hh][r] * inv, ot[4 * hh + 1][r] * inv, ot[4 * hh + 2][r] * inv,
+                           ot[4 * hh + 3][r] * inv};
+        *reinterpret_cast<float4v*>(O + 64 * hh + 16 * g + 4 * r) = v;
+      }
+  }
+}
+
 // Append K_new / V_new rows to the caches: prefill rows 0..seq_len-1, decode
 // row `step`.  Cached: K_new [tokens, n_kv, dim]; Gqa: [n_kv, tokens, dim].
 template <typename T, bool HEAD_MAJOR>
@@ -1453,6 +1706,17 @@ hipError_t run(const Params& p, uint32_t nq, float* ws, size_t ws_floats, hipStr
       const dim3 grid((nq + 63) / 64, p.n_heads);
       if (p.dim == 128) prefill_mfma_kernel<MODE, 128><<<grid, 256, 0, s>>>(p);
       else prefill_mfma_kernel<MODE, 64><<<grid, 256, 0, s>>>(p);
+      return hipGetLastError();
+    }
+  }
+  if constexpr (MODE != nfhip::AttnMode::Paged && std::is_same<T, float>::value) {
+    // f32, head_dim 64 / 128, 16-byte aligned rows: flash attention on fp32 MFMA
+    const bool al16 = ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k) |
+                        reinterpret_cast<uintptr_t>(p.v) | reinterpret_cast<uintptr_t>(p.out)) & 15) == 0;
+    if (al16 && (p.dim == 64 || p.dim == 128)) {
+      const dim3 grid((nq + 63) / 64, p.n_heads);
+      if (p.dim == 128) prefill_f32_mfma_kernel<MODE, 128><<<grid, 256, 0, s>>>(p);
+      else prefill_f32_mfma_kernel<MODE, 64><<<grid, 256, 0, s>>>(p);
       return hipGetLastError();
     }
   }

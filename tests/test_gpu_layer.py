@@ -321,6 +321,10 @@ GPU_ATTN = [
     ("flash_attention_cached", True, dict(H=4, KV=4, D=128, S=130, step=0, max_seq=160, window=40)),
     ("flash_attention_gqa", True, dict(H=8, KV=2, D=64, S=257, step=0, max_seq=300)),
     ("flash_attention_cached", True, dict(H=32, KV=8, D=128, S=200, step=0, max_seq=256)),
+    # f32 prefill on fp32 MFMA (head_dim 64 / 128; the cases above with those
+    # head_dims take it too): 32 heads over 8 KV heads, ragged last blocks
+    ("flash_attention_cached", False, dict(H=32, KV=8, D=128, S=200, step=0, max_seq=256)),
+    ("flash_attention_gqa", False, dict(H=8, KV=2, D=128, S=97, step=0, max_seq=128)),
     # f16 decode with the scores on MFMA (head_dim 64 / 128): partial last
     # tiles, groups of 1 / 3 / 4 / 8 query heads, a sliding window, a 6-key
     # cache (the paged op is f32-only, as in the reference)
