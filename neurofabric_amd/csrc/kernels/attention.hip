@@ -1342,21 +1342,24 @@ __global__ __launch_bounds__(64) void decode_split_kernel(Params p, uint32_t key
   }
 }
 
-// ---- f16 decode with the scores on MFMA ----------------------------------------
+// ---- decode with the scores on MFMA --------------------------------------------
 //
-// One query token, f16 K/V caches, head_dim DD = 64 or 128, G <= 8 query heads
-// per KV head, 16-byte aligned rows.  A workgroup of NW waves covers one KV
-// head and NW x TK keys, one TK-key tile per wave:
-//  * scores: S[key][head] = K[key][dims] . Q[head][dims] on
-//    v_mfma_f32_16x16x32_f16 (A = 16 key rows, B = the query heads as the 16
-//    columns, exact f16 products, fp32 sums); each lane loads its A pieces
-//    (8 dims of one key row) with 16-byte loads straight into registers, the
-//    query operand is loaded once;
+// One query token, f16 or f32 K/V caches, head_dim DD = 64 or 128, G <= 8
+// query heads per KV head, 16-byte aligned rows.  A workgroup of NW waves
+// covers one KV head and NW x TK keys, one TK-key tile per wave:
+//  * scores: S[key][head] = K[key][dims] . Q[head][dims] with A = 16 key rows
+//    and B = the query heads as the 16 columns: f16 on
+//    v_mfma_f32_16x16x32_f16 (exact f16 products, fp32 sums; a lane's A
+//    piece is 8 dims of one key row), f32 on v_mfma_f32_16x16x4_f32 (fp32
+//    products and sums; k-step s of lane group kg takes dim DD/4 kg + s, so
+//    a lane's pieces are DD/4 consecutive floats of its key row); each lane
+//    loads its pieces with 16-byte loads straight into registers, the query
+//    operand is loaded once;
 //  * softmax in base 2 on the scores (scaled by scale * log2 e), per head
 //    across the lanes that hold its 64 keys;
-//  * P.V on the vector ALU: lane (kq, dc) holds 8 dims (chunk dc) of the
-//    value rows RPI*i + kq, loaded with 16-byte loads together with the keys,
-//    and takes the tile's weights from LDS;
+//  * P.V on the vector ALU: lane (kq, dc) holds the 16-byte chunk dc (8 f16
+//    or 4 f32 dims) of the value rows RPI*i + kq, loaded with 16-byte loads
+//    together with the keys, and takes the tile's weights from LDS;
 //  * the NW waves' (m, l, acc) are merged in LDS and written as the split's
 //    partial (m in natural-log units); decode_combine_kernel adds the
 //    splits.
@@ -1367,16 +1370,21 @@ __global__ __launch_bounds__(64) void decode_split_kernel(Params p, uint32_t key
 // (score -inf, value 0), so no load is predicated and unused memory never
 // reaches the sums.  Row `step` is read from K_new / V_new when the append is
 // fused; the workgroup whose range holds it writes it into the cache.
-template <nfhip::AttnMode MODE, int DD, int G, int TK, int NW>
+template <typename T, nfhip::AttnMode MODE, int DD, int G, int TK, int NW>
 __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t keys_per_split, uint32_t lo,
                                                               float* __restrict__ part) {
-  constexpr int KSTEP = DD / 32;   // MFMA k-steps per 16-key block
+  constexpr bool F16 = std::is_same<T, half_t>::value;
+  static_assert(F16 || std::is_same<T, float>::value, "f16 or f32 caches");
+  constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  constexpr int KSTEP = F16 ? DD / 32 : DD / 4;  // MFMA k-steps per 16-key block
   constexpr int KB = TK / 16;      // 16-key blocks per tile
-  constexpr int CPR = DD / 8;      // 16-byte chunks per f16 row
+  constexpr int CPR = DD / EPC;    // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;    // value rows per load instruction
   constexpr int NV = TK / RPI;     // value loads per lane per tile
   static_assert(TK % RPI == 0 && TK % 16 == 0, "tile");
-  typedef half_t T;
+  typedef T chunk_t __attribute__((ext_vector_type(EPC)));
+  // a lane's score operand per k-step: 8 f16 dims, or one f32 dim
+  typedef typename std::conditional<F16, half8, float>::type op_t;
   constexpr int NT = NW * 64;
   __shared__ __attribute__((aligned(16))) float ps[NW][TK][G];  // tile weights [wave][key][head]
   __shared__ float wm[NW][G], wl[NW][G];
@@ -1421,28 +1429,49 @@ __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t
 
   // ---- loads: query operand, key operands, value chunks -------------------------
   const int n = lane & 15, kg = lane >> 4;  // MFMA column (head) / k-group of the lane
-  half8 qb[KSTEP];
+  // dims of k-step s in lane group kg: f16 32 s + 8 kg .. + 7, f32 DD/4 kg + s
+  op_t qb[KSTEP];
+  {
+    const T* qr = Q + q_row<MODE>(p, 0, h0 + (uint32_t)(n < ng ? n : ng - 1));
+    if constexpr (F16) {
 #pragma unroll
-  for (int s = 0; s < KSTEP; ++s) {
-    const T* qr = Q + q_row<MODE>(p, 0, h0 + (uint32_t)(n < ng ? n : ng - 1)) + 32 * s + 8 * kg;
-    qb[s] = *reinterpret_cast<const half8*>(qr);
-    if (n >= ng) qb[s] = half8{};
+      for (int s = 0; s < KSTEP; ++s) {
+        qb[s] = *reinterpret_cast<const half8*>(qr + 32 * s + 8 * kg);
+        if (n >= ng) qb[s] = half8{};
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < KSTEP / 4; ++c) {
+        const float4v x = *reinterpret_cast<const float4v*>(qr + KSTEP * kg + 4 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qb[4 * c + e] = n < ng ? x[e] : 0.f;
+      }
+    }
   }
-  half8 ka[KB][KSTEP];
+  op_t ka[KB][KSTEP];
 #pragma unroll
   for (int j = 0; j < KB; ++j) {
     bool ok;
     const T* kr = key_ptr(K, p.k_new, 16 * j + n, ok);
+    if constexpr (F16) {
 #pragma unroll
-    for (int s = 0; s < KSTEP; ++s) ka[j][s] = *reinterpret_cast<const half8*>(kr + 32 * s + 8 * kg);
+      for (int s = 0; s < KSTEP; ++s) ka[j][s] = *reinterpret_cast<const half8*>(kr + 32 * s + 8 * kg);
+    } else {
+#pragma unroll
+      for (int c = 0; c < KSTEP / 4; ++c) {
+        const float4v x = *reinterpret_cast<const float4v*>(kr + KSTEP * kg + 4 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ka[j][4 * c + e] = x[e];
+      }
+    }
   }
   const int kq = lane / CPR, dc = lane % CPR;
-  half8 vx[NV];
+  chunk_t vx[NV];
   bool vok[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const T* vr = key_ptr(V, p.v_new, RPI * i + kq, vok[i]);
-    vx[i] = *reinterpret_cast<const half8*>(vr + 8 * dc);
+    vx[i] = *reinterpret_cast<const chunk_t*>(vr + EPC * dc);
   }
 
   // ---- scores and the tile softmax (lane: keys 16j + 4kg + i, head n) -----------
@@ -1451,7 +1480,10 @@ __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t
   for (int j = 0; j < KB; ++j) {
     sc[j] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < KSTEP; ++s) sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[j][s], qb[s], sc[j], 0, 0, 0);
+    for (int s = 0; s < KSTEP; ++s) {
+      if constexpr (F16) sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[j][s], qb[s], sc[j], 0, 0, 0);
+      else sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[j][s], qb[s], sc[j], 0, 0, 0);
+    }
   }
   const float sl2 = p.scale * 1.44269504088896341f;
   float sv[KB][4];
@@ -1486,12 +1518,12 @@ __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t
   }
   __syncthreads();
 
-  // ---- P.V (lane: dims 8dc..8dc+7 of rows RPI*i + kq) ----------------------------
-  float acc[G][8];
+  // ---- P.V (lane: dims EPC dc .. EPC dc + EPC - 1 of rows RPI*i + kq) ------------
+  float acc[G][EPC];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    for (int e = 0; e < EPC; ++e) acc[g][e] = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int r = RPI * i + kq;
@@ -1507,7 +1539,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t
       for (int g = 0; g < G; ++g) pr[g] = ps[w][r][g];
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < EPC; ++e) {
       const float x = vok[i] ? (float)vx[i][e] : 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) acc[g][e] = __builtin_fmaf(pr[g], x, acc[g][e]);
@@ -1519,13 +1551,14 @@ __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
+      for (int e = 0; e < EPC; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
   if (kq == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float4v* dst = reinterpret_cast<float4v*>(&wacc[w][g][8 * dc]);
-      dst[0] = float4v{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
-      dst[1] = float4v{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+      float4v* dst = reinterpret_cast<float4v*>(&wacc[w][g][EPC * dc]);
+#pragma unroll
+      for (int c = 0; c < EPC / 4; ++c)
+        dst[c] = float4v{acc[g][4 * c], acc[g][4 * c + 1], acc[g][4 * c + 2], acc[g][4 * c + 3]};
     }
   }
   __syncthreads();
@@ -1630,9 +1663,9 @@ hipError_t run_decode_split(const Params& p, float* ws, size_t ws_floats, hipStr
   const uint64_t n_splits = (n_keys + kps - 1) / kps;
   if (n_splits > (uint64_t)kMaxSplits || n_splits * H * (p.dim + 2) > ws_floats) return hipErrorNotSupported;
   const int G = gmax == 1 ? 1 : gmax == 2 ? 2 : gmax <= 4 ? 4 : 8;
-  // f16 caches with head_dim 64 / 128 and 16-byte aligned rows: scores on MFMA,
-  // 4 waves per workgroup, each over its own range of tk keys
-  if constexpr (std::is_same<T, half_t>::value) {
+  // head_dim 64 / 128 and 16-byte aligned rows: scores on MFMA, 4 waves per
+  // workgroup, each over its own range of tk keys
+  {
     const bool al = ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k) |
                       reinterpret_cast<uintptr_t>(p.v) |
                       (p.fused_append ? reinterpret_cast<uintptr_t>(p.k_new) | reinterpret_cast<uintptr_t>(p.v_new)
@@ -1647,8 +1680,8 @@ hipError_t run_decode_split(const Params& p, float* ws, size_t ws_floats, hipStr
         const dim3 g2((unsigned)ns, KV);
 #define NF_DECODE_MFMA(DDD, GG)                                                                      \
   if (p.dim == DDD && G == GG) {                                                                     \
-    if (tk == 32) decode_mfma_kernel<MODE, DDD, GG, 32, 4><<<g2, 256, 0, s>>>(p, 4 * tk, lo, ws);     \
-    else decode_mfma_kernel<MODE, DDD, GG, 64, 4><<<g2, 256, 0, s>>>(p, 4 * tk, lo, ws);              \
+    if (tk == 32) decode_mfma_kernel<T, MODE, DDD, GG, 32, 4><<<g2, 256, 0, s>>>(p, 4 * tk, lo, ws);  \
+    else decode_mfma_kernel<T, MODE, DDD, GG, 64, 4><<<g2, 256, 0, s>>>(p, 4 * tk, lo, ws);           \
   }
         NF_DECODE_MFMA(64, 1) NF_DECODE_MFMA(64, 2) NF_DECODE_MFMA(64, 4) NF_DECODE_MFMA(64, 8)
         NF_DECODE_MFMA(128, 1) NF_DECODE_MFMA(128, 2) NF_DECODE_MFMA(128, 4) NF_DECODE_MFMA(128, 8)
