@@ -190,27 +190,27 @@ __global__ __launch_bounds__(256, 2) void dense_f32_mfma_kernel(const AT* __rest
   }
   // Split K: partial tile of this workgroup as 16-B groups (values 4q..4q+3
   // of tile (i, j) of thread tid at float4 index ((i*TN + j)*4 + q)*256 +
-  // tid); the last arrival (agent-scope acquire/release counter) loads every
-  // partial of a 32x32 tile before adding them in order kg = 0..KG-1, stores
-  // C and resets the counter.
+  // tid, through sc1 accesses: CoherentTile); the last arrival at the
+  // tile counter loads every partial of a 32x32 tile before adding them in
+  // order kg = 0..KG-1, stores C and resets the counter.
   const int tile = blockIdx.x;
-  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
+  const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4),
+                             (uint32_t)(KG * BM * BN * 4));
   {
-    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          mine[((i * TN + j) * 4 + q) * 256 + tid] =
-              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          tile_ws.store((uint32_t)kg * (BM * BN / 4) + ((i * TN + j) * 4 + q) * 256 + tid,
+                        float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ uint32_t is_last;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == (uint32_t)(KG - 1);
   }
   __syncthreads();
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256, 2) void dense_f32_mfma_kernel(const AT* __rest
       for (int g = 0; g < kMaxKG; ++g)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (g < KG && g != kg) part[g][q] = tile_ws[(size_t)g * (BM * BN / 4) + ((i * TN + j) * 4 + q) * 256 + tid];
+          if (g < KG && g != kg) part[g][q] = tile_ws.load((uint32_t)g * (BM * BN / 4) + ((i * TN + j) * 4 + q) * 256 + tid);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float4v sum = {0.f, 0.f, 0.f, 0.f};

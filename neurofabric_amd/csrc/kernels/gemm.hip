@@ -333,8 +333,8 @@ __device__ __forceinline__ void xcd_tile(int bid, int mt, int nt, int& tm, int& 
 // thread keeps 4*TN*CH loads in flight: the gather costs about KG*TM/CH
 // memory round trips, not one per 16-byte group.
 template <int TM, int TN, int NT, int CH>
-__device__ __forceinline__ void splitk_gather(float16v (&acc)[TM][TN], const float4v* __restrict__ tile_ws,
-                                              size_t stride, int KG, int tid) {
+__device__ __forceinline__ void splitk_gather(float16v (&acc)[TM][TN], const CoherentTile& tile_ws,
+                                              uint32_t stride, int KG, int tid) {
   static_assert(TM % CH == 0, "chunks of whole tile rows");
 #pragma unroll
   for (int i0 = 0; i0 < TM; i0 += CH) {
@@ -346,7 +346,7 @@ __device__ __forceinline__ void splitk_gather(float16v (&acc)[TM][TN], const flo
         for (int j = 0; j < TN; ++j)
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            p[ii][j][q] = tile_ws[(size_t)g * stride + (((i0 + ii) * TN + j) * 4 + q) * NT + tid];
+            p[ii][j][q] = tile_ws.load((uint32_t)g * stride + (((i0 + ii) * TN + j) * 4 + q) * NT + tid);
 #pragma unroll
       for (int ii = 0; ii < CH; ++ii)
 #pragma unroll
@@ -586,27 +586,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(const half
   // Split K across workgroups: each parks its fp32 accumulators in the
   // workspace as 16-byte groups (values 4q..4q+3 of tile (i, j) of thread
   // tid at float4 index ((i*TN + j)*4 + q)*NT + tid, coalesced per wave);
-  // the last workgroup of the tile to arrive (per-tile counter, agent-scope
-  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1
-  // (splitk_gather), stores C and resets the counter.
+  // the last workgroup of the tile to arrive (per-tile counter; the partials
+  // move through sc1 accesses, CoherentTile) adds the KG partial tiles in
+  // order kg = 0..KG-1 (splitk_gather), stores C and resets the counter.
   const int tile = blockIdx.x;
-  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
+  const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4),
+                             (uint32_t)(KG * BM * BN * 4));
   {
-    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          mine[((i * TN + j) * 4 + q) * NT + tid] =
-              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          tile_ws.store((uint32_t)kg * (BM * BN / 4) + ((i * TN + j) * 4 + q) * NT + tid,
+                        float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ uint32_t is_last;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == (uint32_t)(KG - 1);
   }
   __syncthreads();
@@ -925,27 +925,27 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_wq_kernel(const half_t* __res
   // Split K across workgroups: each parks its fp32 accumulators in the
   // workspace as 16-byte groups (values 4q..4q+3 of tile (i, j) of thread tid
   // at float4 index ((i*TN + j)*4 + q)*NT + tid, coalesced per wave); the
-  // last workgroup of the tile to arrive (per-tile counter, agent-scope
-  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1
-  // (splitk_gather), stores C and resets the counter.
+  // last workgroup of the tile to arrive (per-tile counter; the partials
+  // move through sc1 accesses, CoherentTile) adds the KG partial tiles in
+  // order kg = 0..KG-1 (splitk_gather), stores C and resets the counter.
   const int tile = blockIdx.x;
-  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
+  const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4),
+                             (uint32_t)(KG * BM * BN * 4));
   {
-    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          mine[((i * TN + j) * 4 + q) * NT + tid] =
-              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          tile_ws.store((uint32_t)kg * (BM * BN / 4) + ((i * TN + j) * 4 + q) * NT + tid,
+                        float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ uint32_t is_last;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == (uint32_t)(KG - 1);
   }
   __syncthreads();
@@ -1245,23 +1245,23 @@ __global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __r
   // workgroup of the tile adds the KG partial tiles in order (the fix-up of
   // gemm_wq_kernel, with group 0's 256 threads).
   const int tile = blockIdx.x;
-  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
+  const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4),
+                             (uint32_t)(KG * BM * BN * 4));
   if (grp == 0) {
-    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          mine[((i * TN + j) * 4 + q) * NT0 + tid] =
-              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          tile_ws.store((uint32_t)kg * (BM * BN / 4) + ((i * TN + j) * 4 + q) * NT0 + tid,
+                        float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ uint32_t is_last;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == (uint32_t)(KG - 1);
   }
   __syncthreads();
@@ -1776,23 +1776,23 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_f32a_kernel(const float* __re
   }
   // K split across workgroups: the fix-up of gemm_wq_kernel.
   const int tile = blockIdx.x;
-  float4v* tile_ws = reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4);
+  const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)tile * KG * (BM * BN / 4),
+                             (uint32_t)(KG * BM * BN * 4));
   {
-    float4v* mine = tile_ws + (size_t)kg * (BM * BN / 4);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          mine[((i * TN + j) * 4 + q) * NT + tid] =
-              float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          tile_ws.store((uint32_t)kg * (BM * BN / 4) + ((i * TN + j) * 4 + q) * NT + tid,
+                        float4v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ uint32_t is_last;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == (uint32_t)(KG - 1);
   }
   __syncthreads();

@@ -468,24 +468,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     return;
   }
   // Split K across workgroups: each workgroup parks its tile sum in the
-  // workspace; the last one to arrive (per-tile counter, agent-scope
-  // acquire/release) adds the KG partial tiles in order kg = 0..KG-1 and
-  // stores C, then resets the counter for the next launch.
+  // workspace; the last one to arrive (per-tile counter) adds the KG partial
+  // tiles in order kg = 0..KG-1 and stores C, then resets the counter for
+  // the next launch.
   float* mine = ws_part + ((size_t)blockIdx.x * KG + kg) * (NV * 64);
   for (int v = tid; v < NV * 64; v += blockDim.x) {
     float sum = 0.f;
     for (int w = 0; w < KS; ++w) sum += parts[(size_t)w * AREA + v];
-    mine[v] = sum;
+    // agent-scope atomic store: an sc1 store, written through to the level
+    // all XCDs share (the exchange protocol of CoherentTile)
+    __hip_atomic_store(&mine[v], sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // Every wave waits for its stores to complete (the workgroup barrier alone
-  // does not); one thread then publishes them at agent scope (release) with
-  // the counter update, and in the last workgroup acquires the other
-  // workgroups' tiles for the whole workgroup.
+  // does not); one thread then bumps the tile counter (relaxed: the partials
+  // never sit in an XCD's L2, so no writeback or invalidate is needed), and
+  // the last workgroup reads them back with agent-scope atomic (sc1) loads.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ uint32_t is_last;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[blockIdx.x], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == (uint32_t)(KG - 1);
   }
   __syncthreads();
@@ -493,7 +495,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const float* tile = ws_part + (size_t)blockIdx.x * KG * (NV * 64);
   for (int v = tid; v < NV * 64; v += blockDim.x) {
     float sum = 0.f;
-    for (int g = 0; g < KG; ++g) sum += tile[(size_t)g * (NV * 64) + v];
+    for (int g = 0; g < KG; ++g)
+      sum += __hip_atomic_load(&tile[(size_t)g * (NV * 64) + v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     store(v, sum);
   }
   if (tid == 0) __hip_atomic_store(&ws_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -525,10 +528,20 @@ void skinny_split(long wgs, uint32_t K, const nfhip::Workspace& ws, int& ks, int
     const int v = e ? std::atoi(e) : 0;
     return v > 0 && v <= 64 ? v : 4;
   }();
+  static const int min_chunks = [] {
+    const char* e = std::getenv("NF_HIP_SKINNY_MIN_CHUNKS");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 && v <= 8 ? v : 2;
+  }();
+  static const int max_waves = [] {
+    const char* e = std::getenv("NF_HIP_SKINNY_MAX_WAVES");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 ? v : 2048;
+  }();
   ks = std::min(ks_max, wgs <= 256 ? 8 : 4);
   while (ks > 1 && NC < ks) ks >>= 1;
   kg = 1;
-  while (kg < kg_max && wgs * ks * kg * 2 <= 2048 && NC >= 2 * ks * kg && wgs <= (long)ws.cnt_len &&
+  while (kg < kg_max && wgs * ks * kg * 2 <= max_waves && NC >= min_chunks * ks * kg && wgs <= (long)ws.cnt_len &&
          (size_t)wgs * 2 * kg * NV * 64 <= ws.part_floats)
     kg *= 2;
 }

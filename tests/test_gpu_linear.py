@@ -192,6 +192,47 @@ def test_tiled_gemm_split_k(provider, oracle_mod, fmt, tile, shape):
         provider.set_tuning(old)
 
 
+@pytest.mark.parametrize("path,f16,shape", [("skinny", False, (16, 4096, 4096)), ("skinny", True, (8, 8192, 28672)),
+                                             ("tiled", True, (512, 4096, 4096)), ("tiled", False, (128, 4096, 4096))],
+                         ids=["skinny-f32", "skinny-f16", "tiled-f16", "tiled-f32"])
+def test_split_k_back_to_back(provider, oracle_mod, path, f16, shape):
+    """Split-K launches enqueued back to back with no synchronisation between
+    them: every launch parks its partial tiles in the same workspace slots
+    and reuses the same tile counters, so a partial read before the previous
+    launch's was replaced, or a counter not back at zero, shows as a wrong
+    output.  Six launches on distinct activations, each checked against the
+    oracle on a column window."""
+    M, N, K = shape
+    fmt = "q8_0"
+    W = syn.weights(fmt, N, K, seed=N + K)
+    dt = abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32
+    old = provider.get_tuning()
+    bufs = []
+    try:
+        _force_path(provider, path, f16)
+        w = provider.alloc_array(W, QDT[fmt])
+        bufs.append(w)
+        runs = []
+        for rep in range(6):
+            A = syn.activations(M, K, seed=100 + rep, dtype=np.float16 if f16 else np.float32)
+            a = provider.alloc_array(A, dt)
+            c = provider.alloc(dt, M * N * (2 if f16 else 4))
+            bufs += [a, c]
+            provider.dispatch(f"dequant_{fmt}_linear" + ("_f16" if f16 else ""), [a, w], [c], M, N, K)
+            runs.append((A, c))
+        provider.synchronize()
+        cols = (N - 192, N)
+        for rep, (A, c) in enumerate(runs):
+            got = c.download(np.float16 if f16 else np.float32).reshape(M, N)[:, cols[0]:cols[1]]
+            ref = oracle_mod.fused(A, W, fmt, M, N, K, f16=f16, cols=cols, threads=8)
+            ref = (ref.view(np.float16) if f16 else ref)[:, cols[0]:cols[1]]
+            assert_close(got.astype(np.float32), ref.astype(np.float32), what=f"{path} {M}x{N}x{K} launch {rep}")
+    finally:
+        for b in bufs:
+            b.release()
+        provider.set_tuning(old)
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("tile", [-1, 0, 1, 2, 5, 7, 8, 9, 10],
                          ids=lambda t: "regdq" if t < 0 else f"lds{t}" if t < 7 else f"wq{t - 6}")
