@@ -146,9 +146,10 @@ NF_API uint32_t nf_hip_get_skinny_f16_max_k(void);
 /* Kernel of the fused f16 GEMM path (M above the small-batch range): -1
  * (default) = the kernels that dequantize weights in registers, picked by M
  * from measurement on MI355X (two waves per SIMD with 32-row waves up to
- * M = 32 and 64-row waves up to M = 64; 128-row waves for Q4_0 from
- * M = 1024; one wave per SIMD otherwise; the two-wave kernels need
- * K % 128 == 0); 0..6 = the kernel that dequantizes weight tiles into LDS,
+ * M = 32 and 64-row waves up to M = 64 or while ceil(M/64) x ceil(N/256) is
+ * at most 80 (Q4_0) / 64 (Q8_0) with K <= 16384; 128-row waves for the other
+ * Q4_0 batches;
+ * one wave per SIMD otherwise; the two-wave kernels need K % 128 == 0); 0..6 = the kernel that dequantizes weight tiles into LDS,
  * tile shape 256x256, 256x128, 128x128, 256x128 with 4 waves, 256x128 with
  * 4 waves and 3 stages, 128x128 with 3 stages, 128x256; 7 = the
  * register-dequantizing kernel with one wave per SIMD for every shape;

@@ -1901,9 +1901,17 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
     //     TM = 1): 71 against 96-102 us at 28672x8192 / 8192x28672 M = 32;
     //   * M <= 64: the same with 64-row waves (TM = 2): 81 / 84 against
     //     102 / 110 us at M = 64;
-    //   * Q4_0 with M >= 1024: 128-row waves (TM = 4): 816 / 747 / 859
-    //     against 785 / 735 / 804 TFLOP/s on the three Llama-2-7B
-    //     projection shapes at M = 2048;
+    //   * M > 64 with few 64-row tiles (ceil(M/64) x ceil(N/256) <= 80 for
+    //     Q4_0, <= 64 for Q8_0) and K <= 16384: 64-row waves again, which
+    //     spread a short batch over more workgroups (4096x4096 Q4_0 M = 128:
+    //     24.6 against 38.1 us, 4096x11008 M = 256: 45.9 against 62.6; Q8_0
+    //     4096x4096 M = 128: 31.2 against 41.5; not at K = 28672, where
+    //     8192x28672 M = 128 took 122.0 against 104.1 us with 128-row waves);
+    //   * other Q4_0 batches: 128-row waves (TM = 4): at M = 2048 816 / 747
+    //     / 859 against 785 / 735 / 804 TFLOP/s on the three Llama-2-7B
+    //     projection shapes, at M = 512 41.9 / 77.4 / 69.9 against 45.6 /
+    //     78.6 / 76.4 us (within 2 % either way on the 28672-row FFN
+    //     shapes);
     //   * otherwise one wave per SIMD (gemm_wq_kernel; also Q8_0 at larger
     //     M, where the two-wave kernel measured 5-12 % slower);
     // all of them need K % 128 == 0 but gemm_wq_kernel.  Tile 7 forces the
@@ -1912,13 +1920,14 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
     // shapes.
     const bool k128 = K % 128 == 0;
     const bool q4 = q == QFmt::Q4_0;
+    const long tiles64 = (long)((M + 63) / 64) * (long)((N + 255) / 256);
     if ((tile == 10 || (tile < 0 && M <= 32)) && k128)
       return q4 ? nfk::gemm_wq2_launch<nfk::Q4_0, 1, 4>(a, w, c, M, N, K, ws, s)
                 : nfk::gemm_wq2_launch<nfk::Q8_0, 1, 4>(a, w, c, M, N, K, ws, s);
-    if ((tile == 9 || (tile < 0 && M <= 64)) && k128)
+    if ((tile == 9 || (tile < 0 && (M <= 64 || (tiles64 <= (q4 ? 80 : 64) && K <= 16384)))) && k128)
       return q4 ? nfk::gemm_wq2_launch<nfk::Q4_0, 2, 4>(a, w, c, M, N, K, ws, s)
                 : nfk::gemm_wq2_launch<nfk::Q8_0, 2, 4>(a, w, c, M, N, K, ws, s);
-    if ((tile == 8 || (tile < 0 && M >= 1024)) && k128 && q4)
+    if ((tile == 8 || tile < 0) && k128 && q4)
       return nfk::gemm_wq2_launch<nfk::Q4_0, 4, 4>(a, w, c, M, N, K, ws, s);
     if (tile < 0 || tile > 6)
       return (q == QFmt::Q4_0) ? nfk::gemm_wq_launch<nfk::Q4_0, 4, 2, 4, 4>(a, w, c, M, N, K, ws, s)
