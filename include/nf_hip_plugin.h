@@ -154,7 +154,8 @@ NF_API uint32_t nf_hip_get_skinny_f16_max_k(void);
  * 4 waves and 3 stages, 128x128 with 3 stages, 128x256; 7 = the
  * register-dequantizing kernel with one wave per SIMD for every shape;
  * 8 / 9 / 10 = the two-wave kernel with 128 / 64 / 32-row waves wherever it
- * applies (K % 128 == 0; 8: Q4_0 only), else as 7.
+ * applies (K % 128 == 0; 8: Q4_0 only), else as 7.  With f32 activations
+ * (the bf16-piece kernel) 8 / 9 force its 128- / 64-row waves.
  * Other values mean -1.  Environment override NF_HIP_GEMM_TILE (the shape
  * name or number) is read at nf_plugin_register.  No counterpart in the
  * reference (its Metal provider has one fused GEMM kernel); this is

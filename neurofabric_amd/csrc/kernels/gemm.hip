@@ -1881,7 +1881,13 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
     const float* a = static_cast<const float*>(A);
     const uint8_t* w = static_cast<const uint8_t*>(W);
     float* c = static_cast<float*>(C);
-    if (M <= 64)
+    // 64-row waves up to M = 64, and while the batch makes few 64x256
+    // tiles (at most 32, or 64 with K <= 8192): measured on MI355X, Q4_0
+    // 4096x4096 M = 128 39.0 against 56.6 us with 128-row waves, 4096x14336
+    // M = 128 100.0 against 139.6; 128-row waves win from 86 tiles on
+    // (11008x4096 M = 65: 85.0 against 96.0).  Tile 9 / 8 force them.
+    const long tiles64 = (long)((M + 63) / 64) * (long)((N + 255) / 256);
+    if (tile == 9 || (tile != 8 && (M <= 64 || tiles64 <= 32 || (tiles64 <= 64 && K <= 8192))))
       return q == QFmt::Q4_0 ? nfk::gemm_f32a_launch<nfk::Q4_0, 2, 2, 4>(a, w, c, M, N, K, ws, s)
                              : nfk::gemm_f32a_launch<nfk::Q8_0, 2, 2, 4>(a, w, c, M, N, K, ws, s);
     return q == QFmt::Q4_0 ? nfk::gemm_f32a_launch<nfk::Q4_0, 4, 2, 4>(a, w, c, M, N, K, ws, s)
