@@ -477,7 +477,7 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
 // with the matrices transposed so that every operand comes out of registers
 // or LDS in the layout the next MFMA wants.  A workgroup takes 64 query
 // tokens of one head, 16 per wave; per 64-key tile of K and V (staged once
-// in LDS for the workgroup: K row-major, V transposed):
+// in LDS for the workgroup, both row-major):
 //  * S^T[key][query] = K[key][dims] . Q^T[dims][query] on
 //    v_mfma_f32_16x16x32_f16: A = 16 key rows from LDS, B = the wave's 16
 //    queries (held in registers for the whole kernel);
@@ -489,8 +489,8 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
 //  * O^T[dim][query] += V^T[dim][key] . P^T[key][query]: the softmax weights
 //    of S^T's output layout are the B operand as they are (in a fixed key
 //    order), each split into two f16 pieces (two MFMAs, so the products keep
-//    fp32-level accuracy); the A operand is two 8-byte reads of the
-//    transposed V tile; fp32 accumulation.
+//    fp32-level accuracy); the A operand is two transposing 8-byte LDS
+//    reads (ds_read_b64_tr_b16) of the row-major V tile; fp32 accumulation.
 // Masked scores are -inf by select.  A weight of 0 times a non-finite value
 // would still be NaN inside the MFMA, so a tile that holds a non-finite
 // value and a key outside some query's range (the diagonal and window-edge
@@ -509,10 +509,10 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
   static_assert(MODE != nfhip::AttnMode::Paged, "rows of a KV head must be contiguous in position");
   typedef half_t T;
   constexpr int KSTEP = DD / 32, CPR = DD / 8, DB = DD / 16;
-  constexpr int KP = DD + 8, VP = 64 + 8;  // padded LDS row lengths (halves)
+  constexpr int KP = DD + 8;               // padded LDS row length (halves), K and V
   constexpr int NL = 64 * CPR / 256;       // 16-byte K and V chunks per thread and tile
   __shared__ __attribute__((aligned(16))) T Ks[64 * KP];
-  __shared__ __attribute__((aligned(16))) T Vt[DD * VP];
+  __shared__ __attribute__((aligned(16))) T Vs[64 * KP];
   __shared__ __attribute__((aligned(16))) float ps[4][64][16];  // weights for the vector-ALU P.V
   __shared__ int tile_bad[2];  // per tile parity: the staged V holds a non-finite value
   const uint32_t S = p.seq_len;
@@ -558,36 +558,32 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = p.scale * 1.44269504088896341f;
 
-  // Tile loads into registers (next tile while this one computes): K chunk
-  // i = tid + 256u is row i / CPR, 16-byte chunk i % CPR (coalesced); V
-  // chunk u is row tid % 64, chunk tid / 64 + 4u (consecutive threads take
-  // consecutive rows, so the transposed LDS writes do not collide).  In the
-  // last tile, rows past the block's last query read that query's row (in
-  // bounds) and are zeroed when staged.
+  // Tile loads into registers (next tile while this one computes): chunk
+  // i = tid + 256u of K and of V is row i / CPR, 16-byte chunk i % CPR
+  // (coalesced), staged row-major in LDS.  In the last tile, rows past the
+  // block's last query read that query's row (in bounds) and are masked (K)
+  // or zeroed (V) when staged.
   half8 kr[NL], vr[NL];
-  const int vk = tid & 63;
   auto fetch = [&](int64_t t0) {
     if (t0 + 63 <= (int64_t)hi_blk) {  // uniform: the whole tile is in range
       const T* kt = Kh + (uint64_t)t0 * DD;
-      const T* vt = Vh + (uint64_t)(t0 + vk) * DD;
+      const T* vt = Vh + (uint64_t)t0 * DD;
 #pragma unroll
       for (int u = 0; u < NL; ++u) {
         const int i = tid + 256 * u;
         kr[u] = *reinterpret_cast<const half8*>(kt + (i / CPR) * DD + 8 * (i % CPR));
-        vr[u] = *reinterpret_cast<const half8*>(vt + 8 * ((tid >> 6) + 4 * u));
+        vr[u] = *reinterpret_cast<const half8*>(vt + (i / CPR) * DD + 8 * (i % CPR));
       }
     } else {
 #pragma unroll
       for (int u = 0; u < NL; ++u) {
         const int i = tid + 256 * u;
-        const int64_t kt = t0 + i / CPR <= (int64_t)hi_blk ? t0 + i / CPR : (int64_t)hi_blk;
-        kr[u] = *reinterpret_cast<const half8*>(Kh + (uint64_t)kt * DD + 8 * (i % CPR));
-        const int64_t vt = t0 + vk <= (int64_t)hi_blk ? t0 + vk : (int64_t)hi_blk;
-        vr[u] = *reinterpret_cast<const half8*>(Vh + (uint64_t)vt * DD + 8 * ((tid >> 6) + 4 * u));
+        const int64_t row = t0 + i / CPR <= (int64_t)hi_blk ? t0 + i / CPR : (int64_t)hi_blk;
+        kr[u] = *reinterpret_cast<const half8*>(Kh + (uint64_t)row * DD + 8 * (i % CPR));
+        vr[u] = *reinterpret_cast<const half8*>(Vh + (uint64_t)row * DD + 8 * (i % CPR));
       }
     }
   };
-  T* const vtw = &Vt[8 * (tid >> 6) * VP + vk];  // dim 8 (tid / 64 + 4u) + e of key vk
   auto stage_k = [&]() {
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
@@ -597,23 +593,37 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
   };
   auto stage_v = [&]() {
 #pragma unroll
-    for (int u = 0; u < NL; ++u)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vtw[(32 * u + e) * VP] = vr[u][e];
+    for (int u = 0; u < NL; ++u) {
+      const int i = tid + 256 * u;
+      *reinterpret_cast<half8*>(&Vs[(i / CPR) * KP + 8 * (i % CPR)]) = vr[u];
+    }
   };
   // rows past the range as zeros; a non-finite value marks the tile
   auto stage_v_checked = [&](int64_t t0, int par) {
     bool bad = false;
-    const bool vin = t0 + vk <= (int64_t)hi_blk;
 #pragma unroll
-    for (int u = 0; u < NL; ++u)
+    for (int u = 0; u < NL; ++u) {
+      const int i = tid + 256 * u;
+      half8 x = vr[u];
+      if (t0 + i / CPR > (int64_t)hi_blk) x = half8{};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const T x = vin ? vr[u][e] : (T)0.f;
-        bad = bad || !__builtin_isfinite((float)x);
-        vtw[(32 * u + e) * VP] = x;
-      }
+      for (int e = 0; e < 8; ++e) bad = bad || !__builtin_isfinite((float)x[e]);
+      *reinterpret_cast<half8*>(&Vs[(i / CPR) * KP + 8 * (i % CPR)]) = x;
+    }
     if (bad) tile_bad[par] = 1;
+  };
+  // The P.V A operand, V^T[dim][key], from the row-major tile with
+  // ds_read_b64_tr_b16: among each 16 lanes, lane i receives element
+  // i % 4 of the 8 bytes that lane 4e + i / 4 addressed, as its element e.
+  // Lane n (of lane group g) addresses key row 4g + n / 4 (+ the k-step's
+  // base) at dims 16b + 4 (n % 4) .. + 3, so lane n receives dim 16b + n of
+  // keys 4g .. 4g + 3: one half of the A piece (the other half is the keys
+  // 16 further on).
+  const T* const vtr = &Vs[(4 * g + n / 4) * KP + 4 * (n % 4)];
+  auto v_tr = [&](int key0, int dim0) {
+    typedef short short4v __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                         (__attribute__((address_space(3))) short4v*)(vtr + key0 * KP + dim0)));
   };
 
   // Sum / max over the 4 lanes of a query's column (lanes n, n + 16, n + 32,
@@ -725,9 +735,8 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
         half8 av[DB];
 #pragma unroll
         for (int b = 0; b < DB; ++b) {
-          const T* vrow = &Vt[(16 * b + n) * VP + 32 * c + 4 * g];
-          const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow);
-          const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + 16);
+          const uint2 lo4 = v_tr(32 * c, 16 * b);
+          const uint2 hi4 = v_tr(32 * c + 16, 16 * b);
           av[b] = __builtin_bit_cast(half8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
         }
         // each weight as two f16 pieces, hi (rounded toward zero) + lo (the
@@ -764,7 +773,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
 #pragma unroll
         for (int b = 0; b < DB; ++b)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) ot[b][i] += pk * (float)Vt[(16 * b + 4 * g + i) * VP + k];
+          for (int i = 0; i < 4; ++i) ot[b][i] += pk * (float)Vs[k * KP + 16 * b + 4 * g + i];
       }
       __builtin_amdgcn_wave_barrier();
     }
