@@ -126,7 +126,7 @@ NF_API void nf_hip_get_gemv_max_m(uint32_t *f32_path, uint32_t *f16_path);
  * activation stage (2 x K x element size, plus the f32 Q4_0 path's
  * partial sums) is at most m2_max_stage_bytes (default 80 KB: two
  * workgroups per CU), three or four rows only while the weights are at
- * most m34_max_weight_bytes (default 48 MB); past either the small-batch
+ * most m34_max_weight_bytes (default 16 MB); past either the small-batch
  * kernel takes the rows.  Environment overrides NF_HIP_GEMV_M2_MAX_STAGE
  * and NF_HIP_GEMV_M4_MAX_WEIGHT (bytes).  No counterpart in the reference
  * (one kernel for every M, metal_provider.mm:3009-3019). */

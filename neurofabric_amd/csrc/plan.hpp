@@ -87,12 +87,14 @@ struct LayerParams {
 // 32-row launches: 11.7 against 14.3 ms per M = 64 step; 14336x4096 69.6 vs
 // 79.5 us, 4096x14336 84.2 vs 116.3 us), the bf16-piece tiled GEMM above
 // (14336x4096 M = 128: 124.4 vs 137.8 us).
-// At M = 3..4 the winner depends on the weight size: the GEMV wins by far on
-// matrices up to tens of MB, where the small-batch kernel's fixed per-launch
-// cost dominates (f32 M = 4: 2048x2048 6.8 vs 10.4 us, 4096x4096 12.2 vs
-// 15.2 us; f16 5632x2048 8.3 vs 11.5 us), and not on the large ones
-// (28672x8192 f16 M = 3: 49.2 vs 48.5 us).  Hence the GEMV takes M = 3..4
-// only while the weights are at most gemv_m4_max_weight_bytes.
+// At M = 3..4 the winner depends on the weight size: the GEMV wins on
+// matrices up to about 10 MB, where the small-batch kernel's fixed
+// per-launch cost dominates (f32 M = 4: 2048x2048 4.9 vs 8.6 us, 4096x4096
+// 10.4 vs 11.4 us; f16 5632x2048 6.5 vs 8.7 us), they tie at 25 MB
+// (11008x4096 f32 20.2 vs 18.5, 4096x11008 19.5 vs 19.2 us) and the
+// small-batch kernel wins beyond (32000x2048 f32 25.0 vs 21.4 us,
+// 32000x4096 49.3 vs 36.2 us; f16 alike).  Hence the GEMV takes M = 3..4
+// only while the weights are at most gemv_m4_max_weight_bytes (16 MB).
 // skinny_f16_max_k caps K for f16 batches above M = 4 on the small-batch
 // kernel (longer K goes to the tiled GEMM); no cap by default, since the
 // small-batch kernel's K split over workgroups (skinny_split) makes it the
@@ -102,7 +104,7 @@ struct Tuning {
   uint32_t gemv_max_m_f16 = 4;
   uint32_t skinny_max_m_f16 = 16;
   uint32_t skinny_max_m_f32 = 64;
-  uint64_t gemv_m4_max_weight_bytes = 48ull << 20;
+  uint64_t gemv_m4_max_weight_bytes = 16ull << 20;
   uint32_t gemv_m2_max_stage_bytes = 80 * 1024;
   uint32_t skinny_f16_max_k = 1u << 30;
   // Kernel of the f16 GEMM path: -1 = the register-dequantizing kernels,

@@ -283,18 +283,20 @@ def test_crossover_setter_roundtrip():
 def test_default_switch_points(lib):
     """Defaults from the measured sweeps: GEMV for M <= 4 while its
     activation stage fits in 120 KB of LDS (M = 3..4 only for weights up to
-    48 MB), the small-batch MFMA kernel up to 16 rows, the tiled GEMM beyond
+    16 MB), the small-batch MFMA kernel up to 16 rows, the tiled GEMM beyond
     (f16); for f32 activations the small-batch kernel up to 64 rows."""
     f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
     assert _fused(lib, 2, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"   # 2 x 8192 x 2 B = 32 KB
     # M = 2: the GEMV while two of its workgroups fit a CU (stage <= 80 KB)
     assert _fused(lib, 2, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"  # 112 KB stage
     assert _fused(lib, 1, 8192, 28672, **f16)["kernel"] == "gemv_q4_0_f16"
-    # M = 3..4: the GEMV only for weights up to 48 MB (132 MB here)
+    # M = 3..4: the GEMV only for weights up to 16 MB (132 MB here)
     assert _fused(lib, 4, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
-    assert _fused(lib, 4, 11008, 4096, **f16)["kernel"] == "gemv_q4_0_f16"  # 25 MB
+    assert _fused(lib, 4, 11008, 4096, **f16)["kernel"] == "skinny_mfma_q4_0_f16"  # 25 MB
+    assert _fused(lib, 4, 4096, 4096, **f16)["kernel"] == "gemv_q4_0_f16"  # 9.4 MB
     assert _fused(lib, 4, 14336, 4096, op="dequant_q8_0_linear", bs=34)["kernel"] == "skinny_mfma_q8_0_f32"
-    assert _fused(lib, 4, 32000, 2048)["kernel"] == "gemv_q4_0_f32"  # TinyLlama lm_head, 37 MB
+    assert _fused(lib, 4, 32000, 2048)["kernel"] == "skinny_mfma_q4_0_f32"  # TinyLlama lm_head, 37 MB
+    assert _fused(lib, 3, 5632, 2048)["kernel"] == "gemv_q4_0_f32"  # 6.5 MB
     assert _fused(lib, 4, 8192, 28672, **f16)["kernel"] == "skinny_mfma_q4_0_f16"  # 4 x 28672 x 2 B > 120 KB
     assert _fused(lib, 5, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
     assert _fused(lib, 16, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
@@ -321,7 +323,7 @@ def test_gemv_row_limits(lib):
     f16 = dict(a=abi.NF_DTYPE_F16, c=abi.NF_DTYPE_F16, op="dequant_q4_0_linear_f16")
     st, wb = C.c_uint32(), C.c_uint64()
     lib.nf_hip_get_gemv_row_limits(C.byref(st), C.byref(wb))
-    assert (st.value, wb.value) == (80 * 1024, 48 << 20)
+    assert (st.value, wb.value) == (80 * 1024, 16 << 20)
     try:
         lib.nf_hip_set_gemv_row_limits(C.c_uint32(120 * 1024), C.c_uint64(200 << 20))
         assert _fused(lib, 2, 8192, 28672, **f16)["kernel"] == "gemv_q4_0_f16"   # 112 KB stage
