@@ -473,6 +473,33 @@ __global__ __launch_bounds__(NW * 64) void attention_mq_kernel(Params p) {
   }
 }
 
+// Sum / max over the 4 lanes of an MFMA output column (lanes n, n + 16,
+// n + 32, n + 48).  v_permlane16_swap / v_permlane32_swap exchange rows
+// between their two registers, so with both holding v each lane ends with
+// its own value and its partner's (lane ^ 16, then lane ^ 32) in the pair.
+// Inline asm: the compiler's builtins for these instructions lose the second
+// result; the s_nop gives the two wait states a VALU write needs before a
+// permlane reads it.
+template <bool ROW32>
+__device__ __forceinline__ float2s lane_swap_pair(float v) {
+  float a = v, b = v;
+  if constexpr (ROW32)
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  else
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return float2s{a, b};
+}
+__device__ __forceinline__ float col_max(float v) {
+  float2s r = lane_swap_pair<false>(v);
+  r = lane_swap_pair<true>(fmaxf(r[0], r[1]));
+  return fmaxf(r[0], r[1]);
+}
+__device__ __forceinline__ float col_sum(float v) {
+  float2s r = lane_swap_pair<false>(v);
+  r = lane_swap_pair<true>(r[0] + r[1]);
+  return r[0] + r[1];
+}
+
 // Prefill on MFMA (f16, head_dim DD = 64 or 128; not paged): flash attention
 // with the matrices transposed so that every operand comes out of registers
 // or LDS in the layout the next MFMA wants.  A workgroup takes 64 query
@@ -624,32 +651,6 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(Params p) {
     typedef short short4v __attribute__((ext_vector_type(4)));
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                                          (__attribute__((address_space(3))) short4v*)(vtr + key0 * KP + dim0)));
-  };
-
-  // Sum / max over the 4 lanes of a query's column (lanes n, n + 16, n + 32,
-  // n + 48).  v_permlane16_swap / v_permlane32_swap exchange rows between
-  // their two registers, so with both holding v each lane ends with its own
-  // value and its partner's (lane ^ 16, then lane ^ 32) in the pair.  Inline
-  // asm: the compiler's builtins for these instructions lose the second
-  // result; the s_nop gives the two wait states a VALU write needs before a
-  // permlane reads it.
-  auto swap_pair = [](float v, auto row32) {
-    float a = v, b = v;
-    if constexpr (decltype(row32)::value)
-      asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    else
-      asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return float2s{a, b};
-  };
-  auto col_max = [&](float v) {
-    float2s r = swap_pair(v, std::false_type{});
-    r = swap_pair(fmaxf(r[0], r[1]), std::true_type{});
-    return fmaxf(r[0], r[1]);
-  };
-  auto col_sum = [&](float v) {
-    float2s r = swap_pair(v, std::false_type{});
-    r = swap_pair(r[0] + r[1], std::true_type{});
-    return r[0] + r[1];
   };
 
   // One staged tile for this wave.  INTERIOR: every key in every query's
@@ -922,25 +923,6 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_mfma_kernel(Params p) {
       *reinterpret_cast<float4v*>(&Vs[r * DP + 4 * c]) = v;
     }
     if (bad) tile_bad[par] = 1;
-  };
-
-  auto swap_pair = [](float v, auto row32) {
-    float a = v, b = v;
-    if constexpr (decltype(row32)::value)
-      asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    else
-      asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return float2s{a, b};
-  };
-  auto col_max = [&](float v) {
-    float2s r = swap_pair(v, std::false_type{});
-    r = swap_pair(fmaxf(r[0], r[1]), std::true_type{});
-    return fmaxf(r[0], r[1]);
-  };
-  auto col_sum = [&](float v) {
-    float2s r = swap_pair(v, std::false_type{});
-    r = swap_pair(r[0] + r[1], std::true_type{});
-    return r[0] + r[1];
   };
 
   auto tile = [&](int64_t t0, int par, auto interior_c) {
