@@ -1490,8 +1490,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t
       sv[j][i] = ok ? sc[j][i] * sl2 : -INFINITY;
       tmax = fmaxf(tmax, sv[j][i]);
     }
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+  tmax = col_max(tmax);
   float psum = 0.f;
 #pragma unroll
   for (int j = 0; j < KB; ++j)
@@ -1501,8 +1500,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t
       psum += pw;
       if (n < G) ps[w][16 * j + 4 * kg + i][n] = pw;
     }
-  psum += __shfl_xor(psum, 16);
-  psum += __shfl_xor(psum, 32);
+  psum = col_sum(psum);
   if (kg == 0 && n < G) {
     wm[w][n] = tmax;
     wl[w][n] = psum;
@@ -1536,13 +1534,26 @@ __global__ __launch_bounds__(NW * 64) void decode_mfma_kernel(Params p, uint32_t
       for (int g = 0; g < G; ++g) acc[g][e] = __builtin_fmaf(pr[g], x, acc[g][e]);
     }
   }
-  // add the RPI row groups (lanes dc, dc + CPR, ...) in a fixed order
+  // add the RPI row groups (lanes dc, dc + CPR, ...): xor shuffles below a
+  // distance of 16 lanes, lane-row swaps (VALU, no LDS round trip) at 16 and
+  // 32; each pair adds the same two values in the same order on both lanes
 #pragma unroll
-  for (int o = CPR; o < 64; o <<= 1)
+  for (int o = CPR; o < 16; o <<= 1)
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int e = 0; e < EPC; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      if constexpr (CPR <= 16) {
+        const float2s r = lane_swap_pair<false>(acc[g][e]);
+        acc[g][e] = r[0] + r[1];
+      }
+      const float2s r = lane_swap_pair<true>(acc[g][e]);
+      acc[g][e] = r[0] + r[1];
+    }
   if (kq == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
