@@ -1356,7 +1356,9 @@ __global__ __launch_bounds__(64) void decode_split_kernel(Params p, uint32_t key
 //    splits.
 //    (Measured and not kept: the merge in the last-arriving workgroup of
 //    each KV head, 15.7 against 11.4 us at 4096 keys: the store, counter
-//    and reload round trips cost more than a second launch.)
+//    and reload round trips cost more than a second launch; a one-pass
+//    combine, each thread merging its column over its splits with a running
+//    maximum, 12.4 against 11.9 us.)
 // Rows past the range or without storage read row 0 and drop out by select
 // (score -inf, value 0), so no load is predicated and unused memory never
 // reaches the sums.  Row `step` is read from K_new / V_new when the append is
