@@ -1676,8 +1676,9 @@ hipError_t run_decode_split(const Params& p, float* ws, size_t ws_floats, hipStr
                                       : 0)) & 15) == 0;
     if (al && (p.dim == 64 || p.dim == 128)) {
       // 4 waves of 32 keys per workgroup (measured at 4096 keys: 7.1 us
-      // against 9.0 with 8 waves of 32 and 9.1 with 4 of 64), 64-key tiles
-      // past 8192 keys
+      // against 9.0 with 8 waves of 32 and 9.1 with 4 of 64; with 4 of 16,
+      // twice the workgroups and partials, 13.1 against 11.7 us with the
+      // combine), 64-key tiles past 8192 keys
       const uint32_t tk = n_keys <= 8192 ? 32u : 64u;
       const uint64_t ns = (n_keys + 4 * tk - 1) / (4 * tk);
       if (ns <= (uint64_t)kMaxSplits && ns * H * (p.dim + 2) <= ws_floats) {
