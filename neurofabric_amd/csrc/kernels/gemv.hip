@@ -423,7 +423,9 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   // is formed with DPP adds across them (total is a multiple of 8, so the 8
   // lanes of a block are in or out of range together).  Loads past the end
   // are clamped to the last chunk and dropped, so no load is predicated and
-  // all eight are in flight together.
+  // all eight are in flight together (skipping whole rounds past the end
+  // behind a uniform branch instead measured 542 against 437 us for the
+  // TinyLlama decode step).
   {
     const int total = M * P * CP;
     auto load = [&](int c0, ChunkT (&v)[8]) {
