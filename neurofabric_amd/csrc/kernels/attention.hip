@@ -1600,16 +1600,34 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const float* __res
   // add in a fixed order.  A workgroup takes 32 columns, so a head's loads
   // spread over D/32 workgroups (measured with 32 heads x 128 dims and 32
   // splits, the whole decode: 11.9 us with one workgroup per head, 15.2
-  // with 256 threads, 11.0 with 64 columns and 10.9 with 32).
+  // with 256 threads, 11.0 with 64 columns and 10.9 with 32; 10.7 with
+  // each thread's first column value requested at the start and the
+  // splits' (m, l) kept in registers between the passes).
   __shared__ float w[kMaxSplits];
   __shared__ float red[1024];
   __shared__ float mm[2];
   const uint32_t h = blockIdx.x;
   const uint32_t stride = D + 2;
   const uint32_t t = threadIdx.x;
+  // workgroup (h, y) takes columns 32y .. 32y + 31: 32 groups of 32 threads
+  // (head_dim <= 256: at most 8 workgroups per head)
+  constexpr uint32_t dpad = 32, groups = 1024 / dpad;
+  const uint32_t grp = t / dpad, dl = t % dpad, d = blockIdx.y * dpad + dl;
+  const uint64_t cstep = (uint64_t)H * stride;
+  const float* src = part + (uint64_t)h * stride + 2 + (d < D ? d : 0);
+  // the thread's first column value is requested before the weights are
+  // formed, so its latency overlaps theirs
+  const float a0 = d < D && grp < n_splits ? src[(uint64_t)grp * cstep] : 0.0f;
+  // threads 0..63 keep (m, l) of split t in registers for the later passes
+  float m0 = -INFINITY, l0 = 0.0f;
   if (t < 64) {
-    float m = -INFINITY;
-    for (uint32_t sp = t; sp < n_splits; sp += 64) m = fmaxf(m, part[((uint64_t)sp * H + h) * stride]);
+    if (t < n_splits) {
+      const float* r = part + ((uint64_t)t * H + h) * stride;
+      m0 = r[0];
+      l0 = r[1];
+    }
+    float m = m0;
+    for (uint32_t sp = t + 64; sp < n_splits; sp += 64) m = fmaxf(m, part[((uint64_t)sp * H + h) * stride]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if (t == 0) mm[0] = m;
@@ -1617,27 +1635,22 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const float* __res
   __syncthreads();
   const float M = mm[0];
   for (uint32_t sp = t; sp < n_splits; sp += 1024) {
-    const float m = part[((uint64_t)sp * H + h) * stride];
+    const float m = sp < 64 ? m0 : part[((uint64_t)sp * H + h) * stride];  // sp < 64: sp == t
     w[sp] = m == -INFINITY ? 0.0f : expf(m - M);
   }
   __syncthreads();
   if (t < 64) {
-    float L = 0.0f;
-    for (uint32_t sp = t; sp < n_splits; sp += 64) L += part[((uint64_t)sp * H + h) * stride + 1] * w[sp];
+    float L = t < n_splits ? l0 * w[t] : 0.0f;
+    for (uint32_t sp = t + 64; sp < n_splits; sp += 64) L += part[((uint64_t)sp * H + h) * stride + 1] * w[sp];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
     if (t == 0) mm[1] = L > 0.0f ? 1.0f / L : 0.0f;
   }
-  // workgroup (h, y) takes columns 32y .. 32y + 31: 32 groups of 32 threads
-  // (head_dim <= 256: at most 8 workgroups per head)
-  constexpr uint32_t dpad = 32, groups = 1024 / dpad;
-  const uint32_t grp = t / dpad, dl = t % dpad, d = blockIdx.y * dpad + dl;
   float o = 0.0f;
-  if (d < D) {
-    const uint64_t step = (uint64_t)H * stride;
-    const float* src = part + (uint64_t)h * stride + 2 + d;
+  if (d < D && grp < n_splits) {
+    o += a0 * w[grp];
 #pragma unroll 8
-    for (uint32_t sp = grp; sp < n_splits; sp += groups) o += src[sp * step] * w[sp];
+    for (uint32_t sp = grp + groups; sp < n_splits; sp += groups) o += src[sp * cstep] * w[sp];
   }
   red[t] = o;
   __syncthreads();
