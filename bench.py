@@ -9,28 +9,33 @@ Headline workload: one TinyLlama-1.1B decode step
 (default 1), every projection dispatched through the provider's C ABI
 (nf_provider_vtable.dispatch semantics, via nf_hip_run_tasks).  A step is one
 pass over those 155 linears; W warm-up steps, then K steps timed with HIP
-events on the provider's stream.  Weights, activations and outputs are
-resident in HBM before timing starts; the 582 MB of weights per step exceed
-2x the 256 MB Infinity Cache, so steps do not hit in cache.
+events on the provider's stream, one event between consecutive steps.
+Weights, activations and outputs are resident in HBM before timing starts;
+the 582 MB of weights per step exceed 2x the 256 MB Infinity Cache, so steps
+do not hit in cache.
 
   value      = algorithmic bytes per step (Q4_0 blocks 18 B/32 weights +
-               activations + outputs, each counted once per linear) / step time
+               activations + outputs, each counted once per linear) / median
+               step time over the K timed steps (ms_per_step is that median;
+               the mean is in extra.headline)
   roofline   = the dominant kernel (the Q4_0 f32 decode GEMV, every launch of
-               the step): achieved = algorithmic bytes per launch / mean launch
-               duration over the timed region (graph replay: kernels run back
-               to back); traffic = measured HBM bytes per launch
+               the step): achieved = algorithmic bytes per launch / launch
+               duration (median step time / launches; graph replay: kernels
+               run back to back); traffic = measured HBM bytes per launch
                from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/
                (scaled by a copy-kernel calibration), when present
-  cpu_baseline = the oracle (the restated reference CPU dequant + sequential-k
-               loop, oracle/) timed on this host, 1 thread, on whole decode
-               steps repeated for >= 10 s
+  cpu_baseline = the reference's own CPU dequant + naive loop built from its
+               source (oracle/_ref), else the oracle's restatement, on this
+               host, 1 thread, on whole decode steps repeated for >= 10 s
 
-Extras in the same JSON line: decode steps at M=4 and 16, configs[0] (one
+Also measured (key figures in the line's short `extra`, full tables in the
+--full-out file and on stderr): decode steps at M=4 and 16, configs[0] (one
 5632x2048 GEMV over 80 rotated weight copies), a Llama-3-8B Q8_0 decode step
 (configs[3], 32 layers + lm_head) at M=1/16/64, a Llama-2-7B Q4_0 decode step
 at M=1 (north_star's "Llama-7B shapes"), Llama-2-7B Q4_0 prefill GEMMs
-(configs[2]) in TFLOP/s, and the configs[4] GEMV / small-batch / tiled-GEMM
-crossover sweep over M = 1..256 on both 70B FFN shapes.
+(configs[2]) in TFLOP/s over >= 512 MB of rotated weights, and the configs[4]
+GEMV / small-batch / tiled-GEMM crossover sweep over M = 1..256 on both 70B
+FFN shapes.  The stdout line stays under LINE_MAX_BYTES.
 
 Modes: `graph` captures the step's dispatches (one nf_hip_run_tasks call)
 into a HIP graph and replays it; `eager` calls nf_hip_run_tasks every step.
@@ -73,6 +78,8 @@ def parse(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
     ap.add_argument("--only", choices=["c0", "c2", "c3", "c4", "c7b", "dq", "up", "layer", "floor"], default=None,
                     help="run one configs[i] section alone and print its JSON (profiling aid)")
+    ap.add_argument("--full-out", default=str(REPO / "gpurun_out" / "bench_full.json"), metavar="PATH",
+                    help="file for the full tables behind the line's short extra ('' = none)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 4 device-to-device copies of BYTES (reference for HBM byte counters)")
     return ap.parse_args(argv)
@@ -285,19 +292,24 @@ def time_step(prov, st: Step, steps: int, warmup: int, mode: str) -> dict:
     prov.run_tasks(st.tasks, 1)
     prov.synchronize()
     launches = prov.launch_count() - c0
-    e0, e1 = hiprt.Event(), hiprt.Event()
+    # One HIP event between consecutive steps: the step times give the
+    # median; first-to-last event over the step count gives the mean.
+    ev = [hiprt.Event() for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
+    ev[0].record(stream)
+    for i in range(steps):
         run()
-    e1.record(stream)
-    e1.synchronize()
+        ev[i + 1].record(stream)
+    ev[-1].synchronize()
     prov.synchronize()
     hiprt.device_synchronize()
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_ms(e1) / steps
-    return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / steps, "dispatches": len(st.tasks),
-            "launches": launches, "us_per_launch": ms * 1e3 / launches}
+    per = np.array([ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)], np.float64)
+    mean = ev[0].elapsed_ms(ev[-1]) / steps
+    med = float(np.median(per))
+    return {"ms_per_step": med, "mean_ms_per_step": mean, "min_ms_per_step": float(per.min()),
+            "wall_ms_per_step": wall * 1e3 / steps, "dispatches": len(st.tasks), "repetitions": steps,
+            "launches": launches, "us_per_launch": med * 1e3 / launches}
 
 
 def time_dispatches(prov, st: Step, steps: int) -> dict:
@@ -519,7 +531,7 @@ def run_c3(prov, mode: str) -> dict:
     llama3 = WeightSet(prov, llama3_q8_step_shapes(), "q8_0")
     for M in (1, 16, 64):
         s3 = model_step(prov, llama3, M)
-        r3 = time_step(prov, s3, 10, 2, mode)
+        r3 = time_step(prov, s3, 20, 2, mode)
         c3[f"m{M}"] = {"GB_s": s3.bytes / (r3["ms_per_step"] * 1e-3) / 1e9,
                        "us_per_step": r3["ms_per_step"] * 1e3,
                        "tokens_per_s": M / (r3["ms_per_step"] * 1e-3),
@@ -573,23 +585,29 @@ def dense_f16_library_tflops(shapes, reps: int = 20) -> dict:
     return dict(zip(shapes, vals))
 
 
-def run_c2(prov) -> dict:
-    """Llama-2-7B Q4_0 prefill GEMMs, f16 activations, 4 rotated
-    weight copies per shape; beside each, the vendor library's dense fp16
-    GEMM of the same shape (dense_f16_library_tflops)."""
+def run_c2(prov, reps: int = 20) -> dict:
+    """Llama-2-7B Q4_0 prefill GEMMs, f16 activations.  Each shape
+    runs over as many distinct weight copies as make >= 512 MB (twice the
+    Infinity Cache), one pass over all copies per repetition; the figure is
+    the median of `reps` repetitions.  Beside each, the vendor library's
+    dense fp16 GEMM of the same shape (dense_f16_library_tflops)."""
     pre = {}
     shapes = [("qkvo_4096x4096", 4096, 4096), ("gate_up_11008x4096", 11008, 4096), ("down_4096x11008", 4096, 11008)]
     lib = dense_f16_library_tflops([(M, N, K) for (_, N, K) in shapes for M in (512, 2048)])
     for (name, N, K) in shapes:
+        wbytes = N * (K // 32) * 18
+        copies = -(-ROTATE_BYTES // wbytes)
         for M in (512, 2048):
-            sp = rotated_linear(prov, "q4_0", M, N, K, True, 4)
-            rp = time_step(prov, sp, 5, 2, "eager")
+            sp = rotated_linear(prov, "q4_0", M, N, K, True, copies)
+            rp = time_step(prov, sp, reps, 2, "eager")
             tf = sp.flops / (rp["ms_per_step"] * 1e-3) / 1e12
             lib_tf = lib.get((M, N, K))
             pre[f"{name}_m{M}"] = {"TFLOP_s": tf, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS,
                                    "us_per_launch": rp["us_per_launch"], "kernels": sorted(sp.kernels),
-                                   "dense_f16_library_TFLOP_s": lib_tf}
-            log(f"[bench] prefill {name} M={M}: {tf:.1f} TFLOP/s (library dense fp16 GEMM, no dequant: "
+                                   "weight_copies": copies, "rotated_MB": copies * wbytes / 1e6,
+                                   "repetitions": reps, "dense_f16_library_TFLOP_s": lib_tf}
+            log(f"[bench] prefill {name} M={M}: {tf:.1f} TFLOP/s, {rp['us_per_launch']:.1f} us/launch "
+                f"(median of {reps} passes over {copies} weight copies; library dense fp16 GEMM, no dequant: "
                 f"{lib_tf if lib_tf is None else round(lib_tf, 1)} TFLOP/s)")
             sp.release()
     return pre
@@ -747,6 +765,116 @@ def run_upload(prov, mb: int = 512) -> dict:
     return res
 
 
+# ---------------------------------------------------------------------------
+# the stdout line: headline keys, roofline, cpu_baseline and a short extra
+# (the full tables go to a side file and to stderr)
+
+LINE_MAX_BYTES = 6000  # the driver keeps the last 8000 bytes of stdout
+
+
+def _r(x, sig: int = 4):
+    """Round a number to `sig` significant digits (other values unchanged)."""
+    if isinstance(x, bool) or not isinstance(x, (int, float)):
+        return x
+    if isinstance(x, int) or x == 0 or x != x:
+        return x
+    return float(f"{x:.{sig}g}")
+
+
+def summarize_extra(full: dict) -> dict:
+    """Key figures of the full extra tables, a few hundred bytes each."""
+    s = {}
+    h = full.get("headline_step")
+    if h:
+        s["headline"] = {k: _r(h[k]) for k in ("median_us_per_step", "mean_us_per_step", "min_us_per_step",
+                                               "launches", "dispatches", "tokens_per_s", "repetitions") if k in h}
+    for M in (1, 4, 16):
+        d = full.get(f"c1_decode_m{M}")
+        if d:
+            s[f"c1_m{M}"] = {"us": _r(d["us_per_step"]), "GB_s": _r(d["GB_s"]), "tok_s": _r(d["tokens_per_s"])}
+    d = full.get("c0_gemv_5632x2048")
+    if d:
+        s["c0"] = {"us_per_launch": _r(d["us_per_launch_step"]), "GB_s": _r(d["GB_s_step"])}
+    d = full.get("llama2_7b_q4_0_decode_m1")
+    if d:
+        s["llama2_7b_q4_0_m1"] = {"us": _r(d["us_per_step"]), "GB_s": _r(d["GB_s"]),
+                                  "frac": _r(d["frac_of_hbm_peak"], 3), "tok_s": _r(d["tokens_per_s"])}
+    d = full.get("c3_llama3_8b_q8_0_decode")
+    if d:
+        s["c3_q8_0"] = {k: {"us": _r(v["us_per_step"]), "GB_s": _r(v["GB_s"])} for k, v in d.items()}
+    d = full.get("c2_prefill_f16")
+    if d:
+        s["c2_TFLOP_s"] = {k: _r(v["TFLOP_s"]) for k, v in d.items()}
+        s["c2_library_dense_f16_TFLOP_s"] = {k: _r(v.get("dense_f16_library_TFLOP_s")) for k, v in d.items()}
+    d = full.get("c4_crossover")
+    if d:
+        c4 = {"switch_points": d.get("switch_points", {}).get("measured"),
+              "default_not_fastest": len(d.get("switch_points", {}).get("default_not_fastest", []))}
+        for shape, v in d.items():
+            if isinstance(v, dict) and "rows" in v:
+                c4[shape] = {r["M"]: [r["fastest"], _r(r[r["fastest"]]["us"], 3)] for r in v["rows"]}
+        s["c4"] = c4
+    d = full.get("dequant_7b_ffn_weight")
+    if d:
+        g = [v["GB_s"] for v in d.values()]
+        s["dequant_GB_s"] = {"min": _r(min(g)), "max": _r(max(g)), "q4_0_f16": _r(d.get("q4_0_f16", {}).get("GB_s"))}
+    d = full.get("weight_upload_512MiB")
+    if d:
+        s["upload_GB_s"] = {k: _r(v["GB_s"], 3) for k, v in d.items()}
+    d = full.get("layer_ops")
+    if d:
+        s["layer_us"] = {k: _r(v["us_per_launch"], 3) for k, v in d.items()}
+    d = full.get("gemv_launch_floor")
+    if d:
+        s["floor"] = {"empty_us": _r(d.get("empty_kernel_us"), 3)}
+        s["floor"].update({k.split(" ")[0] + "_" + k.split(" ")[-1]: [_r(v["read_us"], 3), _r(v["gemv_us"], 3)]
+                           for k, v in d.items() if isinstance(v, dict)})
+    for k in ("cpu_all_cores", "cpu_x86_64_v3_1_thread"):
+        if full.get(k):
+            s[k] = {"GB_s": _r(full[k]["value"]), "cores": full[k]["cores"]}
+    return s
+
+
+def build_line(*, gbs, med_ms, args, dispatches, launches, kernels, achieved, bytes_per_launch, avg_launch_us,
+               ring_us, traffic, cpu, extra_full, full_path, mode, m) -> dict:
+    """The one JSON line bench.py prints."""
+    extra = summarize_extra(extra_full)
+    if full_path:
+        extra["full_tables"] = str(full_path)
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": med_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights, f32 activations/accumulate",
+        "data": "synthetic (seeded Q4_0 blocks: fp16 scales |N(0,1)|*0.01, codes U{0..15}; x ~ N(0,1))",
+        "config": {"workload": f"configs[1] TinyLlama-1.1B Q4_0 decode step, M={m}: 22 layers x "
+                               f"{{q,k,v,o,gate,up,down}} + lm_head = {dispatches} fused dequant+GEMV "
+                               f"dispatches in {launches} launches ({mode} replay; q/k/v and gate/up read "
+                               f"the same activations and are merged); value and ms_per_step are the median "
+                               f"of {args.steps} timed steps",
+                   "batch": m, "hidden": 2048, "ffn": 5632, "vocab": 32000,
+                   "tokens_per_s": _r(m / (med_ms * 1e-3))},
+        "roofline": {"bound": "hbm", "kernel": ",".join(kernels), "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "bytes_per_launch": round(bytes_per_launch, 1),
+                     "avg_launch_us": _r(avg_launch_us, 5), "event_ring_mean_launch_us": _r(ring_us),
+                     "traffic_source": str(PMC_SUMMARY.relative_to(REPO)) if traffic is not None else None},
+        "cpu_baseline": None if cpu is None else {k: (_r(cpu[k]) if k == "value" else cpu[k])
+                                                  for k in ("value", "unit", "cores", "kind", "sample")},
+        "extra": extra,
+    }
+    if len(json.dumps(line)) > LINE_MAX_BYTES:  # keep the headline keys whatever the extras hold
+        line["extra"] = {"full_tables": extra.get("full_tables"), "dropped": "extra summary over size limit"}
+    return line
+
+
 def load_pmc_summary():
     if PMC_SUMMARY.exists():
         try:
@@ -774,7 +902,7 @@ def main(argv=None) -> int:
     if args.only:
         sections = {"c0": lambda: run_c0(prov, args.mode), "c2": lambda: run_c2(prov),
                     "c3": lambda: run_c3(prov, args.mode), "c4": lambda: crossover_sweep(prov),
-                    "c7b": lambda: run_step(prov, syn.llama2_7b_step_shapes(), "q4_0", 1, 10, 2, args.mode),
+                    "c7b": lambda: run_step(prov, syn.llama2_7b_step_shapes(), "q4_0", 1, 20, 2, args.mode),
                     "dq": lambda: run_dq(prov), "up": lambda: run_upload(prov),
                     "layer": lambda: run_layer(prov), "floor": lambda: launch_floor(prov)}
         print(json.dumps({args.only: sections[args.only]()}), flush=True)
@@ -806,7 +934,10 @@ def main(argv=None) -> int:
     kernels = sorted(st.kernels)
     st.release()
 
-    extra = {"headline_step": {"us_per_step": r["ms_per_step"] * 1e3, "wall_us_per_step": r["wall_ms_per_step"] * 1e3,
+    extra = {"headline_step": {"median_us_per_step": r["ms_per_step"] * 1e3,
+                               "mean_us_per_step": r["mean_ms_per_step"] * 1e3,
+                               "min_us_per_step": r["min_ms_per_step"] * 1e3,
+                               "wall_us_per_step": r["wall_ms_per_step"] * 1e3, "repetitions": r["repetitions"],
                                "dispatches": dispatches, "launches": launches,
                                "bytes_per_step": bytes_per_launch * launches,
                                "tokens_per_s": args.m / (r["ms_per_step"] * 1e-3)}}
@@ -815,7 +946,7 @@ def main(argv=None) -> int:
             if M == args.m:
                 continue
             s2 = model_step(prov, tiny, M)
-            r2 = time_step(prov, s2, max(10, args.steps // 2), args.warmup, args.mode)
+            r2 = time_step(prov, s2, max(20, args.steps // 2), args.warmup, args.mode)
             extra[f"c1_decode_m{M}"] = {"GB_s": s2.bytes / (r2["ms_per_step"] * 1e-3) / 1e9,
                                         "us_per_step": r2["ms_per_step"] * 1e3,
                                         "tokens_per_s": M / (r2["ms_per_step"] * 1e-3),
@@ -825,7 +956,7 @@ def main(argv=None) -> int:
     tiny.release()
     if not args.no_extra:
         extra["c0_gemv_5632x2048"] = run_c0(prov, args.mode)
-        extra["llama2_7b_q4_0_decode_m1"] = run_step(prov, syn.llama2_7b_step_shapes(), "q4_0", 1, 10, 2, args.mode)
+        extra["llama2_7b_q4_0_decode_m1"] = run_step(prov, syn.llama2_7b_step_shapes(), "q4_0", 1, 20, 2, args.mode)
         log(f"[bench] Llama-2-7B Q4_0 decode step M=1: {extra['llama2_7b_q4_0_decode_m1']}")
         extra["c3_llama3_8b_q8_0_decode"] = run_c3(prov, args.mode)
         extra["c2_prefill_f16"] = run_c2(prov)
@@ -853,36 +984,20 @@ def main(argv=None) -> int:
     traffic = None
     if pmc and pmc.get("kernel_family") == kernels[0]:
         traffic = pmc.get("hbm_bytes_per_launch")
-    line = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": r["ms_per_step"],
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "q4_0 weights, f32 activations/accumulate",
-        "data": "synthetic (seeded Q4_0 blocks: fp16 scales |N(0,1)|*0.01, codes U{0..15}; x ~ N(0,1))",
-        "config": {"workload": f"configs[1] TinyLlama-1.1B Q4_0 decode step, M={args.m}: 22 layers x "
-                               f"{{q,k,v,o,gate,up,down}} + lm_head = {dispatches} fused dequant+GEMV "
-                               f"dispatches in {launches} launches ({args.mode}; q/k/v and gate/up, which "
-                               f"read the same activations, are merged by nf_hip_run_tasks)",
-                   "batch": args.m, "hidden": 2048, "ffn": 5632, "vocab": 32000,
-                   "tokens_per_s": args.m / (r["ms_per_step"] * 1e-3)},
-        "roofline": {"bound": "hbm", "kernel": ",".join(kernels), "achieved": round(achieved, 2),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic,
-                     "bytes_per_launch": bytes_per_launch,
-                     "avg_launch_us": avg_launch_us,
-                     "launches_timed": launches * args.steps,
-                     "event_ring_mean_launch_us": ring["mean_launch_us"],
-                     "traffic_source": str(PMC_SUMMARY.relative_to(REPO)) if traffic is not None else None},
-        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
-        "extra": extra,
-    }
+    full_path = None
+    if args.full_out:
+        full_path = Path(args.full_out)
+        try:
+            full_path.parent.mkdir(parents=True, exist_ok=True)
+            full_path.write_text(json.dumps({"extra": extra, "cpu_baseline": cpu}, indent=1))
+            log(f"[bench] full tables written to {full_path}")
+        except OSError as e:
+            log(f"[bench] could not write {full_path}: {e}")
+            full_path = None
+    line = build_line(gbs=gbs, med_ms=r["ms_per_step"], args=args, dispatches=dispatches, launches=launches,
+                      kernels=kernels, achieved=achieved, bytes_per_launch=bytes_per_launch,
+                      avg_launch_us=avg_launch_us, ring_us=ring["mean_launch_us"], traffic=traffic, cpu=cpu,
+                      extra_full=extra, full_path=full_path, mode=args.mode, m=args.m)
     print(json.dumps(line), flush=True)
     return 0
 

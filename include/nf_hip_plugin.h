@@ -197,7 +197,11 @@ NF_API nf_status nf_hip_diag_stream_read(const void *src, uint64_t bytes, void *
 
 /* The in-order hipStream_t (as void*) every dispatch is launched on, so a
  * caller can time or capture (hipStreamBeginCapture) a run of dispatches.
- * NF_ERROR_INVALID_ARG before init. */
+ * A buffer that a captured dispatch writes is marked for good: map,
+ * cache_sync(INVALIDATE) and nf_hip_buffer_read of it drain this stream
+ * first, so they see the results of every graph replay the caller launched
+ * on it.  Work the caller enqueues on any other stream is the caller's to
+ * synchronize before such a read.  NF_ERROR_INVALID_ARG before init. */
 NF_API nf_status nf_hip_get_stream(nf_provider self, void **stream);
 
 /* Device pointer behind one of this provider's buffers (for zero-copy

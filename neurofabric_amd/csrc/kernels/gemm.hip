@@ -1876,8 +1876,12 @@ hipError_t launch_dense_mfma_f16(const void* A, const void* B, void* C, uint32_t
 hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M,
                             uint32_t N, uint32_t K, int tile, const Workspace& ws, hipStream_t s) {
   if (t == EType::F32) {  // f32 activations and output: bf16-piece MFMA kernel
+    // Operands at addresses the kernel's 16-byte activation loads and dword
+    // weight loads cannot take (imported buffers at odd offsets, raw
+    // pointers of the no-allocation entry point): the GEMV, whose block
+    // kernel reads any alignment and any M.
     const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
-    if (K % 64 != 0 || !aligned) return hipErrorInvalidValue;
+    if (K % 64 != 0 || !aligned) return launch_gemv(q, t, A, W, C, M, N, K, s);
     const float* a = static_cast<const float*>(A);
     const uint8_t* w = static_cast<const uint8_t*>(W);
     float* c = static_cast<float*>(C);

@@ -99,9 +99,15 @@ struct Buffer {
   int ev_slot = -1;
   uint64_t ev_seq = 0;
   std::atomic<bool> exported{false};  // a share token was handed out
+  // A launch captured into a graph wrote this buffer: every replay of that
+  // graph rewrites it without passing through the provider, so reads drain
+  // the launch stream and never trust the staging copy.
+  std::atomic<bool> graph_written{false};
 };
 
-inline bool host_current(const Buffer* b) { return b->host_has && b->host_seq == b->last_write_seq.load(); }
+inline bool host_current(const Buffer* b) {
+  return b->host_has && !b->graph_written.load() && b->host_seq == b->last_write_seq.load();
+}
 
 struct TimingRec {
   char op[64];
@@ -170,8 +176,9 @@ nf_status drain(Provider* p) {
 nf_status wait_for_writes(Buffer* b) {
   Provider* p = b->prov;
   // Memory shared with another buffer handle (imported, or exported for
-  // import) may be written through that handle: drain.
-  if (!b->owns_dev || b->exported.load()) return drain(p);
+  // import) may be written through that handle, and a buffer a captured
+  // graph writes by every replay of it on the launch stream: drain.
+  if (!b->owns_dev || b->exported.load() || b->graph_written.load()) return drain(p);
   const uint64_t target = b->last_write_seq.load();
   if (target <= p->done_seq.load()) return NF_OK;
   hipEvent_t ev = nullptr;
@@ -732,10 +739,11 @@ nf_status launch(Provider* p, const Prepared* prs, uint32_t n) {
     // The launch's completion event; none while the stream is being
     // captured into a graph (the written buffers then fall back to a drain).
     int slot = -1;
+    bool captured = false;
     if (e == hipSuccess) {
       hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-      if (hipStreamIsCapturing(p->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
-          hipEventRecord(p->done_ev[p->next_ev], p->stream) == hipSuccess) {
+      captured = hipStreamIsCapturing(p->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+      if (!captured && hipEventRecord(p->done_ev[p->next_ev], p->stream) == hipSuccess) {
         slot = p->next_ev;
         p->next_ev = (p->next_ev + 1) % kEventRing;
       }
@@ -747,6 +755,7 @@ nf_status launch(Provider* p, const Prepared* prs, uint32_t n) {
         b->last_write_seq.store(seq);
         b->ev_slot = slot;
         b->ev_seq = last;
+        if (captured) b->graph_written.store(true);
       };
       for (uint32_t i = 0; i < prs[j].n_out; ++i) wrote(prs[j].out[i]);
       for (uint32_t i = 0; i < prs[j].n_in; ++i)
@@ -1034,30 +1043,43 @@ NF_API void nf_hip_set_skinny_max_m(uint32_t f16_path) {
   g_prov.tuning.skinny_max_m_f16 = f16_path;
 }
 
-NF_API uint32_t nf_hip_get_skinny_max_m(void) { return g_prov.tuning.skinny_max_m_f16; }
+NF_API uint32_t nf_hip_get_skinny_max_m(void) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  return g_prov.tuning.skinny_max_m_f16;
+}
 
 NF_API void nf_hip_set_skinny_max_m_f32(uint32_t f32_path) {
   std::lock_guard<std::mutex> lk(g_prov.mu);
   g_prov.tuning.skinny_max_m_f32 = f32_path;
 }
 
-NF_API uint32_t nf_hip_get_skinny_max_m_f32(void) { return g_prov.tuning.skinny_max_m_f32; }
+NF_API uint32_t nf_hip_get_skinny_max_m_f32(void) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  return g_prov.tuning.skinny_max_m_f32;
+}
 
 NF_API void nf_hip_set_skinny_f16_max_k(uint32_t k) {
   std::lock_guard<std::mutex> lk(g_prov.mu);
   g_prov.tuning.skinny_f16_max_k = k;
 }
 
-NF_API uint32_t nf_hip_get_skinny_f16_max_k(void) { return g_prov.tuning.skinny_f16_max_k; }
+NF_API uint32_t nf_hip_get_skinny_f16_max_k(void) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  return g_prov.tuning.skinny_f16_max_k;
+}
 
 NF_API void nf_hip_set_gemm_tile(int32_t tile) {
   std::lock_guard<std::mutex> lk(g_prov.mu);
   g_prov.tuning.gemm_tile = (tile >= 0 && tile <= 10) ? tile : -1;
 }
 
-NF_API int32_t nf_hip_get_gemm_tile(void) { return g_prov.tuning.gemm_tile; }
+NF_API int32_t nf_hip_get_gemm_tile(void) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
+  return g_prov.tuning.gemm_tile;
+}
 
 NF_API void nf_hip_get_gemv_max_m(uint32_t* f32_path, uint32_t* f16_path) {
+  std::lock_guard<std::mutex> lk(g_prov.mu);
   if (f32_path) *f32_path = g_prov.tuning.gemv_max_m_f32;
   if (f16_path) *f16_path = g_prov.tuning.gemv_max_m_f16;
 }
@@ -1273,10 +1295,16 @@ NF_API nf_status nf_hip_fused_linear_noalloc(nf_dtype wtype, const void* A, cons
   pc.M = M;
   pc.N = N;
   pc.K = K;
+  // The switch points as of this call, copied under the provider lock that
+  // the nf_hip_set_* setters take.
+  Tuning tuning;
+  {
+    std::lock_guard<std::mutex> lk(g_prov.mu);
+    tuning = g_prov.tuning;
+  }
   Plan pl;
   std::string why;
-  nf_status st = make_plan(op, ins, 2, outs, 1, reinterpret_cast<const uint8_t*>(&pc), sizeof(pc), g_prov.tuning, &pl,
-                           &why);
+  nf_status st = make_plan(op, ins, 2, outs, 1, reinterpret_cast<const uint8_t*>(&pc), sizeof(pc), tuning, &pl, &why);
   if (st != NF_OK) return set_error(st, std::string("noalloc: ") + why);
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t* ptr = nullptr;
@@ -1294,7 +1322,7 @@ NF_API nf_status nf_hip_fused_linear_noalloc(nf_dtype wtype, const void* A, cons
   bc.dev = C;
   Buffer* in[2] = {&ba, &bw};
   Buffer* out[1] = {&bc};
-  const hipError_t e = run_plan(pl, in, out, g_prov.tuning.gemm_tile, ws, s);
+  const hipError_t e = run_plan(pl, in, out, tuning.gemm_tile, ws, s);
   return e == hipSuccess ? NF_OK : map_hip(e, (std::string("noalloc launch ") + pl.kernel).c_str());
 }
 

@@ -357,10 +357,12 @@ static void *fused_worker(void *arg) {
     return NULL;
 }
 
-static void fused_run(const void *A, const uint8_t *W, int qfmt, int f16, void *C, uint32_t M,
-                      uint32_t N, uint32_t K, uint32_t n0, uint32_t n1, uint32_t threads) {
+/* 0 on success; -1 when a working buffer could not be allocated (the
+ * output is then incomplete, and the caller must not use it). */
+static int fused_run(const void *A, const uint8_t *W, int qfmt, int f16, void *C, uint32_t M,
+                     uint32_t N, uint32_t K, uint32_t n0, uint32_t n1, uint32_t threads) {
     if (n1 > N) n1 = N;
-    if (n0 >= n1) return;
+    if (n0 >= n1) return 0;
     if (threads < 1) threads = 1;
     if (threads > n1 - n0) threads = n1 - n0;
     if (threads > 256) threads = 256;
@@ -369,7 +371,7 @@ static void fused_run(const void *A, const uint8_t *W, int qfmt, int f16, void *
     if (f16) {
         const uint64_t n = (uint64_t)M * K;
         a32 = (float *)malloc(sizeof(float) * (n ? n : 1));
-        if (!a32) return;
+        if (!a32) return -1;
         for (uint64_t i = 0; i < n; ++i) a32[i] = nf_oracle_f16_to_f32(((const uint16_t *)A)[i]);
     }
     fused_job jobs[256];
@@ -388,23 +390,36 @@ static void fused_run(const void *A, const uint8_t *W, int qfmt, int f16, void *
         j->n0 = n0 + (uint32_t)((uint64_t)span * t / threads);
         j->n1 = n0 + (uint32_t)((uint64_t)span * (t + 1) / threads);
     }
+    int failed = 0;
     if (threads == 1) {
-        fused_worker(&jobs[0]);
+        failed = fused_worker(&jobs[0]) != NULL;
     } else {
-        for (uint32_t t = 0; t < threads; ++t) pthread_create(&tids[t], NULL, fused_worker, &jobs[t]);
-        for (uint32_t t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
+        uint32_t started = 0;
+        for (uint32_t t = 0; t < threads; ++t) {
+            if (pthread_create(&tids[t], NULL, fused_worker, &jobs[t]) != 0) {
+                failed = 1;
+                break;
+            }
+            ++started;
+        }
+        for (uint32_t t = 0; t < started; ++t) {
+            void *r = NULL;
+            pthread_join(tids[t], &r);
+            failed |= r != NULL;
+        }
     }
     free(a32);
+    return failed ? -1 : 0;
 }
 
-void nf_oracle_fused_f32(const float *A, const uint8_t *W, int qfmt, float *C, uint32_t M,
-                         uint32_t N, uint32_t K, uint32_t n0, uint32_t n1, uint32_t threads) {
-    fused_run(A, W, qfmt, 0, C, M, N, K, n0, n1, threads);
+int nf_oracle_fused_f32(const float *A, const uint8_t *W, int qfmt, float *C, uint32_t M,
+                        uint32_t N, uint32_t K, uint32_t n0, uint32_t n1, uint32_t threads) {
+    return fused_run(A, W, qfmt, 0, C, M, N, K, n0, n1, threads);
 }
 
-void nf_oracle_fused_f16(const uint16_t *A, const uint8_t *W, int qfmt, uint16_t *C, uint32_t M,
-                         uint32_t N, uint32_t K, uint32_t n0, uint32_t n1, uint32_t threads) {
-    fused_run(A, W, qfmt, 1, C, M, N, K, n0, n1, threads);
+int nf_oracle_fused_f16(const uint16_t *A, const uint8_t *W, int qfmt, uint16_t *C, uint32_t M,
+                        uint32_t N, uint32_t K, uint32_t n0, uint32_t n1, uint32_t threads) {
+    return fused_run(A, W, qfmt, 1, C, M, N, K, n0, n1, threads);
 }
 
 /* ---- layer ops around the linears ---------------------------------------- */
@@ -639,13 +654,13 @@ static float attn_dot(const void *Q, uint64_t qrow, const void *K, int64_t krow,
     return dot;
 }
 
-void nf_oracle_attention(const uint32_t *P, int f16, const void *Q, const void *K_new, const void *V_new, void *K,
-                         void *V, const uint32_t *table, void *out) {
+int nf_oracle_attention(const uint32_t *P, int f16, const void *Q, const void *K_new, const void *V_new, void *K,
+                        void *V, const uint32_t *table, void *out) {
     const uint32_t mode = P[0], variant = P[1], H = P[2], KV = P[3], D = P[4], S = P[5], step = P[6];
     const uint32_t max_seq = P[7], window = P[8], bs = P[9], n_blocks = P[10];
     const int decode = mode != 0 && step > 0;
     if (mode == 1 || mode == 2) {
-        if (decode && step >= max_seq) return;
+        if (decode && step >= max_seq) return 0;
         const uint32_t tokens = decode ? 1 : S, first = decode ? step : 0;
         for (uint32_t kvh = 0; kvh < KV; ++kvh)
             for (uint32_t t = 0; t < tokens; ++t)
@@ -658,7 +673,8 @@ void nf_oracle_attention(const uint32_t *P, int f16, const void *Q, const void *
     }
     const float scale = 1.0f / sqrtf((float)D);
     const uint32_t nq = decode ? 1 : S;
-    float *acc = (float *)malloc(sizeof(float) * D);
+    float *acc = (float *)malloc(sizeof(float) * (D ? D : 1));
+    if (!acc) return -1;
     for (uint32_t q = 0; q < nq; ++q)
         for (uint32_t h = 0; h < H; ++h) {
             const uint32_t kvh = (uint32_t)((uint64_t)h * KV / H);
@@ -730,4 +746,5 @@ void nf_oracle_attention(const uint32_t *P, int f16, const void *Q, const void *
             for (uint32_t d = 0; d < D; ++d) st_t(out, qrow + d, acc[d] * res_scale, f16);
         }
     free(acc);
+    return 0;
 }

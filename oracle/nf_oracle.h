@@ -95,8 +95,8 @@ void nf_oracle_embedding(const void *w, uint32_t vocab, const int32_t *ids, void
                          uint32_t seq_len, int f16);
 /* prm = {mode, variant, n_heads, n_kv, head_dim, seq_len, step, max_seq,
  * window, block_size, n_blocks, q_offset, pool_blocks}; see nf_oracle.c. */
-void nf_oracle_attention(const uint32_t *prm, int f16, const void *Q, const void *K_new, const void *V_new,
-                         void *K, void *V, const uint32_t *table, void *out);
+int nf_oracle_attention(const uint32_t *prm, int f16, const void *Q, const void *K_new, const void *V_new,
+                        void *K, void *V, const uint32_t *table, void *out);
 
 /* C[M,N] = A[M,K] * B[N,K]^T, fp32 accumulation in k order. */
 void nf_oracle_linear_f32(const float *A, const float *B, float *C,
@@ -107,13 +107,15 @@ void nf_oracle_linear_f16(const uint16_t *A, const uint16_t *B, uint16_t *C,
 
 /* Fused dequant + linear over the output columns n in [n0, n1); the other
  * columns of C are left untouched.  qfmt is NF_ORACLE_Q4_0 / NF_ORACLE_Q8_0.
- * threads > 1 partitions the columns across pthreads (same arithmetic). */
-void nf_oracle_fused_f32(const float *A, const uint8_t *W, int qfmt, float *C,
-                         uint32_t M, uint32_t N, uint32_t K,
-                         uint32_t n0, uint32_t n1, uint32_t threads);
-void nf_oracle_fused_f16(const uint16_t *A, const uint8_t *W, int qfmt, uint16_t *C,
-                         uint32_t M, uint32_t N, uint32_t K,
-                         uint32_t n0, uint32_t n1, uint32_t threads);
+ * threads > 1 partitions the columns across pthreads (same arithmetic).
+ * Returns 0, or -1 when a working buffer or thread could not be had (the
+ * output is then incomplete). */
+int nf_oracle_fused_f32(const float *A, const uint8_t *W, int qfmt, float *C,
+                        uint32_t M, uint32_t N, uint32_t K,
+                        uint32_t n0, uint32_t n1, uint32_t threads);
+int nf_oracle_fused_f16(const uint16_t *A, const uint8_t *W, int qfmt, uint16_t *C,
+                        uint32_t M, uint32_t N, uint32_t K,
+                        uint32_t n0, uint32_t n1, uint32_t threads);
 
 #ifdef __cplusplus
 }

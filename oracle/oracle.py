@@ -63,7 +63,9 @@ def lib() -> C.CDLL:
         L.nf_oracle_linear_f32.argtypes = [f32p, f32p, f32p, C.c_uint32, C.c_uint32, C.c_uint32]
         L.nf_oracle_linear_f16.argtypes = [u16p, u16p, u16p, C.c_uint32, C.c_uint32, C.c_uint32]
         L.nf_oracle_fused_f32.argtypes = [f32p, u8p, C.c_int, f32p] + [C.c_uint32] * 6
+        L.nf_oracle_fused_f32.restype = C.c_int
         L.nf_oracle_fused_f16.argtypes = [u16p, u8p, C.c_int, u16p] + [C.c_uint32] * 6
+        L.nf_oracle_fused_f16.restype = C.c_int
         _lib = L
     return _lib
 
@@ -153,11 +155,13 @@ def fused(A, W, fmt: str, M, N, K, f16: bool = False, cols=None, threads: int = 
         A = np.ascontiguousarray(np.asarray(A).view(np.uint16) if np.asarray(A).dtype == np.float16
                                  else A, np.uint16).reshape(-1)
         out = np.zeros(M * N, np.uint16)
-        lib().nf_oracle_fused_f16(A, W, FMT[fmt], out, M, N, K, n0, n1, threads)
+        rc = lib().nf_oracle_fused_f16(A, W, FMT[fmt], out, M, N, K, n0, n1, threads)
     else:
         A = np.ascontiguousarray(A, np.float32).reshape(-1)
         out = np.zeros(M * N, np.float32)
-        lib().nf_oracle_fused_f32(A, W, FMT[fmt], out, M, N, K, n0, n1, threads)
+        rc = lib().nf_oracle_fused_f32(A, W, FMT[fmt], out, M, N, K, n0, n1, threads)
+    if rc != 0:
+        raise MemoryError(f"oracle fused {fmt} {M}x{N}x{K}: working buffer or thread allocation failed")
     return out.reshape(M, N)
 
 
@@ -197,6 +201,7 @@ def _layer_lib():
         L.nf_oracle_moe_scatter.argtypes = [vp, u32, vp, vp, vp, u32, u32, u32]
         L.nf_oracle_embedding.argtypes = [vp, u32, vp, vp, u64, u32, u32, i]
         L.nf_oracle_attention.argtypes = [vp, i, vp, vp, vp, vp, vp, vp, vp]
+        L.nf_oracle_attention.restype = C.c_int
         L._layer_ready = True
     return L
 
@@ -297,6 +302,8 @@ def attention(op: str, prm: dict, q, k_new=None, v_new=None, k=None, v=None, tab
     tb = None if table is None else np.ascontiguousarray(table, np.uint32)
     assert out is not None and out.flags.c_contiguous
     ptr = lambda a: None if a is None else a.ctypes.data  # noqa: E731
-    _layer_lib().nf_oracle_attention(P.ctypes.data, int(f16), q.ctypes.data, ptr(bufs[0]), ptr(bufs[1]),
-                                     k.ctypes.data, v.ctypes.data, ptr(tb), out.ctypes.data)
+    rc = _layer_lib().nf_oracle_attention(P.ctypes.data, int(f16), q.ctypes.data, ptr(bufs[0]), ptr(bufs[1]),
+                                          k.ctypes.data, v.ctypes.data, ptr(tb), out.ctypes.data)
+    if rc != 0:
+        raise MemoryError(f"oracle attention {op}: working buffer allocation failed")
     return out

@@ -13,8 +13,10 @@
 // Threads split the output rows n; each thread dequantizes the weight rows it
 // owns into a private fp32 row (the reference dequantizes the whole matrix
 // first; per row keeps the working set in cache and does the same work).
-// Built twice by oracle/Makefile, for x86-64-v3 and x86-64-v4, so the bench
-// host runs the widest variant its CPU supports.  The test's main refers to
+// Built twice by oracle/Makefile: with the reference's own Release flags
+// (-O3 -DNDEBUG, no -march), which bench.py times as the cpu_baseline, and
+// for x86-64-v3 (AVX2 + FMA), reported beside it when the host CPU has
+// those features.  The test's main refers to
 // the provider's registration entry points, so the library links against
 // libnf_plugin_hip.so, whose code it never calls.
 #define main nf_ref_dequant_test_main

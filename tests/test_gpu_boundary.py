@@ -254,3 +254,39 @@ def test_diag_stream_read(provider):
         provider.diag_stream_read(b.device_ptr() + 4, 1024)
     assert e.value.status == abi.NF_ERROR_INVALID_ARG
     b.release()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 256), (16, 1024, 4096)], ids=["gemv", "skinny_splitk"])
+def test_graph_replay_then_read(provider, oracle_mod, M, N, K):
+    """Dispatches captured into a HIP graph on the provider stream
+    (nf_hip_get_stream) and replayed there by the caller: a download or
+    nf_hip_buffer_read right after each replay, with no synchronize in
+    between, sees that replay's result.  The activations change between
+    replays (an upload, eager work of the provider's own), and every replay
+    is checked against an eager dispatch of the same inputs and the oracle."""
+    from neurofabric_amd import hiprt
+    W = syn.q4_0_weights(N, K, seed=5)
+    a = provider.alloc(abi.NF_DTYPE_F32, M * K * 4)
+    w = provider.alloc_array(W, abi.NF_DTYPE_Q4_0)
+    c = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    c_eager = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    try:
+        a.upload(syn.activations(M, K, seed=100))
+        provider.dispatch("dequant_q4_0_linear", [a, w], [c], M, N, K)  # warm (any one-time set-up)
+        provider.synchronize()
+        g = hiprt.Graph(provider.stream(), lambda: provider.dispatch("dequant_q4_0_linear", [a, w], [c], M, N, K))
+        for i in range(4):
+            A = syn.activations(M, K, seed=200 + i)
+            a.upload(A)
+            print(f"graph replay {i} M={M} N={N} K={K}", flush=True)
+            g.launch()
+            got = c.download(np.float32) if i % 2 == 0 else c.read(np.float32)
+            provider.dispatch("dequant_q4_0_linear", [a, w], [c_eager], M, N, K)
+            eager = c_eager.download(np.float32)
+            assert np.array_equal(got, eager), f"replay {i}: graph result differs from eager dispatch"
+            assert_close(got.reshape(M, N), oracle_mod.fused(A, W, "q4_0", M, N, K), what=f"replay {i}")
+        del g
+    finally:
+        provider.synchronize()
+        for b in (a, w, c, c_eager):
+            b.release()

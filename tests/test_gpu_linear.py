@@ -521,3 +521,56 @@ def test_dense_linear_decode_gemv(provider, oracle_mod, adt, bdt, cdt, M, N, K):
     assert_close(got, ref)
     for x in (a, b, c):
         x.release()
+
+
+def _import_at(provider, base, offset, dtype, nbytes):
+    """A non-owning buffer over `nbytes` of `base`'s memory from byte
+    `offset` on (an imported DEVICE token, neuro_buffer_abi.h:165-183)."""
+    import ctypes as C
+    from neurofabric_amd.plugin import Buffer
+    ops, h = abi.nf_buffer_ops(), C.c_void_p()
+    desc = abi.make_desc(dtype, nbytes)
+    st = provider.mem.import_buffer(provider.handle, base.device_ptr() + offset, abi.NF_MEM_DOMAIN_DEVICE,
+                                    C.byref(desc), C.byref(ops), C.byref(h))
+    assert st == abi.NF_OK, provider.last_error()
+    return Buffer(provider, h.value, ops, dtype, nbytes)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("M", [128, 24, 2])
+@pytest.mark.parametrize("a_off,w_off", [(4, 0), (0, 2)], ids=["A+4", "W+2"])
+def test_fused_f32_misaligned_operands(provider, oracle_mod, fmt, M, a_off, w_off):
+    """f32 activations 4 bytes past a 16-byte boundary, or weights 2 bytes
+    past a dword, as imported buffers at odd offsets give them: every batch
+    size (the MFMA kernels need aligned operands, so these run on the GEMV's
+    block kernel) matches the oracle, through dispatch and through the
+    no-allocation entry point on the same raw pointers."""
+    import ctypes as C
+    N, K = 512, 4096
+    W = syn.weights(fmt, N, K, seed=M + a_off)
+    A = syn.activations(M, K, seed=M + 1)
+    a_raw = provider.alloc_array(np.concatenate([np.zeros(a_off, np.uint8), A.reshape(-1).view(np.uint8)]),
+                                 abi.NF_DTYPE_U8)
+    w_raw = provider.alloc_array(np.concatenate([np.zeros(w_off, np.uint8), W.reshape(-1).view(np.uint8)]),
+                                 abi.NF_DTYPE_U8)
+    a = _import_at(provider, a_raw, a_off, abi.NF_DTYPE_F32, A.nbytes)
+    w = _import_at(provider, w_raw, w_off, QDT[fmt], W.nbytes)
+    c = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    c2 = provider.alloc(abi.NF_DTYPE_F32, M * N * 4)
+    try:
+        print(f"misaligned f32 {fmt} M={M} A+{a_off} W+{w_off}", flush=True)
+        provider.dispatch(f"dequant_{fmt}_linear", [a, w], [c], M, N, K)
+        fn = provider.lib.nf_hip_fused_linear_noalloc
+        fn.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_bool,
+                       C.c_void_p]
+        fn.restype = C.c_int
+        st = fn(QDT[fmt], a_raw.device_ptr() + a_off, w_raw.device_ptr() + w_off, c2.device_ptr(), M, N, K, False,
+                provider.stream())
+        assert st == abi.NF_OK, provider.last_error()
+        provider.synchronize()
+        ref = oracle_mod.fused(A, W, fmt, M, N, K, threads=8)
+        assert_close(c.download(np.float32).reshape(M, N), ref, what=f"dispatch {fmt} M={M}")
+        assert_close(c2.download(np.float32).reshape(M, N), ref, what=f"noalloc {fmt} M={M}")
+    finally:
+        for b in (a, w, a_raw, w_raw, c, c2):
+            b.release()

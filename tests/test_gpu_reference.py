@@ -35,6 +35,23 @@ def test_reference_kquant_dequant_test_binary_passes():
     assert "OK: all Phase 25 K-quant dequant tests passed" in r.stdout
 
 
+REF_FUSED = REPO / "oracle" / "_ref" / "fused_matmul_test"
+
+
+@pytest.mark.skipif(not REF_FUSED.exists(), reason="reference test binary not built (needs the reference sources)")
+def test_reference_fused_matmul_test_binary_passes():
+    """tests/driver/fused_matmul_test.cpp, unedited (oracle/ref_fused.cpp
+    renames its `sync` around the #include): the fused ops against the
+    separate dequant -> linear_tiled / linear pipeline at (4, 8, 32),
+    (5, 7, 64), (64, 128, 256) f32 and (64, 128, 256) f16, dispatched with its
+    FakeTaskDesc push constants (fused_matmul_test.cpp:108-126, 287-300)."""
+    r = subprocess.run([str(REF_FUSED)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0
+    assert r.stdout.count("PASS") == 4 and "FAIL" not in r.stdout
+    assert "=== 4/4 tests passed ===" in r.stdout
+
+
 # The reference's other driver tests this provider serves, with the line each
 # prints when every check passed (tests/driver/<name>.cpp).
 REF_LAYER_TESTS = {

@@ -8,9 +8,10 @@ static array keeps the first call's partials and counters), and checks both
 against each other and against the CPU oracle within max relative error
 1e-3 (tests/helpers.py).  Shapes cover every kernel family the planner
 picks: the decode GEMV, the small-batch MFMA kernel with K split across
-workgroups (partials and counters in the scratch), the tiled GEMM whose K
-split would need more partials than the scratch holds (runs with fewer
-splits), and the flat-index kernel for K % 32 != 0.
+workgroups (partials and counters in the scratch), the tiled fp16 GEMM whose
+K split would need more partials than the scratch holds (runs with fewer
+splits), the f32 tiled GEMM with a K split, and the flat-index kernel for
+K % 32 != 0.
 """
 import ctypes as C
 
@@ -68,13 +69,16 @@ def orc_fused(A, W, fmt, M, N, K, f16, cols):
 
 
 # (fmt, f16, first shape, second smaller shape): decode GEMV; small-batch MFMA
-# with a cross-workgroup K split; tiled GEMM whose split would need 32 MB of
-# partials; ragged K on the flat-index kernel.
+# with a cross-workgroup K split; tiled fp16 GEMM whose split would need
+# 32 MB of partials; the f32 bf16-piece tiled GEMM with its K split (partials
+# and counters in the scratch, twice in a row); ragged K on the flat-index
+# kernel.
 CASES = [
     ("q4_0", False, (1, 5632, 2048), (1, 256, 2048)),
     ("q8_0", True, (16, 4096, 4096), (8, 1024, 4096)),
     ("q4_0", False, (24, 2048, 5632), (5, 300, 1024)),
     ("q4_0", True, (512, 4096, 4096), (256, 1024, 4096)),
+    ("q4_0", False, (128, 4096, 4096), (96, 1024, 4096)),
     ("q8_0", False, (3, 70, 96), (2, 33, 48)),
 ]
 
