@@ -109,12 +109,19 @@ template <> struct XChunk<half_t> {
 };
 
 // Chunk c of activation pair gp = m * P + pair (the pair's index over all
-// M rows) lives at slot gp * cp + (c ^ (gp & (cp - 1))).
+// M rows) lives at slot gp * (cp + 1) + c: each pair's chunks are followed
+// by one chunk of padding.  The 16 lanes of one ds_read_b128 phase read
+// chunk c of 16 consecutive pairs; with pairs 272 B (f32) or 144 B (f16)
+// apart they fall in 16 different 16-byte bank groups of the 256-byte bank
+// row (17 and 9 are odd), so the reads are conflict-free and every chunk of
+// a pair is the pair's base address plus a constant offset.  (An XOR
+// swizzle of the chunk index is conflict-free too but costs address
+// arithmetic per read; f16 pairs swizzled with gp & 7 collided for pairs p
+// and p + 8: 1.8 M bank-conflict cycles per 132 MB launch.)
 template <typename XT>
 __device__ __forceinline__ int xslot(int m, int P, int pair, int c) {
   constexpr int cp = XChunk<XT>::kPerPair;
-  const int gp = m * P + pair;
-  return gp * cp + (c ^ (gp & (cp - 1)));
+  return (m * P + pair) * (cp + 1) + c;
 }
 
 // ---- per-pair compute -----------------------------------------------------
@@ -224,9 +231,32 @@ __device__ __forceinline__ void pair_f32_q8(const uint32_t (&w)[R2][17], const f
 }
 
 __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
+// (q & mask) | bits in one v_and_or_b32.  Its VOP3 encoding cannot carry
+// 32-bit literals and reads at most one scalar register, so the mask comes
+// from a scalar register and the bits from a (loop-invariant) vector one;
+// the compiler otherwise emits a separate AND and OR.
+__device__ __forceinline__ uint32_t and_or(uint32_t q, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(q), "s"(mask), "v"(bits));
+  return r;
+}
 __device__ __forceinline__ uint32_t as_u32(half2v h) { return __builtin_bit_cast(uint32_t, h); }
 
 // f16 activations (weights rounded to fp16 exactly as dequant_*_f16).
+//
+// Q4_0: the four half2 of code dword t come straight from its nibble
+// positions with one AND-OR each, no byte shuffle: a nibble in bits 0-3 of
+// a 16-bit half under exponent bits 0x64 reads as 1024 + n, a nibble in
+// bits 4-7 under 0x54 as 64 + n (fp16 with unit spacing there), so
+//   (q & 0x000F000F) | 0x64006400       -> elements (4t,    4t+2)
+//   (q & 0x00F000F0) | 0x54005400       -> elements (16+4t, 18+4t)
+//   ((q>>8) & 0x000F000F) | 0x64006400  -> elements (4t+1,  4t+3)
+//   ((q>>8) & 0x00F000F0) | 0x54005400  -> elements (17+4t, 19+4t)
+// then one packed add (-1032 / -72: exact, the signed code) and one packed
+// multiply by d (RNE(d*q), the dequant_q4_0_f16 bits).  The staged
+// activations hold each block's chunk t in that element order (stage_f16_q4).
+// Q8_0: each code byte under 0x64 via a byte permute (1024 + 128 + q).
 template <class QF, int R2, int MM>
 __device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kDwords],
                                          const half8* __restrict__ xs, int P, int pair,
@@ -258,25 +288,21 @@ __device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kD
       for (int t = 0; t < qd; ++t) {
         const uint32_t q = code_dword<QF>(w[j], blk, t);
         if constexpr (kQ4) {
-          // bytes 0..3 of q: low nibbles -> elements 4t..4t+3, high -> 16+4t..
-          const uint32_t lo = q & 0x0F0F0F0Fu;
-          const uint32_t hi = (q >> 4) & 0x0F0F0F0Fu;
-          const half2v off = {(half_t)-1032.f, (half_t)-1032.f};
-          const half2v w0 = (as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + off) * d2;
-          const half2v w1 = (as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + off) * d2;
-          const half2v w2 = (as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) + off) * d2;
-          const half2v w3 = (as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) + off) * d2;
+          const uint32_t s8 = q >> 8;
+          const half2v lo_off = {(half_t)-1032.f, (half_t)-1032.f};
+          const half2v hi_off = {(half_t)-72.f, (half_t)-72.f};
+          const half2v w0 = (as_h2(and_or(q, 0x000F000Fu, 0x64006400u)) + lo_off) * d2;
+          const half2v w1 = (as_h2(and_or(q, 0x00F000F0u, 0x54005400u)) + hi_off) * d2;
+          const half2v w2 = (as_h2(and_or(s8, 0x000F000Fu, 0x64006400u)) + lo_off) * d2;
+          const half2v w3 = (as_h2(and_or(s8, 0x00F000F0u, 0x54005400u)) + hi_off) * d2;
 #pragma unroll
           for (int m = 0; m < MM; ++m) {
-            // elements 4t..4t+3 live in chunk t/2, halves 4*(t&1)..; 16+4t.. in chunk 2+t/2
-            const half8 xl = xv[m][t >> 1];
-            const half8 xh = xv[m][2 + (t >> 1)];
-            const int o = (t & 1) * 4;
+            const half8 xc = xv[m][t];
             float v = part[t & 3][j][m];
-            v = __builtin_amdgcn_fdot2(w0, half2v{xl[o + 0], xl[o + 1]}, v, false);
-            v = __builtin_amdgcn_fdot2(w1, half2v{xl[o + 2], xl[o + 3]}, v, false);
-            v = __builtin_amdgcn_fdot2(w2, half2v{xh[o + 0], xh[o + 1]}, v, false);
-            v = __builtin_amdgcn_fdot2(w3, half2v{xh[o + 2], xh[o + 3]}, v, false);
+            v = __builtin_amdgcn_fdot2(w0, half2v{xc[0], xc[1]}, v, false);
+            v = __builtin_amdgcn_fdot2(w1, half2v{xc[2], xc[3]}, v, false);
+            v = __builtin_amdgcn_fdot2(w2, half2v{xc[4], xc[5]}, v, false);
+            v = __builtin_amdgcn_fdot2(w3, half2v{xc[6], xc[7]}, v, false);
             part[t & 3][j][m] = v;
           }
         } else {
@@ -305,6 +331,22 @@ __device__ __forceinline__ void pair_f16(const uint32_t (&w)[R2][PairFmt<QF>::kD
       acc[j][m] += (part[0][j][m] + part[1][j][m]) + (part[2][j][m] + part[3][j][m]);
 }
 
+// The Q4_0 f16 order of one 32-element block of activations: chunk t (t = 0..3)
+// = (x[4t], x[4t+2]), (x[16+4t], x[18+4t]), (x[4t+1], x[4t+3]), (x[17+4t], x[19+4t]),
+// from the block's four consecutive 8-element chunks v[0..3].
+__device__ __forceinline__ half8 q4_f16_chunk(const half8 (&v)[4], int t) {
+  const u32x4 a = __builtin_bit_cast(u32x4, v[t >> 1]);
+  const u32x4 b = __builtin_bit_cast(u32x4, v[2 + (t >> 1)]);
+  const uint32_t a0 = (t & 1) ? a.z : a.x, a1 = (t & 1) ? a.w : a.y;  // x[4t..4t+1], x[4t+2..4t+3]
+  const uint32_t b0 = (t & 1) ? b.z : b.x, b1 = (t & 1) ? b.w : b.y;
+  u32x4 o;
+  o.x = __builtin_amdgcn_perm(a1, a0, 0x05040100u);  // low halves: x[4t], x[4t+2]
+  o.y = __builtin_amdgcn_perm(b1, b0, 0x05040100u);
+  o.z = __builtin_amdgcn_perm(a1, a0, 0x07060302u);  // high halves: x[4t+1], x[4t+3]
+  o.w = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+  return __builtin_bit_cast(half8, o);
+}
+
 // ---- cross-lane sums --------------------------------------------------------
 
 template <int CTRL, int ROW_MASK = 0xF>
@@ -330,8 +372,11 @@ __device__ __forceinline__ float group_sum(float v, int log2L) {
 // ---- the pair kernel ------------------------------------------------------
 
 // Up to kGroupMax GEMVs over the same activations in one launch: job j owns
-// workgroups begin[j] .. begin[j+1]-1 and runs on its own weights, output and
-// N exactly as a launch of its own would (same geometry, same results).
+// workgroups begin[j] .. begin[j+1]-1, a share of the capped grid in
+// proportion to its rows, which loop over the job's rows exactly as the
+// grid of a single launch loops over one matrix's (a single launch is a
+// group of one).  The job is uniform per workgroup, so weight and output
+// bases stay scalar.
 constexpr int kGroupMax = nfhip::kGemvGroupMax;
 struct GemvGroup {
   const uint8_t* W[kGroupMax];
@@ -374,7 +419,7 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
 
   const int P = K >> 6;
   ChunkT* xs = reinterpret_cast<ChunkT*>(smem);
-  float* sxs = reinterpret_cast<float*>(smem + (size_t)MM * P * CP * 16);
+  float* sxs = reinterpret_cast<float*>(smem + (size_t)MM * P * (CP + 1) * 16);
   const int tid = threadIdx.x;
 
   // fp8 e4m3 value of byte 0x01 (the unit step of the nibble trick)
@@ -417,16 +462,59 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   uint32_t wa[R2][DW], wb[R2][DW], wc[R2][DW];  // wc: only with k3Sets
 
   // ---- stage A into LDS (and the per-block sums of x) ----
-  // Thread tid takes 16-byte chunks tid, tid + 256, ... of the M x K
-  // activations, so every load instruction reads contiguous memory.  A
-  // 32-element block is 8 (f32) chunks held by 8 consecutive lanes; its sum
-  // is formed with DPP adds across them (total is a multiple of 8, so the 8
-  // lanes of a block are in or out of range together).  Loads past the end
-  // are clamped to the last chunk and dropped, so no load is predicated and
-  // all eight are in flight together (skipping whole rounds past the end
-  // behind a uniform branch instead measured 542 against 437 us for the
-  // TinyLlama decode step).
-  {
+  // The first two rounds of activations (all of them up to M * K = 16384
+  // f32 / 32768 f16 elements) are requested before the first weights, so
+  // the two memory round trips overlap; the activations go first because
+  // loads complete in issue order: the (L2-resident) activations are then
+  // staged while the weights stream from HBM (measured on MI355X: 3.3
+  // against 3.8 us at 2048 x 2048 with the weights first).  Later rounds,
+  // if any, follow the weights.  Loads past the end are clamped to the last
+  // item and dropped, so no load is predicated and all of a round are in
+  // flight together (skipping whole rounds past the end behind a uniform
+  // branch instead measured 542 against 437 us for the TinyLlama decode
+  // step).
+  if constexpr (!kF32 && kQ4) {
+    // f16 Q4_0: thread tid takes 32-element blocks tid, tid + 256, ... (four
+    // 16-byte loads each) and writes them in the order pair_f16 reads.
+    const int totb = M * P * 2;
+    typedef half8 Blk[2][4];
+    auto load = [&](int b0, Blk& v) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int b = b0 + u * 256 + tid;
+        const half8* src = reinterpret_cast<const half8*>(A + (size_t)(b < totb ? b : totb - 1) * 32);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[u][c] = src[c];
+      }
+    };
+    auto put = [&](int b0, const Blk& v) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int b = b0 + u * 256 + tid;
+        if (b < totb) {
+          const int gp = b >> 1, blk = b & 1;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) xs[gp * (CP + 1) + blk * 4 + t] = q4_f16_chunk(v[u], t);
+        }
+      }
+    };
+    Blk v0, v1;
+    load(0, v0);
+    const bool two = totb > 512;
+    if (two) load(512, v1);
+    if (T > 0) next_load(wa);
+    put(0, v0);
+    if (two) put(512, v1);
+    for (int b0 = 1024; b0 < totb; b0 += 512) {
+      load(b0, v0);
+      put(b0, v0);
+    }
+  } else {
+    // Thread tid takes 16-byte chunks tid, tid + 256, ... of the M x K
+    // activations, so every load instruction reads contiguous memory.  A
+    // 32-element block is 8 (f32) chunks held by 8 consecutive lanes; its
+    // sum is formed with DPP adds across them (total is a multiple of 8, so
+    // the 8 lanes of a block are in or out of range together).
     const int total = M * P * CP;
     auto load = [&](int c0, ChunkT (&v)[8]) {
 #pragma unroll
@@ -441,7 +529,7 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
         const int c = c0 + u * 256 + tid;
         if (c < total) {
           const int gp = c / CP, j = c & (CP - 1);
-          xs[gp * CP + (j ^ (gp & (CP - 1)))] = v[u];
+          xs[gp * (CP + 1) + j] = v[u];
           if constexpr (kSx) {
             float sum = (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
             sum += dpp_f<0xB1>(sum);   // quad_perm [1,0,3,2]
@@ -452,13 +540,6 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
         }
       }
     };
-    // The first two rounds of 2048 chunks (all of them up to M * K = 16384
-    // f32 / 32768 f16 elements) are requested before the first weights, so
-    // the two memory round trips overlap; the activations go first because
-    // loads complete in issue order: the (L2-resident) activations are then
-    // staged while the weights stream from HBM (measured on MI355X: 3.3
-    // against 3.8 us at 2048 x 2048 with the weights first).  Later rounds,
-    // if any, follow the weights.
     ChunkT v0[8], v1[8];
     load(0, v0);
     const bool two = total > 256 * 8;
@@ -673,9 +754,10 @@ inline int pick_log2L(int P) {
   return best;
 }
 
-// Activations staged per workgroup: up to 120 KB of LDS (above 64 KB the
-// kernel has to opt in, once per instantiation).
-constexpr size_t kPairMaxLds = 120 * 1024;
+// Activations staged per workgroup: up to 136 KB of LDS (above 64 KB the
+// kernel has to opt in, once per instantiation): the planner's 120 KB of
+// activations (plan.cpp) plus the padding chunks and the f32 block sums.
+constexpr size_t kPairMaxLds = 136 * 1024;
 
 template <class QF, typename XT, int R2, int MM>
 hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const GemvGroup& grp, uint32_t M, uint32_t K,
@@ -690,32 +772,19 @@ hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const GemvGroup& g
   return hipGetLastError();
 }
 
-template <class QF, typename XT, int R2, int MM>
-hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const void* W, void* C, uint32_t M,
-                            uint32_t N, uint32_t K, hipStream_t s) {
-  GemvGroup grp{};
-  grp.W[0] = static_cast<const uint8_t*>(W);
-  grp.C[0] = C;
-  grp.N[0] = (int)N;
-  grp.begin[0] = 0;
-  for (int q = 1; q <= kGroupMax; ++q) grp.begin[q] = (int)g.grid;
-  grp.count = 1;
-  return gemv_pair_launch<QF, XT, R2, MM>(g, A, grp, M, K, s);
-}
-
+// Geometry of a pair-kernel launch over `rows` rows (one matrix or a whole
+// group) with M activation rows of K; false when its activation stage would
+// not fit in LDS.
 template <class QF, typename XT>
-hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
-                         hipStream_t s) {
+bool pair_geom(uint32_t M, uint32_t K, long rows, PairGeom& g) {
   constexpr bool kF32 = sizeof(XT) == 4;
-  const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
-  if (K % 64 != 0 || M > 4 || !aligned) return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
-  PairGeom g;
   const int P = (int)(K / 64);
   g.MM = M == 1 ? 1 : (M == 2 ? 2 : 4);
-  const size_t xbytes = (size_t)g.MM * P * 64 * (kF32 ? 4 : 2);
+  // staged pairs with one padding chunk each (xslot)
+  const size_t xbytes = (size_t)g.MM * P * ((kF32 ? 16 : 8) + 1) * 16;
   const size_t sxbytes = (kF32 && PairFmt<QF>::kQd == 4) ? (size_t)g.MM * P * 2 * 4 : 0;
   g.lds = xbytes + sxbytes;
-  if (g.lds > kPairMaxLds) return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
+  if (g.lds > kPairMaxLds) return false;
   g.log2L = pick_log2L(P);
   const int R = 64 >> g.log2L;
   // The grid is capped at two workgroups per CU, which loop over the rows
@@ -730,52 +799,75 @@ hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint
     const long v = e ? std::atol(e) : 0;
     return v > 0 ? v : 256L * 2;
   }();
-  const long wgs = ((long)N + 4L * R - 1) / (4L * R);
+  const long wgs = (rows + 4L * R - 1) / (4L * R);
   g.R2 = 1;
   g.grid = (unsigned)(wgs < cap ? wgs : cap);
-  switch (g.MM) {
-    case 1: return gemv_pair_launch<QF, XT, 1, 1>(g, A, W, C, M, N, K, s);
-    case 2: return gemv_pair_launch<QF, XT, 1, 2>(g, A, W, C, M, N, K, s);
-    default: return gemv_pair_launch<QF, XT, 1, 4>(g, A, W, C, M, N, K, s);
-  }
+  return true;
 }
 
-// Geometry shared by the jobs of a group (same M, K): the single-launch
-// rules with one row per lane group; each job gets its own one-pass grid.
 template <class QF, typename XT>
-hipError_t gemv_group_dispatch(const void* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
-                               hipStream_t s) {
-  constexpr bool kF32 = sizeof(XT) == 4;
-  if (n < 1 || n > (uint32_t)kGroupMax || K % 64 != 0 || M < 1 || M > 4 || (uintptr_t)A % 16 != 0)
-    return hipErrorNotSupported;
-  PairGeom g;
-  const int P = (int)(K / 64);
-  g.MM = M == 1 ? 1 : (M == 2 ? 2 : 4);
-  g.lds = (size_t)g.MM * P * 64 * (kF32 ? 4 : 2) + ((kF32 && PairFmt<QF>::kQd == 4) ? (size_t)g.MM * P * 2 * 4 : 0);
-  if (g.lds > kPairMaxLds) return hipErrorNotSupported;
-  g.log2L = pick_log2L(P);
-  const int R = 64 >> g.log2L;
-  GemvGroup grp{};
-  long total = 0;
-  for (uint32_t j = 0; j < n; ++j) {
-    if ((uintptr_t)jobs[j].W % 4 != 0 || jobs[j].N == 0) return hipErrorNotSupported;
-    const long wgs1 = ((long)jobs[j].N + 4L * R - 1) / (4L * R);
-    if (wgs1 > 256L * 4) return hipErrorNotSupported;  // a single launch would loop over rows instead
-    grp.W[j] = static_cast<const uint8_t*>(jobs[j].W);
-    grp.C[j] = jobs[j].C;
-    grp.N[j] = (int)jobs[j].N;
-    grp.begin[j] = (int)total;
-    total += wgs1;
-  }
-  for (int q = (int)n; q <= kGroupMax; ++q) grp.begin[q] = (int)total;
-  grp.count = (int)n;
-  g.R2 = 1;
-  g.grid = (unsigned)total;
+hipError_t gemv_pair_group(const PairGeom& g, const void* A, const GemvGroup& grp, uint32_t M, uint32_t K,
+                           hipStream_t s) {
   switch (g.MM) {
     case 1: return gemv_pair_launch<QF, XT, 1, 1>(g, A, grp, M, K, s);
     case 2: return gemv_pair_launch<QF, XT, 1, 2>(g, A, grp, M, K, s);
     default: return gemv_pair_launch<QF, XT, 1, 4>(g, A, grp, M, K, s);
   }
+}
+
+template <class QF, typename XT>
+hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint32_t N, uint32_t K,
+                         hipStream_t s) {
+  const bool aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)W % 4 == 0);
+  PairGeom g;
+  if (K % 64 != 0 || M > 4 || !aligned || !pair_geom<QF, XT>(M, K, (long)N, g))
+    return gemv_block_dispatch<QF, XT>(A, W, C, M, N, K, s);
+  GemvGroup grp{};
+  grp.W[0] = static_cast<const uint8_t*>(W);
+  grp.C[0] = C;
+  grp.N[0] = (int)N;
+  grp.begin[0] = 0;
+  for (int q = 1; q <= kGroupMax; ++q) grp.begin[q] = (int)g.grid;
+  grp.count = 1;
+  return gemv_pair_group<QF, XT>(g, A, grp, M, K, s);
+}
+
+// A group: the geometry of a single matrix with all the jobs' rows, its
+// capped grid split among the jobs in proportion to their rows (at least
+// one workgroup each, never more than a job's rows need).
+template <class QF, typename XT>
+hipError_t gemv_group_dispatch(const void* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
+                               hipStream_t s) {
+  if (n < 1 || n > (uint32_t)kGroupMax || K % 64 != 0 || M < 1 || M > 4 || (uintptr_t)A % 16 != 0)
+    return hipErrorNotSupported;
+  long total = 0;
+  for (uint32_t j = 0; j < n; ++j) {
+    if ((uintptr_t)jobs[j].W % 4 != 0 || jobs[j].N == 0) return hipErrorNotSupported;
+    total += jobs[j].N;
+  }
+  PairGeom g;
+  if (!pair_geom<QF, XT>(M, K, total, g)) return hipErrorNotSupported;
+  const long rows_per_wg = 4L * (64 >> g.log2L);
+  GemvGroup grp{};
+  long wg = 0, rows_before = 0;
+  for (uint32_t j = 0; j < n; ++j) {
+    grp.W[j] = static_cast<const uint8_t*>(jobs[j].W);
+    grp.C[j] = jobs[j].C;
+    grp.N[j] = (int)jobs[j].N;
+    grp.begin[j] = (int)wg;
+    // workgroups [begin_j, begin_j+1): job j's share of the grid, rounded at
+    // the running row total so the shares add up to the grid
+    rows_before += jobs[j].N;
+    long end = (long)((double)g.grid * (double)rows_before / (double)total + 0.5);
+    const long need = ((long)jobs[j].N + rows_per_wg - 1) / rows_per_wg;
+    if (end < wg + 1) end = wg + 1;
+    if (end > wg + need) end = wg + need;
+    wg = end;
+  }
+  for (int q = (int)n; q <= kGroupMax; ++q) grp.begin[q] = (int)wg;
+  grp.count = (int)n;
+  g.grid = (unsigned)wg;
+  return gemv_pair_group<QF, XT>(g, A, grp, M, K, s);
 }
 
 // ---- launch-floor calibration ------------------------------------------------

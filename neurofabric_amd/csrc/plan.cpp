@@ -175,11 +175,14 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
       const bool f16 = p.c == EType::F16;
       const uint32_t gemv_max = f16 ? tuning.gemv_max_m_f16 : tuning.gemv_max_m_f32;
       // The GEMV stages M' x K activations per workgroup (M' = M rounded up
-      // to 1, 2 or 4) plus f32 Q4_0 block sums; beyond 120 KB of LDS it would
-      // fall back to its slow block kernel, so the MFMA kernel takes over.
+      // to 1, 2 or 4), each 64-element pair followed by one 16-byte padding
+      // chunk (kernels/gemv.hip: xslot), plus f32 Q4_0 block sums; beyond
+      // 136 KB of LDS it would fall back to its slow block kernel, so the
+      // MFMA kernel takes over.
       const uint64_t mm = p.M <= 2 ? p.M : 4;
-      const uint64_t stage = mm * K * elt_bytes(p.a) + ((!f16 && p.q == QFmt::Q4_0) ? mm * (K / 64) * 8 : 0);
-      const bool gemv_fits = K % 64 != 0 || stage <= 120 * 1024;
+      const uint64_t stage = mm * (K / 64) * (64 * elt_bytes(p.a) + 16) +
+                             ((!f16 && p.q == QFmt::Q4_0) ? mm * (K / 64) * 8 : 0);
+      const bool gemv_fits = K % 64 != 0 || stage <= 136 * 1024;
       // Two rows: the GEMV only while two of its workgroups fit a CU's LDS
       // (stage <= gemv_m2_max_stage_bytes, 80 KB); past that the small-batch kernel is as fast
       // (8192x28672 f16, 112 KB stage: 46.3 against 47.9 us; 28672x8192

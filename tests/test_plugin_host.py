@@ -325,8 +325,9 @@ def test_gemv_row_limits(lib):
     lib.nf_hip_get_gemv_row_limits(C.byref(st), C.byref(wb))
     assert (st.value, wb.value) == (80 * 1024, 16 << 20)
     try:
-        lib.nf_hip_set_gemv_row_limits(C.c_uint32(120 * 1024), C.c_uint64(200 << 20))
-        assert _fused(lib, 2, 8192, 28672, **f16)["kernel"] == "gemv_q4_0_f16"   # 112 KB stage
+        lib.nf_hip_set_gemv_row_limits(C.c_uint32(130 * 1024), C.c_uint64(200 << 20))
+        # 2 x 28672 f16 activations staged with one padding chunk per pair: 129 KB
+        assert _fused(lib, 2, 8192, 28672, **f16)["kernel"] == "gemv_q4_0_f16"
         assert _fused(lib, 4, 28672, 8192, **f16)["kernel"] == "gemv_q4_0_f16"   # 132 MB
         lib.nf_hip_set_gemv_row_limits(C.c_uint32(0), C.c_uint64(0))
         assert _fused(lib, 2, 28672, 8192, **f16)["kernel"] == "skinny_mfma_q4_0_f16"
