@@ -34,12 +34,11 @@
 //     reusing the staged activations.
 //
 // Unpacking (per 32-bit word of codes = 8 Q4_0 codes / 4 Q8_0 codes):
-//   f32, Q4_0: low and high nibbles are masked into bytes 0..15; bytes 0..15
-//       read as OCP/FNUZ fp8 e4m3 are exactly n * u (u = 2^-9 or 2^-10, the
-//       value of byte 0x01, measured in-kernel), so v_cvt_pk_f32_fp8 turns two
-//       codes into two exact floats per instruction.  The "-8" offset is
-//       applied once per block: sum (n-8) x = (sum n*u*x - 8*u*sum x) / u,
-//       with sum x per block precomputed during staging.
+//   f32, Q4_0: the nibbles are masked in place into fp16 subnormals (n *
+//       2^-24 or n * 2^-20) that v_fma_mix_f32 multiplies by the f32
+//       activations exactly (pair_f32_q4).  The "-8" offset is applied once
+//       per block: sum (n-8) x = sum n x - 8 sum x, with sum x per block
+//       precomputed during staging.
 //   f32, Q8_0: v_cvt_f32_i32 with SDWA byte select and sign extension.
 //   f16: bytes are placed under 0x64 (fp16 1024 + n), shifted to the signed
 //       code with one packed f16 add (exact), and multiplied by the fp16 scale
@@ -57,6 +56,9 @@ namespace nfk {
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+__device__ __forceinline__ uint32_t as_u32(half2v h) { return __builtin_bit_cast(uint32_t, h); }
 
 template <class QF> struct PairFmt;
 template <> struct PairFmt<Q4_0> {
@@ -126,11 +128,23 @@ __device__ __forceinline__ int xslot(int m, int P, int pair, int c) {
 
 // ---- per-pair compute -----------------------------------------------------
 
-// f32 activations, Q4_0.
+// f32 activations, Q4_0.  Masking a code dword leaves each nibble as an
+// fp16 subnormal: (q & 0x000F000F) holds n * 2^-24 for elements (4t, 4t+2),
+// (q & 0x00F000F0) 16n * 2^-24 = n * 2^-20 for (16+4t, 18+4t), and the same
+// masks of q >> 8 the odd elements.  v_fma_mix_f32 widens an fp16 half to
+// f32 inside the FMA (exactly, subnormals included: checked on MI355X for
+// every nibble in both positions), so each product code * x is exact and
+// rounded once into its fp32 chain: 5 instructions place 8 codes (against
+// 7 for masking into bytes and four fp8 conversions).  Elements 16..31 of
+// every block are staged divided by 16 (exact), so the 2^-20 codes times
+// them count in the same units, 2^-24, as the rest; the block value is
+// d * 2^24 * (sum - 8 * 2^-24 * sum x), the last term staged per block.
+constexpr float kCodeUnit = 0x1p-24f;
+
 template <int R2, int MM>
 __device__ __forceinline__ void pair_f32_q4(const uint32_t (&w)[R2][9], const float4v* __restrict__ xs,
                                             const float* __restrict__ sxs, int P, int pair,
-                                            float inv_unit, float (&acc)[R2][MM]) {
+                                            float (&acc)[R2][MM]) {
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     // four independent FMA chains per block (one per code dword), added at
@@ -149,34 +163,35 @@ __device__ __forceinline__ void pair_f32_q4(const uint32_t (&w)[R2][9], const fl
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float4v* xl = xa[t];
-      const float4v* xh = xb[t];
+      const float4v* xl = xa[t];  // x[4t .. 4t+3]
+      const float4v* xh = xb[t];  // x[16+4t .. 16+4t+3] / 16
 #pragma unroll
       for (int j = 0; j < R2; ++j) {
         const uint32_t q = code_dword<Q4_0>(w[j], blk, t);
-        const uint32_t lo = q & 0x0F0F0F0Fu;
-        const uint32_t hi = (q >> 4) & 0x0F0F0F0Fu;
-        const float2v a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-        const float2v b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-        const float2v c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-        const float2v e = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+        const uint32_t q8 = q >> 8;
+        const half2v ev_lo = as_h2(q & 0x000F000Fu);   // elements 4t, 4t+2
+        const half2v ev_hi = as_h2(q & 0x00F000F0u);   // 16+4t, 18+4t
+        const half2v od_lo = as_h2(q8 & 0x000F000Fu);  // 4t+1, 4t+3
+        const half2v od_hi = as_h2(q8 & 0x00F000F0u);  // 17+4t, 19+4t
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
-          float v = a.x * xl[m].x;
-          v = __builtin_fmaf(a.y, xl[m].y, v);
-          v = __builtin_fmaf(b.x, xl[m].z, v);
-          v = __builtin_fmaf(b.y, xl[m].w, v);
-          v = __builtin_fmaf(c.x, xh[m].x, v);
-          v = __builtin_fmaf(c.y, xh[m].y, v);
-          v = __builtin_fmaf(e.x, xh[m].z, v);
-          v = __builtin_fmaf(e.y, xh[m].w, v);
+          // the chain starts with an FMA into zero: one v_fma_mix_f32, where
+          // a product would be a conversion and a multiply
+          float v = __builtin_fmaf((float)ev_lo[0], xl[m].x, 0.0f);
+          v = __builtin_fmaf((float)od_lo[0], xl[m].y, v);
+          v = __builtin_fmaf((float)ev_lo[1], xl[m].z, v);
+          v = __builtin_fmaf((float)od_lo[1], xl[m].w, v);
+          v = __builtin_fmaf((float)ev_hi[0], xh[m].x, v);
+          v = __builtin_fmaf((float)od_hi[0], xh[m].y, v);
+          v = __builtin_fmaf((float)ev_hi[1], xh[m].z, v);
+          v = __builtin_fmaf((float)od_hi[1], xh[m].w, v);
           s[t][j][m] = v;
         }
       }
     }
 #pragma unroll
     for (int j = 0; j < R2; ++j) {
-      const float d = h2f_bits((uint16_t)scale_bits<Q4_0>(w[j], blk)) * inv_unit;
+      const float d = h2f_bits((uint16_t)scale_bits<Q4_0>(w[j], blk)) * (1.0f / kCodeUnit);
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
         const float sum = (s[0][j][m] + s[1][j][m]) + (s[2][j][m] + s[3][j][m]);
@@ -230,7 +245,6 @@ __device__ __forceinline__ void pair_f32_q8(const uint32_t (&w)[R2][17], const f
   }
 }
 
-__device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 
 // (q & mask) | bits in one v_and_or_b32.  Its VOP3 encoding cannot carry
 // 32-bit literals and reads at most one scalar register, so the mask comes
@@ -241,7 +255,6 @@ __device__ __forceinline__ uint32_t and_or(uint32_t q, uint32_t mask, uint32_t b
   asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(q), "s"(mask), "v"(bits));
   return r;
 }
-__device__ __forceinline__ uint32_t as_u32(half2v h) { return __builtin_bit_cast(uint32_t, h); }
 
 // f16 activations (weights rounded to fp16 exactly as dequant_*_f16).
 //
@@ -422,8 +435,6 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   float* sxs = reinterpret_cast<float*>(smem + (size_t)MM * P * (CP + 1) * 16);
   const int tid = threadIdx.x;
 
-  // fp8 e4m3 value of byte 0x01 (the unit step of the nibble trick)
-  const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1u, false)[0];
 
   const int lane = tid & 63, wave = tid >> 6;
   const int L = 1 << log2L;
@@ -516,6 +527,10 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
     // sum is formed with DPP adds across them (total is a multiple of 8, so
     // the 8 lanes of a block are in or out of range together).
     const int total = M * P * CP;
+    // chunk c is 4 elements of a 32-element block; its position in the block
+    // is c & 7, which (every round starting at a multiple of 16 chunks) is
+    // tid & 7: elements 16..31 for tid & 4
+    const float xscale = (tid & 4) ? 0.0625f : 1.0f;
     auto load = [&](int c0, ChunkT (&v)[8]) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -529,13 +544,19 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
         const int c = c0 + u * 256 + tid;
         if (c < total) {
           const int gp = c / CP, j = c & (CP - 1);
-          xs[gp * (CP + 1) + j] = v[u];
+          if constexpr (kSx) {
+            // f32 Q4_0 stages elements 16..31 of each block divided by 16
+            // (pair_f32_q4); the block sums below use the values as given
+            xs[gp * (CP + 1) + j] = v[u] * xscale;
+          } else {
+            xs[gp * (CP + 1) + j] = v[u];
+          }
           if constexpr (kSx) {
             float sum = (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
             sum += dpp_f<0xB1>(sum);   // quad_perm [1,0,3,2]
             sum += dpp_f<0x4E>(sum);   // quad_perm [2,3,0,1]
             sum += dpp_f<0x141>(sum);  // row_half_mirror: every lane of the 8 holds the block sum
-            if ((j & 7) == 0) sxs[gp * 2 + (j >> 3)] = sum * (8.0f * unit);
+            if ((j & 7) == 0) sxs[gp * 2 + (j >> 3)] = sum * (8.0f * kCodeUnit);
           }
         }
       }
@@ -554,7 +575,6 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
   }
   __syncthreads();
 
-  const float inv_unit = 1.0f / unit;
   float acc[R2][MM];
 #pragma unroll
   for (int j = 0; j < R2; ++j)
@@ -567,7 +587,7 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
     if (pair < P) {
       if constexpr (kF32) {
         if constexpr (kQ4) {
-          pair_f32_q4<R2, MM>(w, reinterpret_cast<const float4v*>(xs), sxs, P, pair, inv_unit, acc);
+          pair_f32_q4<R2, MM>(w, reinterpret_cast<const float4v*>(xs), sxs, P, pair, acc);
         } else {
           pair_f32_q8<R2, MM>(w, reinterpret_cast<const float4v*>(xs), P, pair, acc);
         }
