@@ -399,7 +399,8 @@ struct GemvGroup {
   int count;
 };
 
-template <class QF, typename XT, int R2, int MM>
+// NS register sets of weights in rotation: the loads run NS - 1 steps ahead.
+template <class QF, typename XT, int R2, int MM, int NS>
 __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A, const GemvGroup grp, int M,
                                                         int K, int log2L) {
   // This workgroup's job (uniform; selects rather than an indexed load of
@@ -470,7 +471,7 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
     }
   };
 
-  uint32_t wa[R2][DW], wb[R2][DW], wc[R2][DW];  // wc: only with k3Sets
+  uint32_t wr[NS][R2][DW];
 
   // ---- stage A into LDS (and the per-block sums of x) ----
   // The first two rounds of activations (all of them up to M * K = 16384
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
     load(0, v0);
     const bool two = totb > 512;
     if (two) load(512, v1);
-    if (T > 0) next_load(wa);
+    if (T > 0) next_load(wr[0]);
     put(0, v0);
     if (two) put(512, v1);
     for (int b0 = 1024; b0 < totb; b0 += 512) {
@@ -565,7 +566,7 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
     load(0, v0);
     const bool two = total > 256 * 8;
     if (two) load(256 * 8, v1);
-    if (T > 0) next_load(wa);
+    if (T > 0) next_load(wr[0]);
     put(0, v0);
     if (two) put(256 * 8, v1);
     for (int c0 = 2 * 256 * 8; c0 < total; c0 += 256 * 8) {
@@ -621,37 +622,17 @@ __global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A
     }
   };
 
-  // Register sets in rotation: with three or more steps the loads run two
-  // steps ahead (three sets; measured 8.1 against 8.8 us at 11008 x 4096),
-  // else one step ahead (two sets; the extra set's loads would be wasted).
-  // One row per lane group only (two rows with three sets measured slower),
-  // and not for four activation rows, whose third set costs occupancy.
-  constexpr bool k3Sets = R2 == 1 && MM <= 2;
-  if (k3Sets && T >= 3) {
-    next_load(wb);
-    for (int t = 0; t < T; t += 3) {
-      next_load(wc);
+  // Register sets in rotation: the loads of step t + NS - 1 are issued
+  // before step t is computed (NS from gemv_sets).  Set 0 was requested
+  // during staging; loads past the last step are clamped and never used.
+#pragma unroll
+  for (int i = 1; i < NS - 1; ++i) next_load(wr[i]);
+  for (int t = 0; t < T; t += NS) {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      next_load(wr[(i + NS - 1) % NS]);
       __builtin_amdgcn_sched_barrier(0);
-      step(wa);
-      __builtin_amdgcn_sched_barrier(0);
-      next_load(wa);
-      __builtin_amdgcn_sched_barrier(0);
-      if (t + 1 < T) step(wb);
-      __builtin_amdgcn_sched_barrier(0);
-      next_load(wb);
-      __builtin_amdgcn_sched_barrier(0);
-      if (t + 2 < T) step(wc);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else {
-    for (int t = 0; t < T; t += 2) {
-      next_load(wb);
-      __builtin_amdgcn_sched_barrier(0);
-      step(wa);
-      __builtin_amdgcn_sched_barrier(0);
-      next_load(wa);
-      __builtin_amdgcn_sched_barrier(0);
-      if (t + 1 < T) step(wb);
+      if (t + i < T) step(wr[i]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -746,7 +727,7 @@ hipError_t gemv_block_dispatch(const void* A, const void* W, void* C, uint32_t M
 
 // Host-side geometry of the pair kernel.
 struct PairGeom {
-  int log2L = 5, R2 = 1, MM = 1;
+  int log2L = 5, R2 = 1, MM = 1, sets = 2;
   unsigned grid = 1;
   size_t lds = 0;
 };
@@ -754,6 +735,12 @@ struct PairGeom {
 // Lanes per row: the largest of 64/32/16 whose round-robin split of the P
 // pairs keeps >= 95% of the lanes busy, else the best split.
 inline int pick_log2L(int P) {
+  static const int forced = [] {
+    const char* e = std::getenv("NF_HIP_GEMV_LOG2L");  // tuning override: 4, 5 or 6
+    const int v = e ? std::atoi(e) : 0;
+    return v >= 4 && v <= 6 ? v : 0;
+  }();
+  if (forced) return forced;
   static const double min_u = [] {
     const char* e = std::getenv("NF_HIP_GEMV_MIN_UTIL");  // tuning override
     const double v = e ? std::atof(e) : 0.0;
@@ -779,18 +766,28 @@ inline int pick_log2L(int P) {
 // activations (plan.cpp) plus the padding chunks and the f32 block sums.
 constexpr size_t kPairMaxLds = 136 * 1024;
 
-template <class QF, typename XT, int R2, int MM>
+template <class QF, typename XT, int R2, int MM, int NS>
 hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const GemvGroup& grp, uint32_t M, uint32_t K,
                             hipStream_t s) {
   if (g.lds > 64 * 1024) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_pair_kernel<QF, XT, R2, MM>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPairMaxLds);
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_pair_kernel<QF, XT, R2, MM, NS>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPairMaxLds);
     if (attr != hipSuccess) return attr;
   }
-  gemv_pair_kernel<QF, XT, R2, MM><<<dim3(g.grid), dim3(256), g.lds, s>>>(static_cast<const XT*>(A), grp, (int)M,
-                                                                          (int)K, g.log2L);
+  gemv_pair_kernel<QF, XT, R2, MM, NS><<<dim3(g.grid), dim3(256), g.lds, s>>>(static_cast<const XT*>(A), grp,
+                                                                              (int)M, (int)K, g.log2L);
   return hipGetLastError();
 }
+
+// Weight register sets for a lane running `steps` steps: one step ahead for
+// one or two steps (a second set's loads would be wasted), two ahead from
+// three steps (11008 x 4096: 8.1 against 8.8 us) with one or two activation
+// rows; four activation rows keep two sets (a third costs occupancy).
+// Three and four steps ahead measured slower on MI355X (Llama-2-7B decode
+// step 1264 / 1234 against 1162 us, 4096 x 11008 11.1 / 10.8 against
+// 10.3 us), so the kernel is instantiated for two and three sets.
+inline int gemv_sets(int MM, long steps) { return (MM <= 2 && steps >= 3) ? 3 : 2; }
 
 // Geometry of a pair-kernel launch over `rows` rows (one matrix or a whole
 // group) with M activation rows of K; false when its activation stage would
@@ -822,16 +819,21 @@ bool pair_geom(uint32_t M, uint32_t K, long rows, PairGeom& g) {
   const long wgs = (rows + 4L * R - 1) / (4L * R);
   g.R2 = 1;
   g.grid = (unsigned)(wgs < cap ? wgs : cap);
+  // steps of a lane: passes over the rows times pair steps per row
+  const long passes = (rows + (long)g.grid * 4L * R - 1) / ((long)g.grid * 4L * R);
+  g.sets = gemv_sets(g.MM, passes * ((P + (1 << g.log2L) - 1) >> g.log2L));
   return true;
 }
 
 template <class QF, typename XT>
 hipError_t gemv_pair_group(const PairGeom& g, const void* A, const GemvGroup& grp, uint32_t M, uint32_t K,
                            hipStream_t s) {
-  switch (g.MM) {
-    case 1: return gemv_pair_launch<QF, XT, 1, 1>(g, A, grp, M, K, s);
-    case 2: return gemv_pair_launch<QF, XT, 1, 2>(g, A, grp, M, K, s);
-    default: return gemv_pair_launch<QF, XT, 1, 4>(g, A, grp, M, K, s);
+  switch (g.MM * 8 + g.sets) {
+    case 8 + 2: return gemv_pair_launch<QF, XT, 1, 1, 2>(g, A, grp, M, K, s);
+    case 8 + 3: return gemv_pair_launch<QF, XT, 1, 1, 3>(g, A, grp, M, K, s);
+    case 16 + 2: return gemv_pair_launch<QF, XT, 1, 2, 2>(g, A, grp, M, K, s);
+    case 16 + 3: return gemv_pair_launch<QF, XT, 1, 2, 3>(g, A, grp, M, K, s);
+    default: return gemv_pair_launch<QF, XT, 1, 4, 2>(g, A, grp, M, K, s);
   }
 }
 
