@@ -54,6 +54,25 @@ __device__ __forceinline__ void split3(const float (&x)[8], bf16x8& p1, bf16x8& 
   }
 }
 
+// Two bf16 pieces of 8 floats: p1 = x truncated to bf16 (its upper 16 bits,
+// exact), p2 = the remainder x - p1 (exact in f32) rounded to nearest bf16.
+// |x - p1 - p2| <= 2^-9 |x - p1| < 2^-16 |x|, so a product p * x taken as
+// p * p1 + p * p2 (each exact in fp32) is within 2^-16 of p * x.
+__device__ __forceinline__ void split2(const float (&x)[8], bf16x8& p1, bf16x8& p2) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t u0 = __builtin_bit_cast(uint32_t, x[2 * j]) & 0xFFFF0000u;
+    const uint32_t u1 = __builtin_bit_cast(uint32_t, x[2 * j + 1]) & 0xFFFF0000u;
+    const float2s r = {x[2 * j] - __builtin_bit_cast(float, u0), x[2 * j + 1] - __builtin_bit_cast(float, u1)};
+    const bf16x2v h2 = __builtin_convertvector(r, bf16x2v);
+    const uint32_t hi = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+    p1[2 * j] = __builtin_bit_cast(bf16x2v, hi)[0];
+    p1[2 * j + 1] = __builtin_bit_cast(bf16x2v, hi)[1];
+    p2[2 * j] = h2[0];
+    p2[2 * j + 1] = h2[1];
+  }
+}
+
 struct Q4_0 {
   static constexpr int kBytes = 18;
 };
