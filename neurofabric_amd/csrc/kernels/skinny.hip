@@ -42,6 +42,15 @@
 // computes while both of chunk c+1 are in flight.
 // At most 32 activation rows per launch keep the two activation register sets
 // and the accumulators in registers; more rows take more launches.
+//
+// f32 activations go to skinny_ring_kernel (below) instead: the same MFMA
+// chain, with the weights streamed through a four-stage LDS ring by buffer
+// loads to LDS (three chunks in flight at no register cost), the activations
+// split into bf16 pieces once per workgroup of 8 waves rather than once per
+// wave, and up to 64 rows in one pass (one read of the weights).  Measured
+// on MI355X: Llama-3-8B Q8_0 decode step at M = 64 10.7 -> 5.95 ms, M = 16
+// 3.39 -> 3.26 ms; TinyLlama Q4_0 M = 16 1042 -> 971 us.  skinny_kernel
+// remains the f32 path with NF_HIP_SKINNY_RING=0.
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
@@ -497,6 +506,452 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   if (tid == 0) __hip_atomic_store(&ws_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------------------
+// skinny_ring_kernel: f32 activations, up to 64 rows in one pass, weights
+// streamed into an LDS ring by buffer loads to LDS.
+//
+// A workgroup is 8 waves (two per SIMD) over 128*T weight rows (wave w: rows
+// 16T*w .. 16T*w + 16T-1 as T 16-row tiles), and all waves walk the same K
+// range chunk by chunk; a chunk is CHP pairs (64*CHP elements).  The weight
+// ring has S stages; chunk i+S-1 is requested while chunk i is computed, by
+// buffer_load ... lds, which writes LDS without passing through registers
+// (so S-1 chunks in flight cost no registers), range-checked: chunks past
+// the workgroup's range read through a resource of zero bytes (zeros, no
+// memory traffic).  A weight row's staged pairs are 9 (17) dwords apart, an
+// odd stride, so the 16 rows of a tile read 16 different banks.
+//
+// The activations (16*MT rows, rows past M repeating row M-1, whose outputs
+// are never stored) are L2-resident: each thread loads the 8 values of its
+// A operand(s) of chunk i+1 into registers while chunk i computes, and after
+// chunk i splits them once for the whole workgroup into the two bf16 pieces
+// of the MFMA operand (x ~ b1 + b2, split2), stored in operand order in one
+// of two LDS buffers, so a wave reads each piece with one conflict-free
+// ds_read_b128.  Every wave then runs skinny_kernel's f32 MFMA chain on its
+// tiles (exact bf16 codes, two chained MFMAs, the block scale applied per
+// block in fp32).
+//
+// With K split over KG workgroups (grid y), each parks its partial tile and
+// the last to arrive adds the KG tiles in order kg = 0..KG-1 (deterministic)
+// and stores C.
+template <class QF, int MT, int T, int CHP>
+struct RingGeom {
+  static constexpr int kWaves = 8;
+  static constexpr int kPB = SkW<QF>::kPairBytes, kPD = kPB / 4;
+  static constexpr int kRW = 16 * T;                   // weight rows per wave
+  static constexpr int kWRow = CHP * kPD;              // dwords per staged weight row
+  static constexpr int kWDw = kRW * kWRow;             // weight dwords of a wave per chunk
+  static constexpr int kJW = (kWDw + 63) / 64;         // dword loads per lane per chunk (last one partial)
+  static constexpr int kStage = kWaves * kWDw;         // dwords of a stage
+  static constexpr int kUnits = CHP * 2 * MT * 64;     // A operands (lane slots) per chunk
+  static constexpr int kUPT = (kUnits + 511) / 512;    // A operands per thread
+  static constexpr int kXB = kUnits * 8;               // dwords of one split buffer (two bf16x8 each)
+};
+
+// s_waitcnt immediate: vmcnt(v) (6 bits, split), expcnt and lgkmcnt not waited on.
+constexpr int sk_vmcnt_imm(int v) { return (v & 15) | ((v >> 4) << 14) | 0x0070 | 0x0F00; }
+
+// Buffer load to LDS: lane i writes lds + 4*i; the builtin exists only in
+// the device pass.
+__device__ __forceinline__ void sk_dma4(__amdgpu_buffer_rsrc_t r, uint32_t* lds, uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, (int)voff,
+                                           (int)soff, 0, 0);
+#endif
+}
+
+// Workgroup barrier without a memory fence (the compiler's fence would wait
+// for every outstanding load, including the ring's younger chunks).
+__device__ __forceinline__ void sk_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <class QF, int MT, int T, int CHP, int S>
+__global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restrict__ A, const SkinnyGroup grp, int M,
+                                                         int K, float* __restrict__ ws_part,
+                                                         uint32_t* __restrict__ ws_cnt) {
+  int job = 0;
+#pragma unroll
+  for (int q = 1; q < kSkGroupMax; ++q) job = (q < grp.count && (int)blockIdx.x >= grp.begin[q]) ? q : job;
+  const uint8_t* __restrict__ W = grp.W[0];
+  void* Cv = grp.C[0];
+  int N = grp.N[0], tile0 = grp.begin[0];
+#pragma unroll
+  for (int q = 1; q < kSkGroupMax; ++q)
+    if (job == q) {
+      W = grp.W[q];
+      Cv = grp.C[q];
+      N = grp.N[q];
+      tile0 = grp.begin[q];
+    }
+  float* __restrict__ C = static_cast<float*>(Cv);
+  typedef RingGeom<QF, MT, T, CHP> G;
+  constexpr bool kQ4 = SkW<QF>::kLoads == 5;
+  constexpr int WL = SkW<QF>::kLoads;
+  constexpr int RW = G::kRW, NW = G::kWaves, UPT = G::kUPT;
+  static_assert(S >= 3 && (S - 2) * G::kJW <= 63, "ring depth and the vmcnt field");
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  uint32_t* const xb0 = smem + S * G::kStage;  // split operands, two buffers of kXB dwords
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, s = lane >> 4;
+  const int NC = (K >> 6) / CHP;
+  const int n0 = ((int)blockIdx.x - tile0) * (NW * RW) + wave * RW;  // this wave's first row
+  const int KG = gridDim.y, kg = blockIdx.y;
+  const int c_begin = (int)((long)NC * kg / KG), c_end = (int)((long)NC * (kg + 1) / KG);
+
+  // Weight loads: dword f = lane + 64j of the wave's RW x kWRow chunk is row
+  // f / kWRow, dword f % kWRow (pairs of a row are contiguous, so the byte
+  // offset within the row is 4 * (f % kWRow)); it lands at LDS dword f.
+  const uint32_t row_bytes = (uint32_t)(K >> 6) * G::kPB;
+  uint32_t wsrc[G::kJW];
+#pragma unroll
+  for (int j = 0; j < G::kJW; ++j) {
+    const int f = lane + 64 * j < G::kWDw ? lane + 64 * j : G::kWDw - 1;
+    const int row = f / G::kWRow, dw = f % G::kWRow;
+    const int n = n0 + row < N ? n0 + row : N - 1;
+    wsrc[j] = (uint32_t)n * row_bytes + (uint32_t)(4 * dw);
+  }
+  const uint32_t w_bytes = (uint32_t)N * row_bytes;
+  auto fetch_w = [&](int c, int st) {
+    const bool live = c < c_end;
+    const __amdgpu_buffer_rsrc_t rw = sk_rsrc(W, __builtin_amdgcn_readfirstlane(live ? w_bytes : 0u));
+    const uint32_t wo = __builtin_amdgcn_readfirstlane(live ? (uint32_t)c * (uint32_t)(CHP * G::kPB) : 0u);
+    uint32_t* wsb = smem + st * G::kStage + wave * G::kWDw;
+#pragma unroll
+    for (int j = 0; j < G::kJW; ++j) {
+      // the last load's lanes past the wave's dwords stay idle (exec mask)
+      if (G::kWDw % 64 == 0 || j + 1 < G::kJW || lane < G::kWDw % 64) sk_dma4(rw, wsb + 64 * j, wsrc[j], wo);
+    }
+  };
+
+  // A operands: unit u = ((pi * 2 + h) * MT + mt) * 64 + l is the operand of
+  // lane l (row 16mt + l%16, slot l/16) for block h of pair pi of a chunk:
+  // activations k = 64pi + 32h + {off0 .. off0+3, off1 .. off1+3} of its row
+  // (the k order of the lane's weight codes).  Thread tid takes units tid,
+  // tid + 512, ...; piece k (0: hi, 1: lo) of unit u goes to 16-byte slot
+  // ((u / 64) * 2 + k) * 64 + l of a split buffer, so a wave's read of one
+  // piece covers 1 KB contiguously.
+  uint32_t xoff[UPT];
+  bool xlive[UPT];
+#pragma unroll
+  for (int k = 0; k < UPT; ++k) {
+    const int u = tid + 512 * k;
+    xlive[k] = G::kUnits % 512 == 0 || u < G::kUnits;
+    const int uu = xlive[k] ? u : 0;
+    const int l = uu & 63, mt = (uu >> 6) % MT, ph = (uu >> 6) / MT, h = ph & 1, pi = ph >> 1;
+    const int m = 16 * mt + (l & 15);
+    const int mm = m < M ? m : M - 1;
+    xoff[k] = ((uint32_t)mm * (uint32_t)K + (uint32_t)(64 * pi + 32 * h + (kQ4 ? 4 : 8) * (l >> 4))) * 4u;
+  }
+  const uint32_t x_bytes = (uint32_t)M * (uint32_t)K * 4u;
+  float4v xr[UPT][2];
+  auto load_x = [&](int c) {
+    const bool live = c < c_end;
+    const __amdgpu_buffer_rsrc_t rx = sk_rsrc(A, __builtin_amdgcn_readfirstlane(live ? x_bytes : 0u));
+    const uint32_t xo = __builtin_amdgcn_readfirstlane(live ? (uint32_t)c * (CHP * 256u) : 0u);
+#pragma unroll
+    for (int k = 0; k < UPT; ++k) {
+      xr[k][0] = __builtin_bit_cast(float4v, sk_buf_load<16>(rx, xoff[k], xo));
+      xr[k][1] = __builtin_bit_cast(float4v, sk_buf_load<16>(rx, xoff[k] + (kQ4 ? 64u : 16u), xo));
+    }
+  };
+  auto split_x = [&](uint32_t* xb) {
+#pragma unroll
+    for (int k = 0; k < UPT; ++k) {
+      if (xlive[k]) {
+        const int u = tid + 512 * k;
+        const float xv[8] = {xr[k][0].x, xr[k][0].y, xr[k][0].z, xr[k][0].w,
+                             xr[k][1].x, xr[k][1].y, xr[k][1].z, xr[k][1].w};
+        bf16x8 a1, a2;
+        split2(xv, a1, a2);
+        uint32_t* dst = xb + (((u >> 6) * 2) * 64 + (u & 63)) * 4;
+        *reinterpret_cast<bf16x8*>(dst) = a1;
+        *reinterpret_cast<bf16x8*>(dst + 256) = a2;
+      }
+    }
+  };
+
+  bool wvalid[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) wvalid[t] = n0 + 16 * t + r16 < N;
+
+  float4v acc[MT][T];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[mt][t] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int st, const uint32_t* xb) {
+    const uint32_t* wsb = smem + st * G::kStage + wave * G::kWDw;
+#pragma unroll
+    for (int pi = 0; pi < CHP; ++pi)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        bf16x8 a1[MT], a2[MT];
+        float4v base[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint32_t* up = xb + ((((pi * 2 + h) * MT + mt) * 2) * 64 + lane) * 4;
+          a1[mt] = *reinterpret_cast<const bf16x8*>(up);
+          a2[mt] = *reinterpret_cast<const bf16x8*>(up + 256);
+          base[mt] = float4v{0.f, 0.f, 0.f, 0.f};
+          if constexpr (kQ4) {
+            // sum_k (-136) * x, the offset of the 128 + n codes, shared by
+            // all weight tiles
+            const __bf16 c8 = (__bf16)(-136.0f);
+            const bf16x8 bc = {c8, c8, c8, c8, c8, c8, c8, c8};
+            base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], bc, base[mt], 0, 0, 0);
+            base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[mt], bc, base[mt], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const uint32_t* pr = wsb + (16 * t + r16) * G::kWRow + pi * G::kPD;
+          uint32_t w[WL];
+          if constexpr (WL == 5) {
+            w[0] = pr[s]; w[1] = pr[s + 1]; w[2] = pr[5 + s]; w[3] = pr[0]; w[4] = pr[4];
+          } else {
+            w[0] = pr[2 * s]; w[1] = pr[2 * s + 1]; w[2] = pr[2 * s + 2];
+            w[3] = pr[9 + 2 * s]; w[4] = pr[10 + 2 * s]; w[5] = pr[0]; w[6] = pr[8];
+          }
+          const bf16x8 b = sk_b_codes<QF>(w, h);
+          float d = h2f_bits((uint16_t)sk_scale_bits<QF>(w, h));
+          if (!wvalid[t]) d = 0.f;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            float4v dd = base[mt];
+            dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mt], b, dd, 0, 0, 0);
+            dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[mt], b, dd, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mt][t][i] = __builtin_fmaf(d, dd[i], acc[mt][t][i]);
+          }
+        }
+      }
+  };
+
+  // Pipeline.  Before the loop: weights of chunks c_begin .. c_begin+S-2 go
+  // out, chunk 0's activations are loaded and split.  Iteration i waits for
+  // chunk i's weights (at most S-2 younger chunks' weight loads in flight;
+  // every thread issues the same number per chunk, in chunk order, so the
+  // count is exact) and for its own split stores; one barrier then makes
+  // chunk i's weights and split operands visible and retires chunk i-1 (its
+  // stage receives chunk i+S-1, its split buffer the split of chunk i+1).
+  // Chunk i+1's activations are requested first (the compiler's own wait
+  // before the split counts the weight loads issued after them), chunk i
+  // computes, chunk i+1 is split.
+  const int nch = c_end - c_begin;
+  load_x(c_begin);
+#pragma unroll
+  for (int i = 0; i < S - 1; ++i) fetch_w(c_begin + i, i);
+  split_x(xb0);
+  for (int i = 0; i < nch; ++i) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(sk_vmcnt_imm((S - 2) * G::kJW) & ~0x0F00);
+    sk_barrier();
+    load_x(c_begin + i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_w(c_begin + i + S - 1, (i + S - 1) % S);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(i % S, xb0 + (i & 1) * G::kXB);
+    __builtin_amdgcn_sched_barrier(0);
+    split_x(xb0 + ((i + 1) & 1) * G::kXB);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  auto store = [&](int mt, int t, int i, float v) {
+    const int n = n0 + 16 * t + r16, m = 16 * mt + 4 * s + i;
+    if (n < N && m < M) C[(size_t)m * N + n] = v;
+  };
+  if (KG == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store(mt, t, i, acc[mt][t][i]);
+    return;
+  }
+  // K split across workgroups: park this tile (float4 (mt*T + t) of thread
+  // tid at index (mt*T + t) * 512 + tid, sc1 stores), count arrivals; the
+  // last workgroup reads the KG tiles back in order kg = 0..KG-1, all of a
+  // thread's loads of one tile issued before any is added.
+  constexpr int NQ = MT * T;
+  const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)blockIdx.x * KG * (NQ * 512),
+                             (uint32_t)(KG * NQ * 512 * 16));
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < T; ++t) tile_ws.store((uint32_t)kg * (NQ * 512) + (mt * T + t) * 512 + tid, acc[mt][t]);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ uint32_t is_last;
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == (uint32_t)(KG - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  for (int g = 0; g < KG; ++g) {
+    float4v p[MT][T];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < T; ++t) p[mt][t] = tile_ws.load((uint32_t)g * (NQ * 512) + (mt * T + t) * 512 + tid);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[mt][t] = g == 0 ? p[mt][t] : acc[mt][t] + p[mt][t];
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) store(mt, t, i, acc[mt][t][i]);
+  if (tid == 0) __hip_atomic_store(&ws_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Ring geometry per format, activation tiles (MT) and weight tiles per wave
+// (T): two pairs per chunk with one activation tile, else one; as many
+// stages as fit in 160 KB of LDS beside the two split buffers, at most 4, at
+// least 3.
+template <class QF, int MT, int T>
+struct RingCfg {
+  static constexpr int kCHP = MT == 1 ? 2 : 1;
+  typedef RingGeom<QF, MT, T, kCHP> G;
+  static constexpr int kFree = 160 * 1024 / 4 - 2 * G::kXB - 64;  // dwords (64 for the static LDS)
+  static constexpr int kSLds = kFree / G::kStage, kSVm = 2 + 63 / G::kJW;  // LDS, vmcnt field
+#ifndef NF_RING_MAX_S
+#define NF_RING_MAX_S 4
+#endif
+  static constexpr int kSMax = NF_RING_MAX_S;
+  static constexpr int kS = kSLds < kSVm ? (kSLds < kSMax ? kSLds : kSMax) : (kSVm < kSMax ? kSVm : kSMax);
+  static constexpr bool kOk = kS >= 3;
+  static constexpr int kLds = (kS * G::kStage + 2 * G::kXB) * 4;
+};
+
+// Weight tiles per wave: the largest of 4, 2, 1 whose ring fits with at
+// least 128 row groups (so a matrix spreads over the CUs with few K splits),
+// else 1.
+template <class QF, int MT>
+int ring_t(uint32_t N) {
+  static const int forced = [] {
+    const char* e = std::getenv("NF_HIP_RING_T");  // tuning override: 1, 2 or 4
+    const int v = e ? std::atoi(e) : 0;
+    return (v == 1 || v == 2 || v == 4) ? v : 0;
+  }();
+  if (forced == 4 && RingCfg<QF, MT, 4>::kOk) return 4;
+  if (forced == 2 && RingCfg<QF, MT, 2>::kOk) return 2;
+  if (forced == 1) return 1;
+  if (RingCfg<QF, MT, 4>::kOk && N >= 128u * 512u) return 4;
+  if (RingCfg<QF, MT, 2>::kOk && N >= 128u * 256u) return 2;
+  return 1;
+}
+
+// Workgroups per row group (kg): up to about 256 workgroups in all, at
+// least `min_chunks` chunks each, within the workspace.
+template <class QF, int MT, int T>
+int ring_split(long tiles, uint32_t K, const nfhip::Workspace& ws) {
+  typedef RingCfg<QF, MT, T> Cfg;
+  constexpr int NQ = MT * T;
+  const int NC = (int)(K / (64 * Cfg::kCHP));
+  static const long target = [] {
+    const char* e = std::getenv("NF_HIP_RING_WGS");  // tuning override
+    const long v = e ? std::atol(e) : 0;
+    return v > 0 ? v : 256L;
+  }();
+  static const int min_chunks = [] {
+    const char* e = std::getenv("NF_HIP_RING_MIN_CHUNKS");  // tuning override
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 ? v : 4;
+  }();
+  int kg = 1;
+  while (tiles * kg * 2 <= target && NC >= min_chunks * kg * 2 && tiles <= (long)ws.cnt_len &&
+         (size_t)tiles * kg * 2 * NQ * 512 * 4 <= ws.part_floats)
+    kg *= 2;
+  return kg;
+}
+
+template <class QF, int MT, int T>
+hipError_t ring_launch_group(const float* A, const SkinnyGroup& grp, long tiles, uint32_t M, uint32_t K, int kg,
+                             const nfhip::Workspace& ws, hipStream_t s) {
+  typedef RingCfg<QF, MT, T> Cfg;
+  if constexpr (!Cfg::kOk) {
+    return hipErrorNotSupported;
+  } else {
+    constexpr int CHP = Cfg::kCHP, S = Cfg::kS;
+    if (kg > 1 && (tiles > (long)ws.cnt_len || (size_t)tiles * kg * MT * T * 512 * 4 > ws.part_floats))
+      return hipErrorNotSupported;
+    if ((K / 64) % CHP != 0) return hipErrorNotSupported;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_ring_kernel<QF, MT, T, CHP, S>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::kLds);
+    if (attr != hipSuccess) return attr;
+    skinny_ring_kernel<QF, MT, T, CHP, S><<<dim3((unsigned)tiles, (unsigned)kg), dim3(512), Cfg::kLds, s>>>(
+        A, grp, (int)M, (int)K, ws.part, ws.cnt);
+    return hipGetLastError();
+  }
+}
+
+// One launch for n jobs (n = 1: a single linear) over the same activations:
+// every job gets the geometry and K split a launch of its own would (so its
+// output is bit-identical to that launch); otherwise hipErrorNotSupported.
+template <class QF, int MT, int T>
+hipError_t ring_group_t(const float* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
+                        const nfhip::Workspace& ws, hipStream_t s) {
+  SkinnyGroup grp{};
+  long tiles = 0;
+  int kg0 = 0;
+  for (uint32_t j = 0; j < n; ++j) {
+    if (ring_t<QF, MT>(jobs[j].N) != T) return hipErrorNotSupported;
+    const long t = ((long)jobs[j].N + 128 * T - 1) / (128 * T);
+    const int kg = ring_split<QF, MT, T>(t, K, ws);
+    if (j == 0) kg0 = kg;
+    else if (kg != kg0) return hipErrorNotSupported;
+    grp.W[j] = static_cast<const uint8_t*>(jobs[j].W);
+    grp.C[j] = jobs[j].C;
+    grp.N[j] = (int)jobs[j].N;
+    grp.begin[j] = (int)tiles;
+    tiles += t;
+  }
+  for (int q = (int)n; q <= kSkGroupMax; ++q) grp.begin[q] = (int)tiles;
+  grp.count = (int)n;
+  return ring_launch_group<QF, MT, T>(A, grp, tiles, M, K, kg0, ws, s);
+}
+
+template <class QF, int MT>
+hipError_t ring_group(const float* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
+                      const nfhip::Workspace& ws, hipStream_t s) {
+  switch (ring_t<QF, MT>(jobs[0].N)) {
+    case 1: return ring_group_t<QF, MT, 1>(A, jobs, n, M, K, ws, s);
+    case 2: return ring_group_t<QF, MT, 2>(A, jobs, n, M, K, ws, s);
+    default: return ring_group_t<QF, MT, 4>(A, jobs, n, M, K, ws, s);
+  }
+}
+
+template <class QF>
+hipError_t ring_dispatch(const float* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
+                         const nfhip::Workspace& ws, hipStream_t s) {
+  if (M <= 16) return ring_group<QF, 1>(A, jobs, n, M, K, ws, s);
+  if (M <= 32) return ring_group<QF, 2>(A, jobs, n, M, K, ws, s);
+  return ring_group<QF, 4>(A, jobs, n, M, K, ws, s);
+}
+
+// The ring kernel serves f32 activations unless turned off for comparison
+// (NF_HIP_SKINNY_RING=0).
+inline bool ring_on() {
+  static const bool on = [] {
+    const char* e = std::getenv("NF_HIP_SKINNY_RING");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 // Waves per workgroup (ks) and workgroups per row tile (kg) for a launch of
 // `wgs` row tiles, bounded by the kernel's launch bound of 512 threads, by
 // at least one chunk per wave and by the workspace: 8 waves per workgroup up
@@ -654,6 +1109,11 @@ hipError_t launch_skinny_group(QFmt q, EType t, const void* A, const GemvJob* jo
                                uint32_t K, const Workspace& ws, hipStream_t s) {
   for (uint32_t j = 0; j < n; ++j)
     if (!skinny_fits(M, jobs[j].N, K, A, jobs[j].W)) return hipErrorNotSupported;
+  if (t == EType::F32 && nfk::ring_on()) {
+    const float* a = static_cast<const float*>(A);
+    return q == QFmt::Q4_0 ? nfk::ring_dispatch<nfk::Q4_0>(a, jobs, n, M, K, ws, s)
+                           : nfk::ring_dispatch<nfk::Q8_0>(a, jobs, n, M, K, ws, s);
+  }
   if (q == QFmt::Q4_0)
     return t == EType::F32 ? nfk::skinny_group_dispatch<nfk::Q4_0, float>(A, jobs, n, M, K, ws, s)
                            : nfk::skinny_group_dispatch<nfk::Q4_0, nfk::half_t>(A, jobs, n, M, K, ws, s);
@@ -668,10 +1128,29 @@ bool skinny_fits(uint32_t M, uint32_t N, uint32_t K, const void* A, const void* 
          wbytes < (1ull << 32) && abytes < (1ull << 32);
 }
 
-uint32_t skinny_max_rows(EType) { return 32u; }
+// f32 activations: all 64 rows in one pass with the ring kernel (32 with
+// skinny_kernel, whose activation registers limit it to two 16-row tiles).
+uint32_t skinny_max_rows(EType t) { return (t == EType::F32 && nfk::ring_on()) ? 64u : 32u; }
 
 hipError_t launch_skinny(QFmt q, EType t, const void* A, const void* W, void* C, uint32_t M, uint32_t N,
                          uint32_t K, const Workspace& ws, hipStream_t s) {
+  if (t == EType::F32 && nfk::ring_on()) {
+    const GemvJob job{W, C, N};
+    const float* a = static_cast<const float*>(A);
+    const hipError_t e = q == QFmt::Q4_0 ? nfk::ring_dispatch<nfk::Q4_0>(a, &job, 1, M, K, ws, s)
+                                         : nfk::ring_dispatch<nfk::Q8_0>(a, &job, 1, M, K, ws, s);
+    if (e != hipErrorNotSupported) return e;
+    // declined (workspace): skinny_kernel, 32 rows per launch
+    for (uint32_t m0 = 0; m0 < M; m0 += 32) {
+      const uint32_t mc = M - m0 < 32 ? M - m0 : 32;
+      const float* am = a + (size_t)m0 * K;
+      float* cm = static_cast<float*>(C) + (size_t)m0 * N;
+      const hipError_t e2 = q == QFmt::Q4_0 ? nfk::skinny_dispatch<nfk::Q4_0, float>(am, W, cm, mc, N, K, ws, s)
+                                            : nfk::skinny_dispatch<nfk::Q8_0, float>(am, W, cm, mc, N, K, ws, s);
+      if (e2 != hipSuccess) return e2;
+    }
+    return hipSuccess;
+  }
   if (q == QFmt::Q4_0)
     return t == EType::F32 ? nfk::skinny_dispatch<nfk::Q4_0, float>(A, W, C, M, N, K, ws, s)
                            : nfk::skinny_dispatch<nfk::Q4_0, nfk::half_t>(A, W, C, M, N, K, ws, s);

@@ -149,6 +149,27 @@ def test_skinny_mfma_shapes(provider, oracle_mod, fmt, f16, shape):
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("shape", [(5, 300, 256), (16, 1000, 4096), (17, 257, 2048), (31, 130, 768),
+                                   (33, 520, 1024), (64, 4096, 512), (48, 33000, 256), (64, 66000, 256)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_skinny_ring_f32_edges(provider, oracle_mod, fmt, shape):
+    """The f32 small-batch kernel (weights through an LDS ring, activations
+    split once per workgroup): one, two and four 16-row activation tiles with
+    ragged M and N, a single chunk per workgroup and K split over
+    workgroups, and the 32- and 64-row waves of tall matrices (N >= 32768,
+    65536); up to 64 rows in one pass.  Each shape twice in a row (the
+    split-K arrival counters must be back at zero)."""
+    M, N, K = shape
+    old = provider.get_tuning()
+    try:
+        _force_path(provider, "skinny", False)
+        for rep in range(2):
+            check_fused(provider, oracle_mod, fmt, M, N, K, f16=False, seed=M * 5 + N + rep)
+    finally:
+        provider.set_tuning(old)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
 @pytest.mark.parametrize("shape", [(4, 300, 4096), (3, 130, 5632), (4, 64, 7168)], ids=lambda s: "x".join(map(str, s)))
 def test_gemv_large_activation_staging(provider, oracle_mod, fmt, f16, shape):
