@@ -569,8 +569,23 @@ __device__ __forceinline__ void sk_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Jobs of one ring launch: job j owns workgroups begin[j] .. begin[j+1]-1,
+// tiles[j] row tiles with its own K split kg[j] (tile-major: the kg[j]
+// workgroups of a tile are consecutive), and arrival counters
+// ctr[j] .. ctr[j] + tiles[j] - 1; a workgroup's partial tile sits at its
+// own index in the workspace.
+struct RingGroup {
+  const uint8_t* W[kSkGroupMax];
+  void* C[kSkGroupMax];
+  int N[kSkGroupMax];
+  int begin[kSkGroupMax + 1];
+  int kg[kSkGroupMax];
+  int ctr[kSkGroupMax];
+  int count;
+};
+
 template <class QF, int MT, int T, int CHP, int S>
-__global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restrict__ A, const SkinnyGroup grp, int M,
+__global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restrict__ A, const RingGroup grp, int M,
                                                          int K, float* __restrict__ ws_part,
                                                          uint32_t* __restrict__ ws_cnt) {
   int job = 0;
@@ -578,16 +593,19 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
   for (int q = 1; q < kSkGroupMax; ++q) job = (q < grp.count && (int)blockIdx.x >= grp.begin[q]) ? q : job;
   const uint8_t* __restrict__ W = grp.W[0];
   void* Cv = grp.C[0];
-  int N = grp.N[0], tile0 = grp.begin[0];
+  int N = grp.N[0], wg0 = grp.begin[0], KG = grp.kg[0], ctr0 = grp.ctr[0];
 #pragma unroll
   for (int q = 1; q < kSkGroupMax; ++q)
     if (job == q) {
       W = grp.W[q];
       Cv = grp.C[q];
       N = grp.N[q];
-      tile0 = grp.begin[q];
+      wg0 = grp.begin[q];
+      KG = grp.kg[q];
+      ctr0 = grp.ctr[q];
     }
   float* __restrict__ C = static_cast<float*>(Cv);
+  const int local = (int)blockIdx.x - wg0, tile = local / KG, kg = local - tile * KG;
   typedef RingGeom<QF, MT, T, CHP> G;
   constexpr bool kQ4 = SkW<QF>::kLoads == 5;
   constexpr int WL = SkW<QF>::kLoads;
@@ -600,8 +618,7 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, s = lane >> 4;
   const int NC = (K >> 6) / CHP;
-  const int n0 = ((int)blockIdx.x - tile0) * (NW * RW) + wave * RW;  // this wave's first row
-  const int KG = gridDim.y, kg = blockIdx.y;
+  const int n0 = tile * (NW * RW) + wave * RW;  // this wave's first row
   const int c_begin = (int)((long)NC * kg / KG), c_end = (int)((long)NC * (kg + 1) / KG);
 
   // Weight loads: dword f = lane + 64j of the wave's RW x kWRow chunk is row
@@ -781,7 +798,7 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
   // last workgroup reads the KG tiles back in order kg = 0..KG-1, all of a
   // thread's loads of one tile issued before any is added.
   constexpr int NQ = MT * T;
-  const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)blockIdx.x * KG * (NQ * 512),
+  const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)(wg0 + tile * KG) * (NQ * 512),
                              (uint32_t)(KG * NQ * 512 * 16));
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -791,7 +808,7 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
   __syncthreads();
   __shared__ uint32_t is_last;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&ws_cnt[ctr0 + tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == (uint32_t)(KG - 1);
   }
   __syncthreads();
@@ -813,7 +830,7 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
     for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) store(mt, t, i, acc[mt][t][i]);
-  if (tid == 0) __hip_atomic_store(&ws_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(&ws_cnt[ctr0 + tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Ring geometry per format, activation tiles (MT) and weight tiles per wave
@@ -878,50 +895,53 @@ int ring_split(long tiles, uint32_t K, const nfhip::Workspace& ws) {
 }
 
 template <class QF, int MT, int T>
-hipError_t ring_launch_group(const float* A, const SkinnyGroup& grp, long tiles, uint32_t M, uint32_t K, int kg,
+hipError_t ring_launch_group(const float* A, const RingGroup& grp, long wgs, uint32_t M, uint32_t K,
                              const nfhip::Workspace& ws, hipStream_t s) {
   typedef RingCfg<QF, MT, T> Cfg;
   if constexpr (!Cfg::kOk) {
     return hipErrorNotSupported;
   } else {
     constexpr int CHP = Cfg::kCHP, S = Cfg::kS;
-    if (kg > 1 && (tiles > (long)ws.cnt_len || (size_t)tiles * kg * MT * T * 512 * 4 > ws.part_floats))
-      return hipErrorNotSupported;
     if ((K / 64) % CHP != 0) return hipErrorNotSupported;
     static const hipError_t attr =
         hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_ring_kernel<QF, MT, T, CHP, S>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::kLds);
     if (attr != hipSuccess) return attr;
-    skinny_ring_kernel<QF, MT, T, CHP, S><<<dim3((unsigned)tiles, (unsigned)kg), dim3(512), Cfg::kLds, s>>>(
-        A, grp, (int)M, (int)K, ws.part, ws.cnt);
+    skinny_ring_kernel<QF, MT, T, CHP, S><<<dim3((unsigned)wgs), dim3(512), Cfg::kLds, s>>>(A, grp, (int)M, (int)K,
+                                                                                          ws.part, ws.cnt);
     return hipGetLastError();
   }
 }
 
-// One launch for n jobs (n = 1: a single linear) over the same activations:
-// every job gets the geometry and K split a launch of its own would (so its
-// output is bit-identical to that launch); otherwise hipErrorNotSupported.
+// One launch for n jobs (n = 1: a single linear) over the same activations,
+// each with the geometry and K split a launch of its own would get (so its
+// output is bit-identical to that launch); hipErrorNotSupported if the
+// jobs need different row tiles per wave or exceed the workspace.
 template <class QF, int MT, int T>
 hipError_t ring_group_t(const float* A, const nfhip::GemvJob* jobs, uint32_t n, uint32_t M, uint32_t K,
                         const nfhip::Workspace& ws, hipStream_t s) {
-  SkinnyGroup grp{};
-  long tiles = 0;
-  int kg0 = 0;
+  RingGroup grp{};
+  long wgs = 0, tiles = 0;
+  bool split = false;
   for (uint32_t j = 0; j < n; ++j) {
     if (ring_t<QF, MT>(jobs[j].N) != T) return hipErrorNotSupported;
     const long t = ((long)jobs[j].N + 128 * T - 1) / (128 * T);
     const int kg = ring_split<QF, MT, T>(t, K, ws);
-    if (j == 0) kg0 = kg;
-    else if (kg != kg0) return hipErrorNotSupported;
+    split = split || kg > 1;
     grp.W[j] = static_cast<const uint8_t*>(jobs[j].W);
     grp.C[j] = jobs[j].C;
     grp.N[j] = (int)jobs[j].N;
-    grp.begin[j] = (int)tiles;
+    grp.begin[j] = (int)wgs;
+    grp.kg[j] = kg;
+    grp.ctr[j] = (int)tiles;
+    wgs += t * kg;
     tiles += t;
   }
-  for (int q = (int)n; q <= kSkGroupMax; ++q) grp.begin[q] = (int)tiles;
+  if (split && (tiles > (long)ws.cnt_len || (size_t)wgs * MT * T * 512 * 4 > ws.part_floats))
+    return hipErrorNotSupported;
+  for (int q = (int)n; q <= kSkGroupMax; ++q) grp.begin[q] = (int)wgs;
   grp.count = (int)n;
-  return ring_launch_group<QF, MT, T>(A, grp, tiles, M, K, kg0, ws, s);
+  return ring_launch_group<QF, MT, T>(A, grp, wgs, M, K, ws, s);
 }
 
 template <class QF, int MT>
