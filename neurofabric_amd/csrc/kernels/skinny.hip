@@ -843,10 +843,7 @@ struct RingCfg {
   typedef RingGeom<QF, MT, T, kCHP> G;
   static constexpr int kFree = 160 * 1024 / 4 - 2 * G::kXB - 64;  // dwords (64 for the static LDS)
   static constexpr int kSLds = kFree / G::kStage, kSVm = 2 + 63 / G::kJW;  // LDS, vmcnt field
-#ifndef NF_RING_MAX_S
-#define NF_RING_MAX_S 4
-#endif
-  static constexpr int kSMax = NF_RING_MAX_S;
+  static constexpr int kSMax = 4;  // deeper rings measured slower (fewer workgroups per CU)
   static constexpr int kS = kSLds < kSVm ? (kSLds < kSMax ? kSLds : kSMax) : (kSVm < kSMax ? kSVm : kSMax);
   static constexpr bool kOk = kS >= 3;
   static constexpr int kLds = (kS * G::kStage + 2 * G::kXB) * 4;

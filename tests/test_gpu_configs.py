@@ -1,10 +1,11 @@
 """Oracle parity at the full BASELINE.json config shapes, through the C ABI.
 
-configs[1] TinyLlama q/o and gate/up at M = 4 and 16; configs[2] Llama-2-7B
-prefill at M = 2048 (the non-split tiled GEMM grid); configs[3] Llama-3-8B
-Q8_0 FFN shapes and the 128256 x 4096 lm_head at M = 1, 16 and 64 (f32
-activations: GEMV, small-batch kernel, bf16-piece tiled GEMM), and the FFN
-shapes through the f32 families the switch points do not pick;
+configs[1] TinyLlama q/o and gate/up at M = 1, 4 and 16; configs[2]
+Llama-2-7B prefill at M = 512 (the K-split grid of the 4096-row outputs) and
+M = 2048 (the non-split tiled GEMM grid); configs[3] Llama-3-8B Q8_0 q/o,
+FFN shapes and the 128256 x 4096 lm_head at M = 1, 16 and 64 (f32
+activations: GEMV, small-batch kernel), and the FFN shapes through the f32
+families the switch points do not pick;
 configs[4] the Llama-70B FFN pair at every M of the crossover sweep, through
 the kernel the switch points select and through each kernel family forced.
 
@@ -122,13 +123,19 @@ class forced:
 
 # ---- TinyLlama decode projections not covered elsewhere ----------------
 
-@pytest.mark.parametrize("M", [4, 16])
+@pytest.mark.parametrize("M", [1, 4, 16])
 @pytest.mark.parametrize("NK", [(2048, 2048), (5632, 2048)], ids=["q_o", "gate_up"])
 def test_config1_q_o_gate_up(provider, oracle_mod, weights, M, NK):
     check_config(provider, oracle_mod, weights, "q4_0", M, *NK, f16=False, seed=M + NK[0])
 
 
-# ---- Llama-2-7B prefill at M = 2048 -------------------------------------
+# ---- Llama-2-7B prefill at M = 512 and 2048 ----------------------------
+
+@pytest.mark.parametrize("NK", [(4096, 4096), (11008, 4096), (4096, 11008)], ids=["qkvo", "gate_up", "down"])
+def test_config2_prefill_m512(provider, oracle_mod, weights, NK):
+    k = check_config(provider, oracle_mod, weights, "q4_0", 512, *NK, f16=True, seed=NK[0] + 5)
+    assert k.startswith("gemm_mfma"), k
+
 
 @pytest.mark.parametrize("NK", [(4096, 4096), (11008, 4096), (4096, 11008)], ids=["qkvo", "gate_up", "down"])
 def test_config2_prefill_m2048(provider, oracle_mod, weights, NK):
@@ -139,7 +146,8 @@ def test_config2_prefill_m2048(provider, oracle_mod, weights, NK):
 # ---- Llama-3-8B Q8_0 decode ------------------------------------------------
 
 @pytest.mark.parametrize("M", [1, 16, 64])
-@pytest.mark.parametrize("NK", [(14336, 4096), (4096, 14336), (128256, 4096)], ids=["gate_up", "down", "lm_head"])
+@pytest.mark.parametrize("NK", [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)],
+                         ids=["q_o", "gate_up", "down", "lm_head"])
 def test_config3_q8_0_ffn_and_lm_head(provider, oracle_mod, weights, M, NK):
     check_config(provider, oracle_mod, weights, "q8_0", M, *NK, f16=False, seed=M * 5 + NK[0])
 
