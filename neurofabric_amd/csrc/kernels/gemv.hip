@@ -19,9 +19,9 @@
 //     dwords are realigned with v_alignbyte; the second block's codes are
 //     already dword aligned.
 //   * The activations (M rows of K) are staged once per workgroup in LDS,
-//     64-element pair by pair, with the 16-byte chunks of a pair XOR-
-//     swizzled by the pair index so the 16 lanes of a ds_read_b128 phase hit
-//     16 different bank groups.
+//     64-element pair by pair, each pair followed by one 16-byte chunk of
+//     padding (xslot), so the 16 lanes of a ds_read_b128 phase hit 16
+//     different bank groups.
 //   * A row is covered by a group of L lanes (L = 16, 32 or 64, chosen on the
 //     host so the pairs of a row spread evenly); a wave holds 64/L groups and
 //     each group works on R2 rows at once, reading each activation chunk
