@@ -540,8 +540,13 @@ struct RingGeom {
   static constexpr int kRW = 16 * T;                   // weight rows per wave
   static constexpr int kWRow = CHP * kPD;              // dwords per staged weight row
   static constexpr int kWDw = kRW * kWRow;             // weight dwords of a wave per chunk
-  static constexpr int kJW = (kWDw + 63) / 64;         // dword loads per lane per chunk (last one partial)
-  static constexpr int kStage = kWaves * kWDw;         // dwords of a stage
+  static constexpr int kJW = (kWDw + 63) / 64;         // dword loads per lane per chunk
+  // A wave's area in a stage is padded to whole loads: every lane issues all
+  // kJW loads (lanes past kWDw reload the last dword into the padding), so
+  // no load sits behind a lane-dependent branch, which made the compiler's
+  // wait analysis drop count and wait for loads issued an iteration later.
+  static constexpr int kWArea = kJW * 64;
+  static constexpr int kStage = kWaves * kWArea;       // dwords of a stage
   static constexpr int kUnits = CHP * 2 * MT * 64;     // A operands (lane slots) per chunk
   static constexpr int kUPT = (kUnits + 511) / 512;    // A operands per thread
   static constexpr int kXB = kUnits * 8;               // dwords of one split buffer (two bf16x8 each)
@@ -583,6 +588,9 @@ struct RingGroup {
   int ctr[kSkGroupMax];
   int count;
 };
+
+// Partial-tile loads (float4 per thread) the split-K fix-up keeps in flight.
+constexpr int kRingGatherF4 = 16;
 
 template <class QF, int MT, int T, int CHP, int S>
 __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restrict__ A, const RingGroup grp, int M,
@@ -638,12 +646,9 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
     const bool live = c < c_end;
     const __amdgpu_buffer_rsrc_t rw = sk_rsrc(W, __builtin_amdgcn_readfirstlane(live ? w_bytes : 0u));
     const uint32_t wo = __builtin_amdgcn_readfirstlane(live ? (uint32_t)c * (uint32_t)(CHP * G::kPB) : 0u);
-    uint32_t* wsb = smem + st * G::kStage + wave * G::kWDw;
+    uint32_t* wsb = smem + st * G::kStage + wave * G::kWArea;
 #pragma unroll
-    for (int j = 0; j < G::kJW; ++j) {
-      // the last load's lanes past the wave's dwords stay idle (exec mask)
-      if (G::kWDw % 64 == 0 || j + 1 < G::kJW || lane < G::kWDw % 64) sk_dma4(rw, wsb + 64 * j, wsrc[j], wo);
-    }
+    for (int j = 0; j < G::kJW; ++j) sk_dma4(rw, wsb + 64 * j, wsrc[j], wo);
   };
 
   // A operands: unit u = ((pi * 2 + h) * MT + mt) * 64 + l is the operand of
@@ -666,24 +671,25 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
     xoff[k] = ((uint32_t)mm * (uint32_t)K + (uint32_t)(64 * pi + 32 * h + (kQ4 ? 4 : 8) * (l >> 4))) * 4u;
   }
   const uint32_t x_bytes = (uint32_t)M * (uint32_t)K * 4u;
-  float4v xr[UPT][2];
-  auto load_x = [&](int c) {
+  typedef float4v XSet[UPT][2];
+  XSet xr[2];  // activations of two chunks in registers (two chunks ahead)
+  auto load_x = [&](int c, XSet& x) {
     const bool live = c < c_end;
     const __amdgpu_buffer_rsrc_t rx = sk_rsrc(A, __builtin_amdgcn_readfirstlane(live ? x_bytes : 0u));
     const uint32_t xo = __builtin_amdgcn_readfirstlane(live ? (uint32_t)c * (CHP * 256u) : 0u);
 #pragma unroll
     for (int k = 0; k < UPT; ++k) {
-      xr[k][0] = __builtin_bit_cast(float4v, sk_buf_load<16>(rx, xoff[k], xo));
-      xr[k][1] = __builtin_bit_cast(float4v, sk_buf_load<16>(rx, xoff[k] + (kQ4 ? 64u : 16u), xo));
+      x[k][0] = __builtin_bit_cast(float4v, sk_buf_load<16>(rx, xoff[k], xo));
+      x[k][1] = __builtin_bit_cast(float4v, sk_buf_load<16>(rx, xoff[k] + (kQ4 ? 64u : 16u), xo));
     }
   };
-  auto split_x = [&](uint32_t* xb) {
+  auto split_x = [&](uint32_t* xb, const XSet& x) {
 #pragma unroll
     for (int k = 0; k < UPT; ++k) {
       if (xlive[k]) {
         const int u = tid + 512 * k;
-        const float xv[8] = {xr[k][0].x, xr[k][0].y, xr[k][0].z, xr[k][0].w,
-                             xr[k][1].x, xr[k][1].y, xr[k][1].z, xr[k][1].w};
+        const float xv[8] = {x[k][0].x, x[k][0].y, x[k][0].z, x[k][0].w,
+                             x[k][1].x, x[k][1].y, x[k][1].z, x[k][1].w};
         bf16x8 a1, a2;
         split2(xv, a1, a2);
         uint32_t* dst = xb + (((u >> 6) * 2) * 64 + (u & 63)) * 4;
@@ -704,7 +710,7 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
     for (int t = 0; t < T; ++t) acc[mt][t] = float4v{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](int st, const uint32_t* xb) {
-    const uint32_t* wsb = smem + st * G::kStage + wave * G::kWDw;
+    const uint32_t* wsb = smem + st * G::kStage + wave * G::kWArea;
 #pragma unroll
     for (int pi = 0; pi < CHP; ++pi)
 #pragma unroll
@@ -751,33 +757,57 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
       }
   };
 
-  // Pipeline.  Before the loop: weights of chunks c_begin .. c_begin+S-2 go
-  // out, chunk 0's activations are loaded and split.  Iteration i waits for
-  // chunk i's weights (at most S-2 younger chunks' weight loads in flight;
-  // every thread issues the same number per chunk, in chunk order, so the
-  // count is exact) and for its own split stores; one barrier then makes
-  // chunk i's weights and split operands visible and retires chunk i-1 (its
-  // stage receives chunk i+S-1, its split buffer the split of chunk i+1).
-  // Chunk i+1's activations are requested first (the compiler's own wait
-  // before the split counts the weight loads issued after them), chunk i
-  // computes, chunk i+1 is split.
+  // Pipeline.  Before the loop: chunk 0's activations, the weights of
+  // chunks c_begin .. c_begin+S-3, chunk 1's activations and chunk S-2's
+  // weights go out, in that order (the order of the loop's own issue, so the
+  // loads pending at the loop entry match those pending around the loop and
+  // the compiler's waits stay exact), and chunk 0 is split.  Iteration i
+  // (activation register set p = i & 1):
+  //   wait for chunk i's weights and for its own split stores, then one
+  //   barrier makes chunk i's weights and split operands visible and retires
+  //   chunk i-1 (its stage receives chunk i+S-1, its split buffer the split
+  //   of chunk i+1);
+  //   chunk i+2's activations are requested into set p (chunk i's, split in
+  //   iteration i-1), then chunk i+S-1's weights;
+  //   chunk i computes, and chunk i+1 (set p^1, requested one iteration
+  //   earlier) is split.
+  // Loads complete in issue order, so the activations are requested two
+  // chunks ahead: the split's wait then covers only loads issued an
+  // iteration earlier (with them one chunk ahead, it also waited for the
+  // weight loads issued just before them).  Measured on MI355X: Llama-3-8B
+  // Q8_0 decode step 5.30 -> 5.21 ms at M = 64, 3.31 -> 3.20 ms at M = 16;
+  // 14336 x 4096 at M = 64 stays at about 1.4 us per chunk, which the load
+  // order therefore does not set.  Every thread issues the same loads per
+  // chunk (2 * UPT activation, kJW weight), so the counts below are exact:
+  // after chunk i's weights come at most S-2 chunks of weight loads and one
+  // of activation loads.
+  static_assert((S - 2) * G::kJW + 2 * UPT <= 63, "vmcnt field");
   const int nch = c_end - c_begin;
-  load_x(c_begin);
+  load_x(c_begin, xr[0]);
 #pragma unroll
-  for (int i = 0; i < S - 1; ++i) fetch_w(c_begin + i, i);
-  split_x(xb0);
-  for (int i = 0; i < nch; ++i) {
+  for (int i = 0; i < S - 2; ++i) fetch_w(c_begin + i, i);
+  load_x(c_begin + 1, xr[1]);
+  fetch_w(c_begin + S - 2, S - 2);
+  split_x(xb0, xr[0]);
+  auto iteration = [&](auto pc, int i) {
+    constexpr int p = decltype(pc)::value;
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(sk_vmcnt_imm((S - 2) * G::kJW) & ~0x0F00);
+    __builtin_amdgcn_s_waitcnt(sk_vmcnt_imm((S - 2) * G::kJW + 2 * UPT) & ~0x0F00);
     sk_barrier();
-    load_x(c_begin + i + 1);
+    load_x(c_begin + i + 2, xr[p]);
     __builtin_amdgcn_sched_barrier(0);
     fetch_w(c_begin + i + S - 1, (i + S - 1) % S);
     __builtin_amdgcn_sched_barrier(0);
-    compute(i % S, xb0 + (i & 1) * G::kXB);
+    compute(i % S, xb0 + p * G::kXB);
     __builtin_amdgcn_sched_barrier(0);
-    split_x(xb0 + ((i + 1) & 1) * G::kXB);
+    split_x(xb0 + (p ^ 1) * G::kXB, xr[p ^ 1]);
+  };
+  int i = 0;
+  for (; i + 2 <= nch; i += 2) {
+    iteration(std::integral_constant<int, 0>{}, i);
+    iteration(std::integral_constant<int, 1>{}, i + 1);
   }
+  if (i < nch) iteration(std::integral_constant<int, 0>{}, i);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   auto store = [&](int mt, int t, int i, float v) {
@@ -795,8 +825,11 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
   }
   // K split across workgroups: park this tile (float4 (mt*T + t) of thread
   // tid at index (mt*T + t) * 512 + tid, sc1 stores), count arrivals; the
-  // last workgroup reads the KG tiles back in order kg = 0..KG-1, all of a
-  // thread's loads of one tile issued before any is added.
+  // last workgroup reads the KG tiles back and adds them in order kg =
+  // 0..KG-1.  The loads of GB tiles are issued before any of them is added
+  // (indices past KG - 1 reload the last tile and are not added): each load
+  // is a round trip to the level all XCDs share, so one tile per round trip
+  // made the fix-up of a 16-way split take about 16 of them.
   constexpr int NQ = MT * T;
   const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)(wg0 + tile * KG) * (NQ * 512),
                              (uint32_t)(KG * NQ * 512 * 16));
@@ -813,16 +846,26 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
   }
   __syncthreads();
   if (!is_last) return;
-  for (int g = 0; g < KG; ++g) {
-    float4v p[MT][T];
+  constexpr int GB = NQ >= kRingGatherF4 ? 1 : kRingGatherF4 / NQ;
+  for (int g0 = 0; g0 < KG; g0 += GB) {
+    float4v p[GB][MT][T];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int gb = 0; gb < GB; ++gb) {
+      const int g = g0 + gb < KG ? g0 + gb : KG - 1;
 #pragma unroll
-      for (int t = 0; t < T; ++t) p[mt][t] = tile_ws.load((uint32_t)g * (NQ * 512) + (mt * T + t) * 512 + tid);
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+        for (int t = 0; t < T; ++t) p[gb][mt][t] = tile_ws.load((uint32_t)g * (NQ * 512) + (mt * T + t) * 512 + tid);
+    }
 #pragma unroll
-      for (int t = 0; t < T; ++t) acc[mt][t] = g == 0 ? p[mt][t] : acc[mt][t] + p[mt][t];
+    for (int gb = 0; gb < GB; ++gb) {
+      const int g = g0 + gb;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          acc[mt][t] = g == 0 ? p[gb][mt][t] : (g < KG ? acc[mt][t] + p[gb][mt][t] : acc[mt][t]);
+    }
   }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -842,7 +885,7 @@ struct RingCfg {
   static constexpr int kCHP = MT == 1 ? 2 : 1;
   typedef RingGeom<QF, MT, T, kCHP> G;
   static constexpr int kFree = 160 * 1024 / 4 - 2 * G::kXB - 64;  // dwords (64 for the static LDS)
-  static constexpr int kSLds = kFree / G::kStage, kSVm = 2 + 63 / G::kJW;  // LDS, vmcnt field
+  static constexpr int kSLds = kFree / G::kStage, kSVm = 2 + (63 - 2 * G::kUPT) / G::kJW;  // LDS, vmcnt field
   static constexpr int kSMax = 4;  // deeper rings measured slower (fewer workgroups per CU)
   static constexpr int kS = kSLds < kSVm ? (kSLds < kSMax ? kSLds : kSMax) : (kSVm < kSMax ? kSVm : kSMax);
   static constexpr bool kOk = kS >= 3;
