@@ -1,8 +1,9 @@
 """nf_hip_run_tasks merges adjacent decode GEMVs and small-batch linears
-that read the same activation buffer (q/k/v, gate/up) into one launch.  Each merged result must
-be bit-identical to dispatching the tasks one by one, the launch count must
-show the merge, and a hazard between two tasks (here: both write the same
-output) must keep them in separate launches."""
+that read the same activation buffer (q/k/v, gate/up) into one launch.  Each
+result must be bit-identical to dispatching the tasks one by one, the launch
+count must show the merge, and a hazard between two tasks (here: both write
+the same output; a weight buffer written mid-list; each task reading the
+previous one's output) must keep the order."""
 import ctypes as C
 
 import numpy as np
@@ -165,4 +166,46 @@ def test_run_tasks_chain_bit_identical(provider, fmt):
             assert np.array_equal(got[i].view(np.uint32), c.download(np.float32).view(np.uint32)), i
     finally:
         for b in bufs:
+            b.release()
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("dims", [(2048, 1024, 64, 5632, 2048, 128, 4096), (512, 256, 64, 256, 1024)],
+                         ids=["mixed", "small"])
+def test_run_tasks_dependent_sequence(provider, oracle_mod, fmt, f16, dims):
+    """Decode GEMVs where each reads the previous one's output (layer i:
+    K = dims[i], N = dims[i+1]), some with few rows: one launch each (no
+    two share an input), bit-identical to one dispatch each, in order; the
+    first layer against the oracle."""
+    M = 1
+    adt = abi.NF_DTYPE_F16 if f16 else abi.NF_DTYPE_F32
+    npdt = np.float16 if f16 else np.float32
+    op = f"dequant_{fmt}_linear" + ("_f16" if f16 else "")
+    x0 = syn.activations(M, dims[0], seed=31, dtype=npdt)
+    acts = [provider.alloc_array(x0, adt)] + [provider.alloc(adt, M * n * x0.itemsize) for n in dims[1:]]
+    host_w, ws, tasks = [], [], []
+    for i in range(len(dims) - 1):
+        K, N = dims[i], dims[i + 1]
+        host_w.append(syn.weights(fmt, N, K, seed=40 + i))
+        ws.append(provider.alloc_array(host_w[-1], QDT[fmt]))
+        tasks.append(provider.task(op, [acts[i], ws[-1]], [acts[i + 1]], M, N, K))
+    try:
+        before = provider.launch_count()
+        provider.run_tasks(_array(tasks), 1)
+        provider.synchronize()
+        assert provider.launch_count() - before == len(tasks)
+        chained = [a.download(npdt).copy() for a in acts[1:]]
+        for t_i in range(len(tasks)):
+            K, N = dims[t_i], dims[t_i + 1]
+            provider.dispatch(op, [acts[t_i], ws[t_i]], [acts[t_i + 1]], M, N, K)
+        provider.synchronize()
+        for i, a in enumerate(acts[1:]):
+            assert np.array_equal(chained[i].view(np.uint8), a.download(npdt).view(np.uint8)), f"layer {i}"
+        ref = oracle_mod.fused(x0, host_w[0], fmt, M, dims[1], dims[0], f16=f16, threads=8)
+        if f16:
+            ref = ref.view(np.float16)
+        assert_close(chained[0].reshape(M, dims[1]).astype(np.float32), ref.astype(np.float32), what=f"{fmt} layer 0")
+    finally:
+        for b in acts + ws:
             b.release()
