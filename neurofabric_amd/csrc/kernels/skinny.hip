@@ -774,10 +774,11 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
   // Loads complete in issue order, so the activations are requested two
   // chunks ahead: the split's wait then covers only loads issued an
   // iteration earlier (with them one chunk ahead, it also waited for the
-  // weight loads issued just before them).  Measured on MI355X: Llama-3-8B
-  // Q8_0 decode step 5.30 -> 5.21 ms at M = 64, 3.31 -> 3.20 ms at M = 16;
-  // 14336 x 4096 at M = 64 stays at about 1.4 us per chunk, which the load
-  // order therefore does not set.  Every thread issues the same loads per
+  // weight loads issued just before them).  Measured on MI355X with the
+  // batched fix-up below (same box, against the previous kernel): Llama-3-8B
+  // Q8_0 decode step 5.31 -> 5.17 ms at M = 64, 3.32 -> 3.11 ms at M = 16,
+  // TinyLlama Q4_0 M = 16 961 -> 940 us; 14336 x 4096 at M = 64 stays at
+  // about 1.4 us per chunk, which the load order therefore does not set.  Every thread issues the same loads per
   // chunk (2 * UPT activation, kJW weight), so the counts below are exact:
   // after chunk i's weights come at most S-2 chunks of weight loads and one
   // of activation loads.
@@ -826,10 +827,10 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
   // K split across workgroups: park this tile (float4 (mt*T + t) of thread
   // tid at index (mt*T + t) * 512 + tid, sc1 stores), count arrivals; the
   // last workgroup reads the KG tiles back and adds them in order kg =
-  // 0..KG-1.  The loads of GB tiles are issued before any of them is added
-  // (indices past KG - 1 reload the last tile and are not added): each load
-  // is a round trip to the level all XCDs share, so one tile per round trip
-  // made the fix-up of a 16-way split take about 16 of them.
+  // 0..KG-1.  The loads of up to GB tiles are issued before any of them is
+  // added: each load is a round trip to the level all XCDs share, so one
+  // tile per round trip made the fix-up of a 16-way split take about 16 of
+  // them.
   constexpr int NQ = MT * T;
   const CoherentTile tile_ws(reinterpret_cast<float4v*>(ws_part) + (size_t)(wg0 + tile * KG) * (NQ * 512),
                              (uint32_t)(KG * NQ * 512 * 16));
@@ -851,20 +852,23 @@ __global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restric
     float4v p[GB][MT][T];
 #pragma unroll
     for (int gb = 0; gb < GB; ++gb) {
-      const int g = g0 + gb < KG ? g0 + gb : KG - 1;
+      const int g = g0 + gb;
+      if (g < KG) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int t = 0; t < T; ++t) p[gb][mt][t] = tile_ws.load((uint32_t)g * (NQ * 512) + (mt * T + t) * 512 + tid);
+          for (int t = 0; t < T; ++t) p[gb][mt][t] = tile_ws.load((uint32_t)g * (NQ * 512) + (mt * T + t) * 512 + tid);
+      }
     }
 #pragma unroll
     for (int gb = 0; gb < GB; ++gb) {
       const int g = g0 + gb;
+      if (g < KG) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-          acc[mt][t] = g == 0 ? p[gb][mt][t] : (g < KG ? acc[mt][t] + p[gb][mt][t] : acc[mt][t]);
+          for (int t = 0; t < T; ++t) acc[mt][t] = g == 0 ? p[gb][mt][t] : acc[mt][t] + p[gb][mt][t];
+      }
     }
   }
 #pragma unroll
