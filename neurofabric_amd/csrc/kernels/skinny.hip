@@ -935,6 +935,13 @@ int ring_split(long tiles, uint32_t K, const nfhip::Workspace& ws) {
   while (tiles * kg * 2 <= target && NC >= min_chunks * kg * 2 && tiles <= (long)ws.cnt_len &&
          (size_t)tiles * kg * 2 * NQ * 512 * 4 <= ws.part_floats)
     kg *= 2;
+  // Longer K ranges (at least 8 chunks) where the launch keeps at least 128
+  // workgroups: each split adds a partial tile written and read back.
+  // Measured on MI355X: Llama-3-8B Q8_0 decode step at M = 16 3.11 ->
+  // 3.01 ms (4096-row linears at K = 4096: 4 splits of 8 chunks instead of 8
+  // of 4); TinyLlama at M = 16 keeps its splits (fewer workgroups there
+  // took the step from 0.94 to 1.12 ms).
+  while (kg > 1 && NC / kg < 8 && tiles * (kg / 2) >= 128) kg /= 2;
   return kg;
 }
 
