@@ -148,13 +148,15 @@ NF_API uint32_t nf_hip_get_skinny_f16_max_k(void);
  * from measurement on MI355X (two waves per SIMD with 32-row waves up to
  * M = 32 and 64-row waves up to M = 64 or while ceil(M/64) x ceil(N/256) is
  * at most 80 (Q4_0) / 64 (Q8_0) with K <= 16384; 128-row waves for the other
- * Q4_0 batches;
+ * Q4_0 batches, on 128-column tiles when ceil(M/128) x ceil(N/256) x K/128 <=
+ * 4096;
  * one wave per SIMD otherwise; the two-wave kernels need K % 128 == 0); 0..6 = the kernel that dequantizes weight tiles into LDS,
  * tile shape 256x256, 256x128, 128x128, 256x128 with 4 waves, 256x128 with
  * 4 waves and 3 stages, 128x128 with 3 stages, 128x256; 7 = the
  * register-dequantizing kernel with one wave per SIMD for every shape;
  * 8 / 9 / 10 = the two-wave kernel with 128 / 64 / 32-row waves wherever it
- * applies (K % 128 == 0; 8: Q4_0 only), else as 7.  With f32 activations
+ * applies (K % 128 == 0; 8: Q4_0 only), else as 7; 11 = its 128-row waves
+ * on 128-column tiles (Q4_0 only), else as 7.  With f32 activations
  * (the bf16-piece kernel) 8 / 9 force its 128- / 64-row waves.
  * Other values mean -1.  Environment override NF_HIP_GEMM_TILE (the shape
  * name or number) is read at nf_plugin_register.  No counterpart in the

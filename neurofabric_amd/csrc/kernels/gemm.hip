@@ -1922,12 +1922,22 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
     //     projection shapes, at M = 512 41.9 / 77.4 / 69.9 against 45.6 /
     //     78.6 / 76.4 us (within 2 % either way on the 28672-row FFN
     //     shapes);
+    //     but Q4_0 batches whose 128 x 256 grid holds little work
+    //     (ceil(M/128) x ceil(N/256) x K/128 <= 4096 step pairs) take
+    //     128 x 128 tiles (two waves per K group), which double the
+    //     workgroups and halve each split-K partial: 4096x4096 M = 384 /
+    //     512 / 1024 34.5 / 36.4 / 50.6 against 37.0 / 40.5 / 55.6 us,
+    //     2048x4096 M = 1024 35.5 against 40.3, 1024x4096 M = 2048 34.5
+    //     against 38.9, 4096x8192 M = 512 55.1 against 57.7; above that
+    //     bound they lost (8192x8192 M = 512 95.0 against 92.2, 11008x4096
+    //     M = 512 91.8 against 72.7, 4096x11008 M = 512 73.4 against 70.8,
+    //     4096x4096 M = 2048 91.4 against 79.8 us);
     //   * otherwise one wave per SIMD (gemm_wq_kernel; also Q8_0 at larger
     //     M, where the two-wave kernel measured 5-12 % slower);
     // all of them need K % 128 == 0 but gemm_wq_kernel.  Tile 7 forces the
     // one-wave kernel, tiles 8 / 9 / 10 the two-wave kernel with 128 / 64 /
-    // 32-row waves (8: Q4_0 only); 0..6 select one of the LDS-staged tile
-    // shapes.
+    // 32-row waves (8: Q4_0 only), tile 11 the 128-row waves on 128 x 128
+    // tiles (Q4_0 only); 0..6 select one of the LDS-staged tile shapes.
     const bool k128 = K % 128 == 0;
     const bool q4 = q == QFmt::Q4_0;
     const long tiles64 = (long)((M + 63) / 64) * (long)((N + 255) / 256);
@@ -1937,6 +1947,9 @@ hipError_t launch_gemm_mfma(QFmt q, EType t, const void* A, const void* W, void*
     if ((tile == 9 || (tile < 0 && (M <= 64 || (tiles64 <= (q4 ? 80 : 64) && K <= 16384)))) && k128)
       return q4 ? nfk::gemm_wq2_launch<nfk::Q4_0, 2, 4>(a, w, c, M, N, K, ws, s)
                 : nfk::gemm_wq2_launch<nfk::Q8_0, 2, 4>(a, w, c, M, N, K, ws, s);
+    const long pairs128 = (long)((M + 127) / 128) * (long)((N + 255) / 256) * (long)(K / 128);
+    if ((tile == 11 || (tile < 0 && pairs128 <= 4096)) && k128 && q4)
+      return nfk::gemm_wq2_launch<nfk::Q4_0, 4, 2>(a, w, c, M, N, K, ws, s);
     if ((tile == 8 || tile < 0) && k128 && q4)
       return nfk::gemm_wq2_launch<nfk::Q4_0, 4, 4>(a, w, c, M, N, K, ws, s);
     if (tile < 0 || tile > 6)

@@ -236,11 +236,12 @@ nf_status make_plan(const char* op_name, const nf_tensor_desc* const* ins, uint3
 int gemm_tile_from_name(const char* name) {
   if (!name) return -1;
   static const char* const kNames[] = {"256x256", "256x128", "128x128", "256x128w4",
-                                       "256x128w4s3", "128x128s3", "128x256", "wq1", "wq2", "wq2m64", "wq2m32"};
-  for (int i = 0; i < 11; ++i)
+                                       "256x128w4s3", "128x128s3", "128x256", "wq1", "wq2", "wq2m64", "wq2m32", "wq2n128"};
+  for (int i = 0; i < 12; ++i)
     if (std::strcmp(name, kNames[i]) == 0) return i;
   if (name[0] >= '0' && name[0] <= '9' && name[1] == '\0') return name[0] - '0';
   if (std::strcmp(name, "10") == 0) return 10;
+  if (std::strcmp(name, "11") == 0) return 11;
   return -1;
 }
 

@@ -1070,7 +1070,7 @@ NF_API uint32_t nf_hip_get_skinny_f16_max_k(void) {
 
 NF_API void nf_hip_set_gemm_tile(int32_t tile) {
   std::lock_guard<std::mutex> lk(g_prov.mu);
-  g_prov.tuning.gemm_tile = (tile >= 0 && tile <= 10) ? tile : -1;
+  g_prov.tuning.gemm_tile = (tile >= 0 && tile <= 11) ? tile : -1;
 }
 
 NF_API int32_t nf_hip_get_gemm_tile(void) {

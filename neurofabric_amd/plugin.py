@@ -374,8 +374,9 @@ class Provider:
         """-1: register-dequantizing GEMM kernels picked by M (default); 0..6:
         LDS-staged tile shapes; 7: the one-wave-per-SIMD register kernel;
         8 / 9 / 10: the two-wave kernel with 128 / 64 / 32-row waves wherever
-        it applies (K % 128 == 0; 8: Q4_0 only); with f32 activations 8 / 9
-        force the bf16-piece kernel's 128- / 64-row waves."""
+        it applies (K % 128 == 0; 8: Q4_0 only); 11: its 128-row waves on
+        128-column tiles (Q4_0 only); with f32 activations 8 / 9 force the
+        bf16-piece kernel's 128- / 64-row waves."""
         self.lib.nf_hip_set_gemm_tile(tile)
 
     def get_gemm_tile(self) -> int:

@@ -185,7 +185,7 @@ def test_gemv_large_activation_staging(provider, oracle_mod, fmt, f16, shape):
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("tile", [-1, 8, 9, 10], ids=["default", "wq2", "wq2m64", "wq2m32"])
+@pytest.mark.parametrize("tile", [-1, 8, 9, 10, 11], ids=["default", "wq2", "wq2m64", "wq2m32", "wq2n128"])
 @pytest.mark.parametrize("shape", [(200, 520, 8192), (130, 300, 16384), (512, 4096, 11008)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_tiled_gemm_split_k(provider, oracle_mod, fmt, tile, shape):
@@ -193,9 +193,8 @@ def test_tiled_gemm_split_k(provider, oracle_mod, fmt, tile, shape):
     2-4 workgroups per tile and the last one adds the partial tiles.  Two
     calls in a row: the per-tile counters must be back at zero after each.
     Tiles 8 / 9 / 10 force the two-waves-per-SIMD kernel with 128 / 64 /
-    32-row waves (8: Q4_0 only; Q8_0 falls back to the one-wave kernel),
-    which the default picks only for M <= 64 and, with 128-row waves, from
-    M = 1024."""
+    32-row waves, tile 11 its 128-row waves on 128-column tiles (8 and 11:
+    Q4_0 only; Q8_0 falls back to the one-wave kernel)."""
     M, N, K = shape
     W = syn.weights(fmt, N, K, seed=N + 1)
     old = provider.get_tuning()
@@ -255,7 +254,7 @@ def test_split_k_back_to_back(provider, oracle_mod, path, f16, shape):
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 5, 7, 8, 9, 10],
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 5, 7, 8, 9, 10, 11],
                          ids=lambda t: "regdq" if t < 0 else f"lds{t}" if t < 7 else f"wq{t - 6}")
 @pytest.mark.parametrize("shape", [(129, 260, 64), (257, 514, 192), (130, 302, 320), (200, 777, 448),
                                    (129, 260, 128), (257, 514, 384), (130, 302, 640), (200, 777, 896)],
@@ -264,7 +263,7 @@ def test_gemm_kernels_edges(provider, oracle_mod, fmt, tile, shape):
     """Every f16 GEMM kernel (weights dequantized in registers: tile -1 the
     default pick, tile 7 the one-wave kernel, tiles 8 / 9 / 10 the
     two-waves-per-SIMD kernel with 128 / 64 / 32-row waves where K % 128 ==
-    0; into LDS: tiles 0..6) against the oracle on ragged
+    0, tile 11 its 128-row waves on 128-column tiles; into LDS: tiles 0..6) against the oracle on ragged
     shapes: M and N past a tile edge, N % 4 != 0 (element-wise stores), and
     1, 3, 5, 7 K steps, or 1, 3, 5, 7 step pairs per K-group (K = 128 ..
     896), i.e. fewer steps than the prefetch depth and every loop
