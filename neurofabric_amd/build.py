@@ -46,8 +46,15 @@ COMMON_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-fvisibility=hidden",
                 f"-I{REPO / 'include'}", f"-I{CSRC}"]
 # Packed-FP32 instructions are disabled for all device code (the host pass
 # of hipcc warns that it does not know the feature; that is harmless).
+# Kernel arguments are preloaded into SGPRs at wave launch (gfx950 kernarg
+# preloading, as many leading arguments as fit in the user SGPRs): a wave
+# then starts computing addresses without a scalar load from the argument
+# block (measured on MI355X: 2048x2048 Q4_0 GEMV 2.87 against 3.45 us per
+# launch).  The compiler adds a fallback prologue that loads the same
+# arguments where the firmware does not preload.
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-             "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
+             "-packed-fp32-ops", "-Wno-unused-command-line-argument",
+             "-mllvm", "-amdgpu-kernarg-preload-count=16"]
 
 
 def _run(cmd: list[str]) -> None:

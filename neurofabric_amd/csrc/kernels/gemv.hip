@@ -391,35 +391,40 @@ __device__ __forceinline__ float group_sum(float v, int log2L) {
 // group of one).  The job is uniform per workgroup, so weight and output
 // bases stay scalar.
 constexpr int kGroupMax = nfhip::kGemvGroupMax;
+static_assert(kGroupMax == 4, "gemv_pair_kernel passes begin[1..3] as scalar arguments");
 struct GemvGroup {
   const uint8_t* W[kGroupMax];
   void* C[kGroupMax];
   int N[kGroupMax];
   int begin[kGroupMax + 1];
-  int count;
 };
 
 // NS register sets of weights in rotation: the loads run NS - 1 steps ahead.
+//
+// Arguments: job 0's weights, output and rows and the job boundaries
+// begin[1..3] come first as plain scalars (W0 = grp.W[0], ...), so they are
+// among the arguments preloaded into SGPRs at wave launch: a workgroup of
+// job 0 (every workgroup of a single launch) issues its first loads without
+// waiting on a scalar load from the argument block.  Other jobs read their
+// entries of `grp` (one round trip).
 template <class QF, typename XT, int R2, int MM, int NS>
-__global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A, const GemvGroup grp, int M,
-                                                        int K, int log2L) {
-  // This workgroup's job (uniform; selects rather than an indexed load of
-  // the argument block).
-  int job = 0;
-#pragma unroll
-  for (int q = 1; q < kGroupMax; ++q) job = (q < grp.count && (int)blockIdx.x >= grp.begin[q]) ? q : job;
-  const uint8_t* __restrict__ W = grp.W[0];
-  void* Cv = grp.C[0];
-  int N = grp.N[0], wg0 = grp.begin[0], wg1 = grp.begin[1];
-#pragma unroll
-  for (int q = 1; q < kGroupMax; ++q)
-    if (job == q) {
-      W = grp.W[q];
-      Cv = grp.C[q];
-      N = grp.N[q];
-      wg0 = grp.begin[q];
-      wg1 = grp.begin[q + 1];
-    }
+__global__ __launch_bounds__(256) void gemv_pair_kernel(const XT* __restrict__ A, const uint8_t* __restrict__ W0,
+                                                        void* C0, int N0, int b1, int b2, int b3, int M, int K,
+                                                        int log2L, const GemvGroup grp) {
+  // This workgroup's job (uniform): begin[] is non-decreasing, and unused
+  // entries equal the grid size.
+  const int bx = (int)blockIdx.x;
+  const int job = (bx >= b1) + (bx >= b2) + (bx >= b3);
+  const uint8_t* __restrict__ W = W0;
+  void* Cv = C0;
+  int N = N0, wg0 = 0, wg1 = b1;
+  if (job > 0) {
+    W = grp.W[job];
+    Cv = grp.C[job];
+    N = grp.N[job];
+    wg0 = grp.begin[job];
+    wg1 = grp.begin[job + 1];
+  }
   XT* __restrict__ C = static_cast<XT*>(Cv);
   const int bid = (int)blockIdx.x - wg0, nwg = wg1 - wg0;
   constexpr bool kF32 = sizeof(XT) == 4;
@@ -775,8 +780,9 @@ hipError_t gemv_pair_launch(const PairGeom& g, const void* A, const GemvGroup& g
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPairMaxLds);
     if (attr != hipSuccess) return attr;
   }
-  gemv_pair_kernel<QF, XT, R2, MM, NS><<<dim3(g.grid), dim3(256), g.lds, s>>>(static_cast<const XT*>(A), grp,
-                                                                              (int)M, (int)K, g.log2L);
+  gemv_pair_kernel<QF, XT, R2, MM, NS><<<dim3(g.grid), dim3(256), g.lds, s>>>(
+      static_cast<const XT*>(A), grp.W[0], grp.C[0], grp.N[0], grp.begin[1], grp.begin[2], grp.begin[3], (int)M,
+      (int)K, g.log2L, grp);
   return hipGetLastError();
 }
 
@@ -850,7 +856,6 @@ hipError_t gemv_dispatch(const void* A, const void* W, void* C, uint32_t M, uint
   grp.N[0] = (int)N;
   grp.begin[0] = 0;
   for (int q = 1; q <= kGroupMax; ++q) grp.begin[q] = (int)g.grid;
-  grp.count = 1;
   return gemv_pair_group<QF, XT>(g, A, grp, M, K, s);
 }
 
@@ -887,7 +892,6 @@ hipError_t gemv_group_dispatch(const void* A, const nfhip::GemvJob* jobs, uint32
     wg = end;
   }
   for (int q = (int)n; q <= kGroupMax; ++q) grp.begin[q] = (int)wg;
-  grp.count = (int)n;
   g.grid = (unsigned)wg;
   return gemv_pair_group<QF, XT>(g, A, grp, M, K, s);
 }

@@ -199,29 +199,36 @@ struct SkinnyGroup {
   void* C[kSkGroupMax];
   int N[kSkGroupMax];
   int begin[kSkGroupMax + 1];
-  int count;
 };
+static_assert(kSkGroupMax == 4, "the small-batch kernels pass begin[1..3] as scalar arguments");
+
+// Arguments of the small-batch kernels: job 0's fields and the job
+// boundaries begin[1..3] come first as plain scalars (W0 = grp.W[0], ...),
+// so they are among the arguments preloaded into SGPRs at wave launch and a
+// workgroup of job 0 (every workgroup of a single launch) issues its first
+// loads without a scalar load from the argument block; other jobs read
+// their entries of `grp`.  begin[] is non-decreasing and its unused entries
+// equal the number of workgroups (tiles) along x.
+__device__ __forceinline__ int group_job(int b1, int b2, int b3) {
+  const int bx = (int)blockIdx.x;
+  return (bx >= b1) + (bx >= b2) + (bx >= b3);
+}
 
 template <class QF, typename XT, int MT, int CHP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 4))) void skinny_kernel(
-    const XT* __restrict__ A, const SkinnyGroup grp, int M, int K, float* __restrict__ ws_part,
-    uint32_t* __restrict__ ws_cnt) {
-  // This workgroup's job (uniform; selects rather than an indexed load of
-  // the argument block).
-  int job = 0;
-#pragma unroll
-  for (int q = 1; q < kSkGroupMax; ++q) job = (q < grp.count && (int)blockIdx.x >= grp.begin[q]) ? q : job;
-  const uint8_t* __restrict__ W = grp.W[0];
-  void* Cv = grp.C[0];
-  int N = grp.N[0], tile0 = grp.begin[0];
-#pragma unroll
-  for (int q = 1; q < kSkGroupMax; ++q)
-    if (job == q) {
-      W = grp.W[q];
-      Cv = grp.C[q];
-      N = grp.N[q];
-      tile0 = grp.begin[q];
-    }
+    const XT* __restrict__ A, const uint8_t* __restrict__ W0, int N0, int b1, int b2, int b3, int M, int K,
+    void* C0, float* __restrict__ ws_part, uint32_t* __restrict__ ws_cnt, const SkinnyGroup grp) {
+  // This workgroup's job (uniform).
+  const int job = group_job(b1, b2, b3);
+  const uint8_t* __restrict__ W = W0;
+  void* Cv = C0;
+  int N = N0, tile0 = 0;
+  if (job > 0) {
+    W = grp.W[job];
+    Cv = grp.C[job];
+    N = grp.N[job];
+    tile0 = grp.begin[job];
+  }
   XT* __restrict__ C = static_cast<XT*>(Cv);
   constexpr bool kF32 = sizeof(XT) == 4;
   constexpr bool kQ4 = SkW<QF>::kLoads == 5;
@@ -586,32 +593,31 @@ struct RingGroup {
   int begin[kSkGroupMax + 1];
   int kg[kSkGroupMax];
   int ctr[kSkGroupMax];
-  int count;
 };
 
 // Partial-tile loads (float4 per thread) the split-K fix-up keeps in flight.
 constexpr int kRingGatherF4 = 16;
 
+// Arguments as skinny_kernel's (job 0's fields first: W0 = grp.W[0], N0,
+// KG0 = grp.kg[0], C0, CTR0 = grp.ctr[0]).
 template <class QF, int MT, int T, int CHP, int S>
-__global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restrict__ A, const RingGroup grp, int M,
-                                                         int K, float* __restrict__ ws_part,
-                                                         uint32_t* __restrict__ ws_cnt) {
-  int job = 0;
-#pragma unroll
-  for (int q = 1; q < kSkGroupMax; ++q) job = (q < grp.count && (int)blockIdx.x >= grp.begin[q]) ? q : job;
-  const uint8_t* __restrict__ W = grp.W[0];
-  void* Cv = grp.C[0];
-  int N = grp.N[0], wg0 = grp.begin[0], KG = grp.kg[0], ctr0 = grp.ctr[0];
-#pragma unroll
-  for (int q = 1; q < kSkGroupMax; ++q)
-    if (job == q) {
-      W = grp.W[q];
-      Cv = grp.C[q];
-      N = grp.N[q];
-      wg0 = grp.begin[q];
-      KG = grp.kg[q];
-      ctr0 = grp.ctr[q];
-    }
+__global__ __launch_bounds__(512) void skinny_ring_kernel(const float* __restrict__ A,
+                                                         const uint8_t* __restrict__ W0, int N0, int KG0, int b1,
+                                                         int b2, int b3, int M, int K, void* C0, int CTR0,
+                                                         float* __restrict__ ws_part,
+                                                         uint32_t* __restrict__ ws_cnt, const RingGroup grp) {
+  const int job = group_job(b1, b2, b3);
+  const uint8_t* __restrict__ W = W0;
+  void* Cv = C0;
+  int N = N0, wg0 = 0, KG = KG0, ctr0 = CTR0;
+  if (job > 0) {
+    W = grp.W[job];
+    Cv = grp.C[job];
+    N = grp.N[job];
+    wg0 = grp.begin[job];
+    KG = grp.kg[job];
+    ctr0 = grp.ctr[job];
+  }
   float* __restrict__ C = static_cast<float*>(Cv);
   const int local = (int)blockIdx.x - wg0, tile = local / KG, kg = local - tile * KG;
   typedef RingGeom<QF, MT, T, CHP> G;
@@ -958,8 +964,9 @@ hipError_t ring_launch_group(const float* A, const RingGroup& grp, long wgs, uin
         hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_ring_kernel<QF, MT, T, CHP, S>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::kLds);
     if (attr != hipSuccess) return attr;
-    skinny_ring_kernel<QF, MT, T, CHP, S><<<dim3((unsigned)wgs), dim3(512), Cfg::kLds, s>>>(A, grp, (int)M, (int)K,
-                                                                                          ws.part, ws.cnt);
+    skinny_ring_kernel<QF, MT, T, CHP, S><<<dim3((unsigned)wgs), dim3(512), Cfg::kLds, s>>>(
+        A, grp.W[0], grp.N[0], grp.kg[0], grp.begin[1], grp.begin[2], grp.begin[3], (int)M, (int)K, grp.C[0],
+        grp.ctr[0], ws.part, ws.cnt, grp);
     return hipGetLastError();
   }
 }
@@ -991,7 +998,6 @@ hipError_t ring_group_t(const float* A, const nfhip::GemvJob* jobs, uint32_t n, 
   if (split && (tiles > (long)ws.cnt_len || (size_t)wgs * MT * T * 512 * 4 > ws.part_floats))
     return hipErrorNotSupported;
   for (int q = (int)n; q <= kSkGroupMax; ++q) grp.begin[q] = (int)wgs;
-  grp.count = (int)n;
   return ring_launch_group<QF, MT, T>(A, grp, wgs, M, K, ws, s);
 }
 
@@ -1079,7 +1085,8 @@ hipError_t skinny_launch_group(const void* A, const SkinnyGroup& grp, long tiles
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
   if (attr != hipSuccess) return attr;
   skinny_kernel<QF, XT, MT, CHP><<<dim3((unsigned)tiles, (unsigned)kg), dim3(64 * ks), lds, s>>>(
-      static_cast<const XT*>(A), grp, (int)M, (int)K, ws.part, ws.cnt);
+      static_cast<const XT*>(A), grp.W[0], grp.N[0], grp.begin[1], grp.begin[2], grp.begin[3], (int)M, (int)K,
+      grp.C[0], ws.part, ws.cnt, grp);
   return hipGetLastError();
 }
 
@@ -1094,7 +1101,6 @@ hipError_t skinny_launch(const void* A, const void* W, void* C, uint32_t M, uint
   grp.C[0] = C;
   grp.N[0] = (int)N;
   for (int q = 1; q <= kSkGroupMax; ++q) grp.begin[q] = (int)wgs;
-  grp.count = 1;
   return skinny_launch_group<QF, XT, MT, CHP>(A, grp, wgs, M, K, ks, kg, ws, s);
 }
 
@@ -1124,7 +1130,6 @@ hipError_t skinny_group_same_split(const void* A, const nfhip::GemvJob* jobs, ui
     tiles += wgs;
   }
   for (int q = (int)n; q <= kSkGroupMax; ++q) grp.begin[q] = (int)tiles;
-  grp.count = (int)n;
   return skinny_launch_group<QF, XT, MT, CHP>(A, grp, tiles, M, K, ks0, kg0, ws, s);
 }
 
