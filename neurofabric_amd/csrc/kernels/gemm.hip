@@ -983,24 +983,37 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_wq_kernel(const half_t* __res
 // that halve the dequantization per MFMA, measured slower: 693 against 816
 // TFLOP/s at 4096 x 4096, M = 2048.)
 
+// Q4_0: the lane's loaded window realigned in place, once per block, so
+// w[t] = code dword t (bytes 2+2h+4t.. of the window, h = the block's 2-byte
+// misalignment, selected by `sel`); the four slices then read it directly
+// (a realignment per slice would redo dwords 0..3 twice).
+__device__ __forceinline__ void realign_q4(uint32_t (&w)[WBlk<Q4_0>::kDwords], uint32_t sel) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) w[t] = __builtin_amdgcn_perm(w[t + 1], w[t], sel);
+}
+
 // Elements 8kk..8kk+7 of the lane's block as 4 dwords of fp16 (the
 // dequant_*_f16 bits): Q4_0 low nibbles of code dwords 2(kk&1), 2(kk&1)+1
-// for kk < 2, high nibbles for kk >= 2; Q8_0 code dwords 2kk, 2kk+1.
+// for kk < 2, high nibbles for kk >= 2 (w realigned by realign_q4); Q8_0
+// code dwords 2kk, 2kk+1 (w as loaded).  A low nibble n goes under exponent
+// byte 0x64 (fp16 1024 + n), a high one, masked in place (16n), under 0x54
+// (fp16 64 + 16n/16 = 64 + n: unit spacing there), so no shift is needed;
+// the packed add of -1032 or -72 leaves n - 8 exactly, and the packed
+// multiply rounds d(n - 8) once.
 template <class QF>
 __device__ __forceinline__ u32x4 dequant_slice(const uint32_t (&w)[WBlk<QF>::kDwords], uint32_t sel, half2v d2,
                                                int kk) {
   u32x4 o;
   if constexpr (std::is_same<QF, Q4_0>::value) {
-    const half2v off = {(half_t)-1032.f, (half_t)-1032.f};
+    const bool hi = (kk >> 1) != 0;
+    const half2v off = hi ? half2v{(half_t)-72.f, (half_t)-72.f} : half2v{(half_t)-1032.f, (half_t)-1032.f};
+    const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu, expo = hi ? 0x54545454u : 0x64646464u;
     const int t0 = 2 * (kk & 1);
-    const uint32_t qa = __builtin_amdgcn_perm(w[t0 + 1], w[t0], sel);
-    const uint32_t qb = __builtin_amdgcn_perm(w[t0 + 2], w[t0 + 1], sel);
-    const uint32_t xa = (kk >> 1) ? (qa >> 4) & 0x0F0F0F0Fu : qa & 0x0F0F0F0Fu;
-    const uint32_t xb = (kk >> 1) ? (qb >> 4) & 0x0F0F0F0Fu : qb & 0x0F0F0F0Fu;
-    o.x = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, xa, 0x04010400u)) + off) * d2);
-    o.y = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, xa, 0x04030402u)) + off) * d2);
-    o.z = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, xb, 0x04010400u)) + off) * d2);
-    o.w = u32_of((h2_of(__builtin_amdgcn_perm(0x64646464u, xb, 0x04030402u)) + off) * d2);
+    const uint32_t xa = w[t0] & mask, xb = w[t0 + 1] & mask;
+    o.x = u32_of((h2_of(__builtin_amdgcn_perm(expo, xa, 0x04010400u)) + off) * d2);
+    o.y = u32_of((h2_of(__builtin_amdgcn_perm(expo, xa, 0x04030402u)) + off) * d2);
+    o.z = u32_of((h2_of(__builtin_amdgcn_perm(expo, xb, 0x04010400u)) + off) * d2);
+    o.w = u32_of((h2_of(__builtin_amdgcn_perm(expo, xb, 0x04030402u)) + off) * d2);
   } else {
     const half2v off = {(half_t)-1152.f, (half_t)-1152.f};
     const uint32_t ua = __builtin_amdgcn_perm(w[2 * kk + 1], w[2 * kk], sel) ^ 0x80808080u;
@@ -1081,12 +1094,15 @@ __global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __r
     for (int i = 0; i < A_DMA; ++i) lds_dma16(asrc[i] + (size_t)ks * kBK, dst + (wv * A_DMA + i) * 8 * 64);
   };
   half2v dsc[2][TN];  // fp16 scales of the two register sets' blocks
+  // Once a register set has landed: its blocks' scales, and (Q4_0) its code
+  // dwords realigned in place.
   auto scales = [&](int set) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       uint32_t db = (wr[set][j][0] >> w_sh) & 0xFFFFu;
       db = w_valid[j] ? db : 0u;
       dsc[set][j] = h2_of(db | (db << 16));
+      if constexpr (std::is_same<QF, Q4_0>::value) realign_q4(wr[set][j], w_sel);
     }
   };
   u32x4 bw[2][TN];
