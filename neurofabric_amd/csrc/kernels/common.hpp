@@ -35,22 +35,20 @@ __device__ __forceinline__ uint32_t pack_hi16(float a, float b) {
   return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, a), 0x07060302u);
 }
 
-// Exact three-way bf16 split of 8 floats.
-__device__ __forceinline__ void split3(const float (&x)[8], bf16x8& p1, bf16x8& p2, bf16x8& p3) {
+// Two round-to-nearest bf16 pieces of 8 floats: p1 = RNE_bf16(x), p2 =
+// RNE_bf16(x - p1) (x - p1 is exact in f32),
+// so |p2| <= 2^-8 |x| and |x - p1 - p2| <= 2^-8 |x - p1| <= 2^-16 |x|.
+__device__ __forceinline__ void split2_rne(const float (&x)[8], bf16x8& p1, bf16x8& p2) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const float2s v = {x[2 * j], x[2 * j + 1]};
     const bf16x2v h1 = __builtin_convertvector(v, bf16x2v);
     const float2s r1 = v - __builtin_convertvector(h1, float2s);
     const bf16x2v h2 = __builtin_convertvector(r1, bf16x2v);
-    const float2s r2 = r1 - __builtin_convertvector(h2, float2s);
-    const bf16x2v h3 = __builtin_convertvector(r2, bf16x2v);
     p1[2 * j] = h1[0];
     p1[2 * j + 1] = h1[1];
     p2[2 * j] = h2[0];
     p2[2 * j + 1] = h2[1];
-    p3[2 * j] = h3[0];
-    p3[2 * j + 1] = h3[1];
   }
 }
 

@@ -1533,20 +1533,24 @@ hipError_t gemm_wq2_launch(const half_t* a, const uint8_t* w, half_t* c, uint32_
 // weights once per 32 rows).  Here a workgroup streams each weight once per
 // 32*TM rows, and the products are formed on v_mfma_f32_32x32x16_bf16 from
 // exact bf16 pieces:
-//   * each activation x = a1 + a2 + a3 exactly (split3: round-to-nearest
-//     bf16 pieces, |a2| <= 2^-8 |x|, |a3| <= 2^-16 |x|), split once per
-//     workgroup while its 64-column K step is staged into three bf16 planes
-//     in LDS;
+//   * each activation x = a1 + a2 + r (split2_rne: round-to-nearest bf16
+//     pieces, |a2| <= 2^-8 |x|, |r| <= 2^-16 |x|), split once per workgroup
+//     while its 64-column K step is staged into two bf16 planes in LDS;
 //   * each weight v (at most 15 significant bits for Q4_0, 18 for Q8_0) =
 //     b1 + b2 (+ b3 for Q8_0) exactly (truncated bf16 pieces, |b2| < 2^-7 |v|,
 //     |b3| < 2^-14 |v|), formed in registers from the codes and the scale one
 //     MFMA slice ahead;
-//   * every piece product a_i*b_j that can exceed 2^-22 |x v| is an MFMA
-//     term: Q4_0 a1b1, a2b1, a3b1, a1b2, a2b2 (dropped: a3b2 < 2^-23 |x v|);
-//     Q8_0 the same and a1b3 (dropped: a2b3, a3b2, a3b3 < 2^-21 |x v|).  The
+//   * the MFMA terms are a1b1, a2b1, a1b2 (+ a1b3 for Q8_0); the dropped
+//     a2b2 < 2^-15 |x v|, r v < 2^-16 |x v| and a2b3 < 2^-22 |x v|.  The
 //     products are exact and the MFMA accumulates in fp32, so each x*v
-//     enters the sum to within a few units of its fp32 rounding, as in the
-//     reference's sequential f32 loop (metal_provider.mm:1396-1431).
+//     enters the sum within 3 * 2^-16 (4.6e-5) of its value, and an output
+//     within 4.6e-5 of the sum of |x v| over K plus its fp32 accumulation
+//     error: the 1e-3 bar of the reference's f32 loop
+//     (metal_provider.mm:1396-1431) with room to spare.  (Three activation
+//     pieces and 5 / 6 terms, every piece product above 2^-22 |x v|, took
+//     4096x4096 at M = 2048 / 512 / 128 to 249 / 203 / 124 TFLOP/s against
+//     351 / 261 / 139 for Q4_0, and Q8_0 M = 2048 to 213 against 282, on
+//     MI355X.)
 // Tiling as gemm_wq_kernel: 32*TM x 32*TN per wave, NW waves along N, the
 // same K permutation (slice kk of a step pairs lane group kb with elements
 // 8kk..8kk+7 of block kb) and output layout; A through a two-stage LDS
@@ -1599,14 +1603,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_f32a_kernel(const float* __re
                                                                uint32_t* __restrict__ ws_cnt) {
   constexpr bool kQ4 = std::is_same<QF, Q4_0>::value;
   constexpr int NB = kQ4 ? 2 : 3;  // bf16 pieces of a weight
-  constexpr int NTERM = kQ4 ? 5 : 6;
+  constexpr int NA = 2;            // bf16 pieces of an activation
+  constexpr int NTERM = kQ4 ? 3 : 4;
   constexpr int BM = 32 * TM, BN = 32 * TN * NW, NT = 64 * NW;
-  constexpr int PLANE = BM * 64;    // bf16 values per piece plane per stage
-  constexpr int STAGE = 3 * PLANE;  // three activation pieces
+  constexpr int PLANE = BM * 64;     // bf16 values per piece plane per stage
+  constexpr int STAGE = NA * PLANE;  // the activation pieces
   constexpr int A_T = BM / (8 * NW);  // 8-float activation chunks per lane per step
   static_assert(BM % (8 * NW) == 0, "A rows per wave");
   constexpr int WD = WBlk<QF>::kDwords;
-  extern __shared__ __attribute__((aligned(16))) uint16_t ldsb[];  // [2][3][BM][64] bf16
+  extern __shared__ __attribute__((aligned(16))) uint16_t ldsb[];  // [2][NA][BM][64] bf16
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -1659,11 +1664,10 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_f32a_kernel(const float* __re
     uint16_t* dst = ldsb + stage * STAGE;
 #pragma unroll
     for (int i = 0; i < A_T; ++i) {
-      bf16x8 p1, p2, p3;
-      split3(ra[i], p1, p2, p3);
+      bf16x8 p1, p2;
+      split2_rne(ra[i], p1, p2);
       *reinterpret_cast<bf16x8*>(dst + adst[i]) = p1;
       *reinterpret_cast<bf16x8*>(dst + PLANE + adst[i]) = p2;
-      *reinterpret_cast<bf16x8*>(dst + 2 * PLANE + adst[i]) = p3;
     }
   };
   uint32_t wr[2][TN][WD];
@@ -1684,11 +1688,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_f32a_kernel(const float* __re
 #pragma unroll
     for (int j = 0; j < TN; ++j) f32a_weight_slice<QF, NB>(wr[set][j], w_sel, dsc[set][j], kk, bp[buf][j]);
   };
-  bf16x8 ap[2][3][TM];
+  bf16x8 ap[2][NA][TM];
   auto read_a = [&](int stage, int kk, int buf) {
     const uint16_t* As = ldsb + stage * STAGE;
 #pragma unroll
-    for (int p = 0; p < 3; ++p)
+    for (int p = 0; p < NA; ++p)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
         ap[buf][p][i] = *reinterpret_cast<const bf16x8*>(As + p * PLANE + tile_off(32 * i + r32, 4 * kb + kk));
@@ -1699,7 +1703,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_f32a_kernel(const float* __re
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = float16v{};
   // Terms (weight piece, activation piece), most significant first.
-  constexpr int kWb[6] = {0, 0, 0, 1, 1, 2}, kAb[6] = {0, 1, 2, 0, 1, 0};
+  constexpr int kWb[4] = {0, 0, 1, 2}, kAb[4] = {0, 1, 0, 0};
   auto mfma = [&](int buf) {
 #pragma unroll
     for (int t = 0; t < NTERM; ++t)
@@ -1841,7 +1845,7 @@ hipError_t gemm_f32a_launch(const float* a, const uint8_t* w, float* c, uint32_t
     const long cost = ((tiles * g + kCUs - 1) / kCUs) * ((nk + g - 1) / g);
     if (cost < best) best = cost, kg = g;
   }
-  const size_t lds = (size_t)2 * 3 * BM * 64 * sizeof(uint16_t);
+  const size_t lds = (size_t)2 * 2 * BM * 64 * sizeof(uint16_t);  // two stages of two activation planes
   if (kg == 1) {
     static const hipError_t attr =
         hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_f32a_kernel<QF, TM, TN, NW, false>),

@@ -308,15 +308,17 @@ def test_f32_tiled_gemm(provider, oracle_mod, fmt, shape):
 
 @pytest.mark.parametrize("path", ["skinny", "tiled"])
 def test_f32_large_activations(provider, oracle_mod, path):
-    """The exact three-way bf16 split keeps f32 activations far outside the
-    fp16 range (|x| ~ 1e6 and 1e-6) exact before accumulation, on both
-    bf16-piece kernels.  With such data most outputs are sums that cancel to
-    far below their terms, where any two fp32 summation orders (the oracle's
-    sequential one included) differ by more than 1e-3 of the result; so each
-    output is held to the fp32 summation bound |got - exact| <= 4 K 2^-24
-    sum_k |x_k w_k| against the float64 result, and to 1e-3 normwise against
-    the oracle.  A lost piece (fp16 overflow at 1e6, underflow at 1e-6, or a
-    dropped term) breaks the bound by orders of magnitude."""
+    """The two bf16 pieces keep f32 activations far outside the fp16 range
+    (|x| ~ 1e6 and 1e-6) within 2^-16 of their value before accumulation,
+    on both bf16-piece kernels.  With such data most outputs are sums that
+    cancel to far below their terms, where any two fp32 summation orders (the
+    oracle's sequential one included) differ by more than 1e-3 of the
+    result; so each output is held to the fp32 summation bound
+    |got - exact| <= 4 K 2^-24 sum_k |x_k w_k| against the float64 result
+    (at K = 512, 1.2e-4 of sum_k |x_k w_k|, above the tiled kernel's 4.6e-5
+    for its dropped piece products), and to 1e-3 normwise against the
+    oracle.  A lost piece (fp16 overflow at 1e6, underflow at 1e-6, or a
+    dropped leading term) breaks the bound by orders of magnitude."""
     M, N, K = 40, 128, 512
     W = syn.q4_0_weights(N, K, seed=11)
     rng = np.random.default_rng(5)
