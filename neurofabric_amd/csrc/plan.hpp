@@ -83,10 +83,10 @@ struct LayerParams {
 // leaves one: 47.9 against 46.3 us; plan.cpp), the small-batch kernel for M = 4..16 (58.6 and
 // 61.6 us at M = 16 against 67.6 and 69.2 us for the tiled GEMM), the tiled
 // GEMM from M = 32 (70.2 vs 88.8 us and 69.4 vs 88.7 us).  f32 activations
-// (configs[3] Llama-3-8B Q8_0 step): the small-batch kernel up to M = 64 (two
-// 32-row launches: 11.7 against 14.3 ms per M = 64 step; 14336x4096 69.6 vs
-// 79.5 us, 4096x14336 84.2 vs 116.3 us), the bf16-piece tiled GEMM above
-// (14336x4096 M = 128: 124.4 vs 137.8 us).
+// (configs[3] Llama-3-8B Q8_0 step): the small-batch ring kernel up to
+// M = 64, all rows in one launch (5.12 against 11.75 ms per M = 64 step and
+// 4.86 against 11.64 ms at M = 48 with the bf16-piece tiled GEMM), the tiled
+// GEMM above, where the ring kernel does not go.
 // At M = 3..4 the winner depends on the weight size: the GEMV wins on
 // matrices up to about 10 MB, where the small-batch kernel's fixed
 // per-launch cost dominates (f32 M = 4: 2048x2048 4.9 vs 8.6 us, 4096x4096
