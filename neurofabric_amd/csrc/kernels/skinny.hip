@@ -921,7 +921,15 @@ int ring_t(uint32_t N) {
 }
 
 // Workgroups per row group (kg): up to about 256 workgroups in all, at
-// least `min_chunks` chunks each, within the workspace.
+// least `min_chunks` chunks each (2 where a row's whole K is at most 16
+// chunks, else 4), within the workspace.  The short-K rows are the
+// latency-bound ones, and two chunks per workgroup halve each workgroup's
+// chain: TinyLlama decode step at M = 16 884 -> 854 us (2048-row linears at
+// K = 2048: 8 splits instead of 4, the q+k+v launch 160 workgroups).  At
+// K = 4096 two chunks measured slower (Llama-3-8B Q8_0 step at M = 16: 2.94
+// -> 3.05 ms, its k / v rows taking 16 splits and the q+k+v launch 384
+// workgroups).  The choice depends on the job alone, so a grouped launch
+// splits every job as its own launch would.
 template <class QF, int MT, int T>
 int ring_split(long tiles, uint32_t K, const nfhip::Workspace& ws) {
   typedef RingCfg<QF, MT, T> Cfg;
@@ -932,11 +940,12 @@ int ring_split(long tiles, uint32_t K, const nfhip::Workspace& ws) {
     const long v = e ? std::atol(e) : 0;
     return v > 0 ? v : 256L;
   }();
-  static const int min_chunks = [] {
+  static const int forced_min = [] {
     const char* e = std::getenv("NF_HIP_RING_MIN_CHUNKS");  // tuning override
     const int v = e ? std::atoi(e) : 0;
-    return v > 0 ? v : 4;
+    return v > 0 ? v : 0;
   }();
+  const int min_chunks = forced_min ? forced_min : (NC <= 16 ? 2 : 4);
   int kg = 1;
   while (tiles * kg * 2 <= target && NC >= min_chunks * kg * 2 && tiles <= (long)ws.cnt_len &&
          (size_t)tiles * kg * 2 * NQ * 512 * 4 <= ws.part_floats)
