@@ -840,7 +840,10 @@ def build_line(*, gbs, med_ms, args, dispatches, launches, kernels, achieved, by
     """The one JSON line bench.py prints."""
     extra = summarize_extra(extra_full)
     if full_path:
-        extra["full_tables"] = str(full_path)
+        p = Path(full_path).resolve()
+        # relative to the repository root when it lies inside it (the root
+        # is a scratch path on a GPU box)
+        extra["full_tables"] = str(p.relative_to(REPO.resolve())) if p.is_relative_to(REPO.resolve()) else str(p)
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
