@@ -73,8 +73,8 @@ struct LayerParams {
 // Switch points between the kernel families of the fused op: the VALU GEMV
 // while M <= gemv_max_m (and its activation stage fits in LDS), the
 // small-batch MFMA kernel while M <= skinny_max_m (f16 and f32 activations
-// each have their own; at most 32 f32 rows per launch), the tiled MFMA GEMM
-// above (f16: fp16 MFMA; f32: bf16-piece MFMA, K % 64 == 0, else the GEMV).
+// each have their own; the f32 ring kernel takes all 64 rows in one launch),
+// the tiled MFMA GEMM above (f16: fp16 MFMA; f32: bf16-piece MFMA, K % 64 == 0, else the GEMV).
 // Defaults from measured sweeps on MI355X (graph replay over 4 rotated weight
 // copies).  bench.py's configs[4] section (28672x8192 and 8192x28672 Q4_0,
 // f16 activations): the GEMV is fastest up to M = 2 (31.0 / 38.8 us against
@@ -111,14 +111,15 @@ struct Tuning {
   // picked by M (launch_gemm_mfma); 0..6 = one of the LDS-staged tile
   // shapes; 7 = the register-dequantizing kernel with one wave per SIMD;
   // 8 / 9 / 10 = the two-wave kernel with 128 / 64 / 32-row waves wherever
-  // it applies (K % 128 == 0; 8: Q4_0 only).
+  // it applies (K % 128 == 0; 8: Q4_0 only); 11 = its 128-row waves on
+  // 128-column tiles (Q4_0, K % 128 == 0).
   int32_t gemm_tile = -1;
 };
 
 // "256x256" -> 0, "256x128" -> 1, "128x128" -> 2, "256x128w4" -> 3,
 // "256x128w4s3" -> 4, "128x128s3" -> 5, "128x256" -> 6, "wq1" -> 7,
-// "wq2" -> 8, "wq2m64" -> 9, "wq2m32" -> 10, or the number 0..10; anything
-// else (including null) -> -1.
+// "wq2" -> 8, "wq2m64" -> 9, "wq2m32" -> 10, "wq2n128" -> 11, or the number
+// 0..11; anything else (including null) -> -1.
 int gemm_tile_from_name(const char* name);
 
 struct Plan {
