@@ -1149,10 +1149,15 @@ __global__ __launch_bounds__(128 * NW, 1) void gemm_wq2_kernel(const half_t* __r
 
   // Prologue: A of step 0 into stage 0; weights of steps 0 and 1 (past the
   // last step: its loads again, never used) into register sets 0 and 1.
-  // Only A and set 0 are waited for: set 1 (the kInFlight youngest loads) is
-  // first read after step 0's barrier, whose own wait covers it.  Measured
-  // on MI355X against waiting for all three: 4096x4096 M = 2048 875 -> 885
-  // TFLOP/s, 11008x4096 857 -> 874, 4096x4096 M = 512 461 -> 469.
+  // The barrier's wait leaves at most kInFlight (one weight set's) loads
+  // outstanding, so A, issued first, has landed for every wave.  The
+  // compiler may move set 1's loads below the barrier (the loads through the
+  // restrict-qualified W are free to cross its empty asm statements); then
+  // set 0 is the set left in flight, and the compiler waits for its
+  // registers where they are first read.  Either way set 1 is first read
+  // after step 0's barrier, whose own wait covers it.  Measured on MI355X
+  // against waiting for all three: 4096x4096 M = 2048 875 -> 885 TFLOP/s,
+  // 11008x4096 857 -> 874, 4096x4096 M = 512 461 -> 469.
   dma_a(0, 0);
   load_w(0, 0);
   load_w(nk > 1 ? 1 : 0, 1);
